@@ -1,0 +1,211 @@
+"""ctypes front-end of the CPU oracle (oracle/bn_oracle.c).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, ``__graft_entry__.smoke()`` and
+the ``cpu_baseline`` leg of bench.py, always as the checker / baseline.  The
+product (``bten`` and ``libbnhip.so``) never imports this module.
+
+All arrays are numpy float32 (int32 for lengths).  Functions take and return
+dense row-major arrays; strided views are exercised through ``view()``.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "libbn_oracle.so")
+_lib = None
+
+
+class OrView(C.Structure):
+    _fields_ = [("p", C.POINTER(C.c_float)), ("offset", C.c_int64),
+                ("h", C.c_int32), ("w", C.c_int32),
+                ("stride_h", C.c_int32), ("stride_w", C.c_int32)]
+
+
+def build(force: bool = False) -> str:
+    """Compile the oracle with its Makefile (gcc)."""
+    if force or not os.path.exists(_LIB_PATH):
+        subprocess.run(["make", "-s", "-B" if force else "all"], cwd=_HERE,
+                       check=True)
+    return _LIB_PATH
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        L = C.CDLL(_LIB_PATH)
+        V = OrView
+        fp, ip = C.POINTER(C.c_float), C.POINTER(C.c_int32)
+        i64 = C.c_int64
+        L.or_rmsnorm.argtypes = [V, V, V, C.c_float]
+        L.or_rmsnorm_backward.argtypes = [V, V, V, V, V, C.c_float]
+        L.or_rope_freq.argtypes = [C.c_int, C.c_int, C.c_float]
+        L.or_rope_freq.restype = C.c_float
+        L.or_rope.argtypes = [V, V, C.c_int, C.c_int, C.c_float]
+        L.or_rope_backward.argtypes = [V, V, C.c_int, C.c_int, C.c_float]
+        L.or_rmsnorm_rope.argtypes = [V, V, V, C.c_float, C.c_int, C.c_int, C.c_float]
+        L.or_softmax.argtypes = [V, V, C.c_int, C.c_int]
+        L.or_softmax_backward.argtypes = [V, V, V]
+        L.or_matmul.argtypes = [V, V, V]
+        L.or_scale.argtypes = [V, C.c_float, V]
+        L.or_repeat_kv.argtypes = [V, V, C.c_int, C.c_int]
+        L.or_gqa_prefill.argtypes = [fp, fp, fp, fp] + [C.c_int] * 6 + [i64] * 6 + \
+            [C.c_float, C.c_int, C.c_int, fp]
+        L.or_gqa_decode.argtypes = [fp, fp, fp, ip, fp] + [C.c_int] * 5 + [C.c_float, fp]
+        L.or_gqa_layer_scratch.argtypes = [C.c_int] * 4
+        L.or_gqa_layer_scratch.restype = i64
+        L.or_gqa_layer.argtypes = [fp, C.c_int, C.c_int, C.c_int, C.c_int, fp, fp, fp, fp,
+                                   C.c_float, C.c_int, C.c_int, fp, fp]
+        _lib = L
+    return _lib
+
+
+def _f32(a):
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    return a
+
+
+def _ptr(a):
+    return a.ctypes.data_as(C.POINTER(C.c_float))
+
+
+def view(a: np.ndarray, offset=0, h=None, w=None, stride_h=None, stride_w=1) -> OrView:
+    """Strided view over a float32 buffer (kept alive by the caller)."""
+    assert a.dtype == np.float32 and a.flags.c_contiguous
+    if a.ndim == 1:
+        a2w = a.shape[0]
+    else:
+        a2w = a.shape[-1]
+    h = a.shape[0] if h is None else h
+    w = a2w if w is None else w
+    stride_h = a2w if stride_h is None else stride_h
+    return OrView(_ptr(a), offset, h, w, stride_h, stride_w)
+
+
+def _v(a):
+    return view(a)
+
+
+def rmsnorm(x, weight, eps=1e-6):
+    x, weight = _f32(x), _f32(weight).reshape(1, -1)
+    y = np.empty_like(x)
+    lib().or_rmsnorm(_v(x), _v(weight), _v(y), eps)
+    return y
+
+
+def rmsnorm_backward(x, weight, dy, eps=1e-6):
+    x, weight, dy = _f32(x), _f32(weight).reshape(1, -1), _f32(dy)
+    dx = np.empty_like(x)
+    dw = np.empty_like(weight)
+    lib().or_rmsnorm_backward(_v(x), _v(weight), _v(dy), _v(dx), _v(dw), eps)
+    return dx, dw
+
+
+def rope_freq(pair, head_dim, theta):
+    return lib().or_rope_freq(pair, head_dim, theta)
+
+
+def rope(x, position_offset=0, head_dim=64, theta=10000.0):
+    x = _f32(x)
+    y = np.empty_like(x)
+    lib().or_rope(_v(x), _v(y), position_offset, head_dim, theta)
+    return y
+
+
+def rope_backward(dy, position_offset=0, head_dim=64, theta=10000.0):
+    dy = _f32(dy)
+    dx = np.empty_like(dy)
+    lib().or_rope_backward(_v(dy), _v(dx), position_offset, head_dim, theta)
+    return dx
+
+
+def rmsnorm_rope(x, weight, eps=1e-6, position_offset=0, head_dim=64, theta=10000.0):
+    x, weight = _f32(x), _f32(weight).reshape(1, -1)
+    y = np.empty_like(x)
+    lib().or_rmsnorm_rope(_v(x), _v(weight), _v(y), eps, position_offset, head_dim, theta)
+    return y
+
+
+def softmax(x, causal=False, seq_offset=0):
+    x = _f32(x)
+    y = np.empty_like(x)
+    lib().or_softmax(_v(x), _v(y), int(causal), seq_offset)
+    return y
+
+
+def softmax_backward(y, dy):
+    y, dy = _f32(y), _f32(dy)
+    dx = np.empty_like(y)
+    lib().or_softmax_backward(_v(y), _v(dy), _v(dx))
+    return dx
+
+
+def matmul(a, b):
+    a, b = _f32(a), _f32(b)
+    c = np.empty((a.shape[0], b.shape[1]), np.float32)
+    lib().or_matmul(_v(a), _v(b), _v(c))
+    return c
+
+
+def matmul_views(a: OrView, b: OrView, c: OrView):
+    lib().or_matmul(a, b, c)
+
+
+def scale(x, c):
+    x = _f32(x)
+    y = np.empty_like(x)
+    lib().or_scale(_v(x), c, _v(y))
+    return y
+
+
+def repeat_kv(kv, head_dim, n_rep):
+    kv = _f32(kv)
+    out = np.empty((kv.shape[0], kv.shape[1] * n_rep), np.float32)
+    lib().or_repeat_kv(_v(kv), _v(out), head_dim, n_rep)
+    return out
+
+
+def gqa_prefill(q, k, v, scale, causal=True, seq_offset=0):
+    """q [B,Sq,H,D], k/v [B,Skv,Hkv,D] float32 -> o [B,Sq,H,D]."""
+    q, k, v = _f32(q), _f32(k), _f32(v)
+    B, Sq, H, D = q.shape
+    _, Skv, Hkv, _ = k.shape
+    o = np.empty_like(q)
+    scratch = np.empty(2 * Sq * Skv + 1, np.float32)
+    lib().or_gqa_prefill(_ptr(q), _ptr(k), _ptr(v), _ptr(o), B, Sq, Skv, H, Hkv, D,
+                         Sq * H * D, H * D, Skv * Hkv * D, Hkv * D, Sq * H * D, H * D,
+                         scale, int(causal), seq_offset, _ptr(scratch))
+    return o
+
+
+def gqa_decode(q, k_cache, v_cache, seq_lens, scale):
+    """q [B,H,D], caches [B,Lmax,Hkv,D], seq_lens [B] -> o [B,H,D]."""
+    q, k_cache, v_cache = _f32(q), _f32(k_cache), _f32(v_cache)
+    lens = np.ascontiguousarray(seq_lens, dtype=np.int32)
+    B, H, D = q.shape
+    _, Lmax, Hkv, _ = k_cache.shape
+    o = np.empty_like(q)
+    scratch = np.empty(2 * Lmax + 1, np.float32)
+    lib().or_gqa_decode(_ptr(q), _ptr(k_cache), _ptr(v_cache),
+                        lens.ctypes.data_as(C.POINTER(C.c_int32)), _ptr(o), B, Lmax, H,
+                        Hkv, D, scale, _ptr(scratch))
+    return o
+
+
+def gqa_layer(x, wq, wk, wv, wo, n_heads, n_kv_heads, theta=10000.0,
+              position_offset=0, per_head=False):
+    x = _f32(x)
+    S, hidden = x.shape
+    out = np.empty_like(x)
+    n = lib().or_gqa_layer_scratch(S, hidden, n_heads, n_kv_heads)
+    scratch = np.empty(n, np.float32)
+    lib().or_gqa_layer(_ptr(x), S, hidden, n_heads, n_kv_heads, _ptr(_f32(wq)),
+                       _ptr(_f32(wk)), _ptr(_f32(wv)), _ptr(_f32(wo)), theta,
+                       position_offset, int(per_head), _ptr(out), _ptr(scratch))
+    return out
