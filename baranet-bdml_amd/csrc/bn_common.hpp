@@ -1,0 +1,135 @@
+// bn_common.hpp -- internal helpers shared by the libbnhip translation units:
+// error reporting behind the C ABI, host-side view validation, device-side
+// strided views and bf16 conversion.  Not part of the public interface.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdint>
+#include <cstring>
+#include <initializer_list>
+#include <string>
+#include <type_traits>
+
+#include "bn_hip.h"
+
+namespace bn {
+
+// ----------------------------------------------------------------- errors
+void set_error(const std::string &msg);
+inline int fail(int status, const std::string &msg) {
+  set_error(msg);
+  return status;
+}
+int hip_fail(hipError_t err, const char *file, int line);
+
+// Returns from the enclosing C-ABI function with BN_ERR_HIP on error.
+#define BN_HIP_TRY(expr)                                              \
+  do {                                                                \
+    hipError_t bn_e_ = (expr);                                        \
+    if (bn_e_ != hipSuccess) return ::bn::hip_fail(bn_e_, __FILE__, __LINE__); \
+  } while (0)
+
+// After a kernel launch: report launch-configuration errors.
+#define BN_LAUNCH_CHECK() BN_HIP_TRY(hipGetLastError())
+
+inline hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s); }
+
+// Makes sure the library's device is current on the calling thread.
+int ensure_device();
+
+// ------------------------------------------------------------ validation
+inline size_t dtype_size(int dt) { return dt == BN_BF16 ? 2 : 4; }
+
+// Checks a view's fields; `op` prefixes the message ("RMSNorm", ...).
+// dtype_mask: bit (1 << dtype) set for each accepted dtype.
+int check_view(const bn_view *v, const char *op, const char *name, unsigned dtype_mask,
+               bool need_device = false);
+
+// The reference validates shapes first and the device last (op_rmsnorm.cuh:
+// 142-150); GPU-only ops end their validation with this check.
+inline int require_device(const char *op, std::initializer_list<const bn_view *> vs) {
+  for (const bn_view *v : vs)
+    if (!v->on_device)
+      return fail(BN_ERR_NOT_DEVICE, std::string(op) + ": only GPU implementation available");
+  return BN_OK;
+}
+
+inline bool same_shape(const bn_view *a, const bn_view *b) {
+  return a->h == b->h && a->w == b->w;
+}
+
+// True when the view is row-major contiguous within rows (stride_w == 1) and
+// every row starts on a `align`-byte boundary.
+inline bool rows_aligned(const bn_view *v, int align) {
+  size_t es = dtype_size(v->dtype);
+  uintptr_t base = reinterpret_cast<uintptr_t>(v->data) + (uintptr_t)(v->offset * (int64_t)es);
+  return v->stride_w == 1 && (base % align) == 0 &&
+         ((size_t)((int64_t)v->stride_h * (int64_t)es) % align) == 0;
+}
+
+// ----------------------------------------------------- device-side views
+template <typename T>
+struct DView {
+  T *p;  // already offset to element (0, 0)
+  int h, w;
+  int64_t sh, sw;
+  __device__ __forceinline__ T &at(int r, int c) const { return p[r * sh + c * sw]; }
+};
+
+template <typename T>
+inline DView<T> dview(const bn_view *v) {
+  DView<T> d;
+  d.p = reinterpret_cast<T *>(v->data) + v->offset;
+  d.h = v->h;
+  d.w = v->w;
+  d.sh = v->stride_h;
+  d.sw = v->stride_w;
+  return d;
+}
+
+// ------------------------------------------------------------------ bf16
+// bf16 values are stored as raw 16-bit patterns; conversions are exact
+// (bf16 -> f32) and round-to-nearest-even (f32 -> bf16).
+typedef uint16_t bf16_t;
+
+__device__ __forceinline__ float bf16_to_f32(bf16_t b) {
+  return __uint_as_float(((uint32_t)b) << 16);
+}
+__device__ __forceinline__ bf16_t f32_to_bf16(float f) {
+  __bf16 h = (__bf16)f;  // v_cvt_pk_bf16_f32 on gfx950: RNE, NaN-preserving
+  return __builtin_bit_cast(bf16_t, h);
+}
+
+template <typename T> struct Elem;
+template <> struct Elem<float> {
+  __device__ static __forceinline__ float load(const float *p) { return *p; }
+  __device__ static __forceinline__ void store(float *p, float v) { *p = v; }
+};
+template <> struct Elem<bf16_t> {
+  __device__ static __forceinline__ float load(const bf16_t *p) { return bf16_to_f32(*p); }
+  __device__ static __forceinline__ void store(bf16_t *p, float v) { *p = f32_to_bf16(v); }
+};
+
+// --------------------------------------------------------- wave reductions
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
+  return v;
+}
+
+// RoPE frequencies formed on the host as the reference forms them
+// (op_rope.cuh:82): e = (float)(2p)/head_dim, freq = (float)(1.0/(double)theta^e).
+constexpr int kMaxRopePairs = 256;
+struct RopeFreqs {
+  float f[kMaxRopePairs];
+};
+int make_rope_freqs(const char *op, int head_dim, float theta, RopeFreqs *out);
+
+}  // namespace bn

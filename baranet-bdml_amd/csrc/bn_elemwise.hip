@@ -1,0 +1,517 @@
+// bn_elemwise.hip -- the rest of the op surface the attention layers call:
+// row softmax (causal / offset), fp32 matmul on strided views, the device
+// repeat_kv mapping, and the elementwise / reduction helpers.
+//
+// Reference kernels replaced:
+//   op_softmax_kernel / op_softmax_causal_kernel / op_softmax_backward_kernel
+//     (src/ops/op_softmax.cuh:8-246)
+//   op_mm_kernel / op_mm_tiled_kernel (src/ops/op_mm.cuh:23-57,
+//     src/ops/op_mm_optimized.cuh:13-87)
+//   repeat_kv host loop (src/llama/llama_layers.hpp:131-175)
+//   functor kernels of src/ops/op_elemwise.cuh:169-283, op_silu.cuh:33-48,
+//     op_reduction.cuh:36-109
+#include <cfloat>
+
+#include "bn_common.hpp"
+
+namespace bn {
+namespace {
+
+// ------------------------------------------------------------- softmax
+// One 256-thread workgroup per row with the reference's reduction shape:
+// thread t owns columns t, t+256, ... and partials meet in an LDS tree
+// (op_softmax.cuh:96-143), so the fp32 sums associate as the reference's.
+template <typename T>
+__global__ __launch_bounds__(256) void softmax_kernel(DView<const T> x, DView<T> y, int causal,
+                                                      int seq_offset) {
+  __shared__ float red[256];
+  const int row = blockIdx.x, tid = threadIdx.x;
+  const long q = causal ? (long)row + seq_offset : (long)x.w;  // :89
+  float m = -INFINITY;
+  for (int i = tid; i < x.w; i += 256)
+    if (i <= q) {
+      float v = Elem<T>::load(&x.at(row, i));
+      if (v > m) m = v;
+    }
+  red[tid] = m;
+  __syncthreads();
+  for (int s = 128; s > 0; s >>= 1) {
+    if (tid < s && red[tid + s] > red[tid]) red[tid] = red[tid + s];
+    __syncthreads();
+  }
+  const float mx = red[0];
+  __syncthreads();
+  float sum = 0.f;
+  for (int i = tid; i < x.w; i += 256) {
+    if (i <= q) {
+      float e = expf(Elem<T>::load(&x.at(row, i)) - mx);
+      Elem<T>::store(&y.at(row, i), e);
+      sum += e;
+    } else {
+      Elem<T>::store(&y.at(row, i), 0.f);  // :129
+    }
+  }
+  red[tid] = sum;
+  __syncthreads();
+  for (int s = 128; s > 0; s >>= 1) {
+    if (tid < s) red[tid] += red[tid + s];
+    __syncthreads();
+  }
+  const float total = red[0];
+  for (int i = tid; i < x.w; i += 256)
+    if (i <= q) Elem<T>::store(&y.at(row, i), Elem<T>::load(&y.at(row, i)) / total);
+}
+
+__global__ __launch_bounds__(256) void softmax_backward_kernel(DView<const float> y,
+                                                               DView<const float> dy,
+                                                               DView<float> dx) {
+  __shared__ float red[256];
+  const int row = blockIdx.x, tid = threadIdx.x;
+  float s = 0.f;
+  for (int i = tid; i < y.w; i += 256) s += y.at(row, i) * dy.at(row, i);
+  red[tid] = s;
+  __syncthreads();
+  for (int k = 128; k > 0; k >>= 1) {
+    if (tid < k) red[tid] += red[tid + k];
+    __syncthreads();
+  }
+  const float tot = red[0];
+  for (int i = tid; i < y.w; i += 256) dx.at(row, i) = y.at(row, i) * (dy.at(row, i) - tot);
+}
+
+// -------------------------------------------------------------- matmul
+// fp32 c = a @ b on arbitrary strided views.  64x64 output tile per
+// 256-thread workgroup, 4x4 outputs per thread, k staged through LDS in
+// steps of 16.  Each output keeps one fp32 accumulator with k ascending, the
+// association of op_mm_tiled_kernel (op_mm_optimized.cuh:35-62).
+constexpr int MT = 64, KT = 16;
+__global__ __launch_bounds__(256) void matmul_kernel(DView<const float> a, DView<const float> b,
+                                                     DView<float> c) {
+  __shared__ float As[KT][MT + 4];
+  __shared__ float Bs[KT][MT + 4];
+  const int tid = threadIdx.x;
+  const int tr = tid / 16, tc = tid % 16;
+  const int row0 = blockIdx.y * MT, col0 = blockIdx.x * MT;
+  float acc[4][4] = {};
+  for (int k0 = 0; k0 < a.w; k0 += KT) {
+    for (int e = tid; e < MT * KT; e += 256) {
+      int r = e / KT, k = e % KT;  // A tile: 64 rows x 16 k
+      int gr = row0 + r, gk = k0 + k;
+      As[k][r] = (gr < a.h && gk < a.w) ? a.at(gr, gk) : 0.f;
+      int kk = e / MT, cc = e % MT;  // B tile: 16 k x 64 cols
+      int bk = k0 + kk, bc = col0 + cc;
+      Bs[kk][cc] = (bk < b.h && bc < b.w) ? b.at(bk, bc) : 0.f;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < KT; ++k) {
+      float av[4], bv[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) av[i] = As[k][tr + 16 * i];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) bv[j] = Bs[k][tc + 16 * j];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] += av[i] * bv[j];
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      int r = row0 + tr + 16 * i, cidx = col0 + tc + 16 * j;
+      if (r < c.h && cidx < c.w) c.at(r, cidx) = acc[i][j];
+    }
+}
+
+// ---------------------------------------------------------- elementwise
+template <typename T>
+__global__ void repeat_kv_kernel(DView<const T> kv, DView<T> out, int head_dim, int n_rep) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (int64_t)out.h * out.w) return;
+  const int r = (int)(idx / out.w), c = (int)(idx % out.w);
+  const int dst_head = c / head_dim, d = c % head_dim;
+  // destination head kv_h*n_rep + rep reads source head kv_h (llama_layers.hpp:159-163)
+  out.at(r, c) = kv.at(r, (dst_head / n_rep) * head_dim + d);
+}
+
+__device__ __forceinline__ float b_at(const DView<const float> &b, int i, int j) {
+  if (b.h == 1) return b.at(0, j);  // op_elemwise.cuh:232-238
+  if (b.w == 1) return b.at(i, 0);
+  return b.at(i, j);
+}
+
+__global__ void binary_kernel(int op, DView<const float> a, DView<const float> b, DView<float> y,
+                              DView<uint32_t> yu) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (int64_t)a.h * a.w) return;
+  const int i = (int)(idx / a.w), j = (int)(idx % a.w);
+  const float x = a.at(i, j), z = b_at(b, i, j);
+  switch (op) {
+    case BN_ADD: y.at(i, j) = x + z; break;
+    case BN_SUB: y.at(i, j) = x - z; break;
+    case BN_MUL: y.at(i, j) = x * z; break;
+    default: yu.at(i, j) = (x == z) ? 1u : 0u; break;
+  }
+}
+
+__global__ void binary_u32_kernel(int op, DView<const uint32_t> a, DView<const uint32_t> b,
+                                  DView<uint32_t> y) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (int64_t)a.h * a.w) return;
+  const int i = (int)(idx / a.w), j = (int)(idx % a.w);
+  const uint32_t x = a.at(i, j);
+  const uint32_t z = b.h == 1 ? b.at(0, j) : (b.w == 1 ? b.at(i, 0) : b.at(i, j));
+  switch (op) {
+    case BN_ADD: y.at(i, j) = x + z; break;
+    case BN_SUB: y.at(i, j) = x - z; break;
+    case BN_MUL: y.at(i, j) = x * z; break;
+    default: y.at(i, j) = (x == z) ? 1u : 0u; break;
+  }
+}
+
+__global__ void unary_kernel(int op, DView<const float> x, float c, DView<float> y) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (int64_t)x.h * x.w) return;
+  const int i = (int)(idx / x.w), j = (int)(idx % x.w);
+  const float v = x.at(i, j);
+  float r;
+  switch (op) {
+    case BN_RELU: r = v > 0.f ? v : 0.f; break;               // ReluFunc
+    case BN_SILU: r = v / (1.0f + expf(-v)); break;           // op_silu.cuh SiLUFunc
+    case BN_ADD_SCALAR: r = v + c; break;                     // AddConstFunc
+    default: r = c * v; break;                                // MultiplyConstFunc
+  }
+  y.at(i, j) = r;
+}
+
+__global__ void unary_backward_kernel(int op, DView<const float> x, DView<const float> dy,
+                                      DView<float> dx) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (int64_t)x.h * x.w) return;
+  const int i = (int)(idx / x.w), j = (int)(idx % x.w);
+  const float v = x.at(i, j), g = dy.at(i, j);
+  if (op == BN_RELU_BACK) {
+    dx.at(i, j) = v > 0.f ? g : 0.f;
+  } else {
+    float sg = 1.0f / (1.0f + expf(-v));
+    dx.at(i, j) = g * (sg + v * (sg * (1.0f - sg)));
+  }
+}
+
+template <typename T>
+__global__ void fill_kernel(DView<T> y, T v) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (int64_t)y.h * y.w) return;
+  y.at((int)(idx / y.w), (int)(idx % y.w)) = v;
+}
+
+template <typename Tin, typename Tout>
+__global__ void copy_kernel(DView<const Tin> x, DView<Tout> y) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (int64_t)x.h * x.w) return;
+  const int i = (int)(idx / x.w), j = (int)(idx % x.w);
+  if constexpr (std::is_same<Tin, Tout>::value)
+    y.at(i, j) = x.at(i, j);
+  else
+    Elem<Tout>::store(&y.at(i, j), Elem<Tin>::load(&x.at(i, j)));
+}
+
+// op_reduction_kernel_colwise / _rowwise: sequential accumulation from
+// element 0 (op_reduction.cuh:36-92); argmax keeps the first maximum.
+template <typename T>
+__global__ void sum_kernel(DView<const T> x, DView<T> y, int axis) {
+  const int idx = blockIdx.x * 256 + threadIdx.x;
+  if (axis == 0) {
+    if (idx >= x.w) return;
+    T acc = x.at(0, idx);
+    for (int r = 1; r < x.h; ++r) acc = x.at(r, idx) + acc;
+    y.at(0, idx) = acc;
+  } else {
+    if (idx >= x.h) return;
+    T acc = x.at(idx, 0);
+    for (int c = 1; c < x.w; ++c) acc = x.at(idx, c) + acc;
+    y.at(idx, 0) = acc;
+  }
+}
+
+template <typename T>
+__global__ void argmax_kernel(DView<const T> x, DView<uint32_t> y) {
+  const int r = blockIdx.x * 256 + threadIdx.x;
+  if (r >= x.h) return;
+  T best = x.at(r, 0);
+  uint32_t bi = 0;
+  for (int c = 1; c < x.w; ++c) {
+    T v = x.at(r, c);
+    if (v > best) {
+      best = v;
+      bi = (uint32_t)c;
+    }
+  }
+  y.at(r, 0) = bi;
+}
+
+inline dim3 grid1d(int64_t n) { return dim3((unsigned)((n + 255) / 256)); }
+
+}  // namespace
+}  // namespace bn
+
+using namespace bn;
+
+extern "C" {
+
+int bn_softmax(const bn_view *x, const bn_view *y, int causal, int seq_offset, void *stream) {
+  const unsigned mask = (1u << BN_F32) | (1u << BN_BF16);
+  int st;
+  if ((st = check_view(x, "Softmax", "input", mask))) return st;
+  if ((st = check_view(y, "Softmax", "output", mask))) return st;
+  if (!same_shape(x, y)) return fail(BN_ERR_SHAPE, "Softmax: input/output shape mismatch");
+  if (x->dtype != y->dtype) return fail(BN_ERR_UNSUPPORTED, "Softmax: input and output dtypes differ");
+  if ((st = require_device("Softmax", {x, y}))) return st;
+  if ((st = ensure_device())) return st;
+  if (x->h == 0) return BN_OK;
+  hipStream_t s = as_stream(stream);
+  if (x->dtype == BN_F32)
+    hipLaunchKernelGGL(softmax_kernel<float>, dim3(x->h), dim3(256), 0, s, dview<const float>(x),
+                       dview<float>(y), causal ? 1 : 0, seq_offset);
+  else
+    hipLaunchKernelGGL(softmax_kernel<bf16_t>, dim3(x->h), dim3(256), 0, s,
+                       dview<const bf16_t>(x), dview<bf16_t>(y), causal ? 1 : 0, seq_offset);
+  BN_LAUNCH_CHECK();
+  return BN_OK;
+}
+
+int bn_softmax_backward(const bn_view *y, const bn_view *dy, const bn_view *dx, void *stream) {
+  const unsigned mask = 1u << BN_F32;
+  int st;
+  if ((st = check_view(y, "Softmax backward", "output", mask))) return st;
+  if ((st = check_view(dy, "Softmax backward", "grad_output", mask))) return st;
+  if ((st = check_view(dx, "Softmax backward", "grad_input", mask))) return st;
+  if (!same_shape(y, dy) || !same_shape(y, dx))
+    return fail(BN_ERR_SHAPE, "Softmax backward: shape mismatch");
+  if ((st = require_device("Softmax backward", {y, dy, dx}))) return st;
+  if ((st = ensure_device())) return st;
+  if (y->h == 0) return BN_OK;
+  hipLaunchKernelGGL(softmax_backward_kernel, dim3(y->h), dim3(256), 0, as_stream(stream),
+                     dview<const float>(y), dview<const float>(dy), dview<float>(dx));
+  BN_LAUNCH_CHECK();
+  return BN_OK;
+}
+
+int bn_matmul(const bn_view *a, const bn_view *b, const bn_view *c, void *stream) {
+  const unsigned mask = 1u << BN_F32;
+  int st;
+  if ((st = check_view(a, "Matrix multiply", "a", mask))) return st;
+  if ((st = check_view(b, "Matrix multiply", "b", mask))) return st;
+  if ((st = check_view(c, "Matrix multiply", "out", mask))) return st;
+  if (a->h != c->h || b->w != c->w || a->w != b->h)  // op_mm.cuh:13-15
+    return fail(BN_ERR_SHAPE, "a,b,out tensor shape mismatch a:(" + std::to_string(a->h) + ", " +
+                                  std::to_string(a->w) + "), b:(" + std::to_string(b->h) + ", " +
+                                  std::to_string(b->w) + "), out:(" + std::to_string(c->h) +
+                                  ", " + std::to_string(c->w) + ")");
+  if ((st = require_device("Matrix multiply", {a, b, c}))) return st;
+  if ((st = ensure_device())) return st;
+  if (c->h == 0 || c->w == 0) return BN_OK;
+  dim3 grid((c->w + MT - 1) / MT, (c->h + MT - 1) / MT);
+  hipLaunchKernelGGL(matmul_kernel, grid, dim3(256), 0, as_stream(stream), dview<const float>(a),
+                     dview<const float>(b), dview<float>(c));
+  BN_LAUNCH_CHECK();
+  return BN_OK;
+}
+
+int bn_repeat_kv(const bn_view *kv, const bn_view *out, int head_dim, int n_rep, void *stream) {
+  const unsigned mask = (1u << BN_F32) | (1u << BN_BF16);
+  int st;
+  if ((st = check_view(kv, "repeat_kv", "kv", mask))) return st;
+  if ((st = check_view(out, "repeat_kv", "out", mask))) return st;
+  if (head_dim <= 0 || n_rep <= 0 || kv->w % head_dim != 0)
+    return fail(BN_ERR_SHAPE, "repeat_kv: kv width must be a multiple of head_dim");
+  if (out->h != kv->h || (int64_t)out->w != (int64_t)kv->w * n_rep)
+    return fail(BN_ERR_SHAPE, "repeat_kv: out must be [rows, kv_width * n_rep]");
+  if (kv->dtype != out->dtype) return fail(BN_ERR_UNSUPPORTED, "repeat_kv: dtypes differ");
+  if ((st = require_device("repeat_kv", {kv, out}))) return st;
+  if ((st = ensure_device())) return st;
+  const int64_t n = (int64_t)out->h * out->w;
+  if (n == 0) return BN_OK;
+  if (kv->dtype == BN_F32)
+    hipLaunchKernelGGL(repeat_kv_kernel<float>, grid1d(n), dim3(256), 0, as_stream(stream),
+                       dview<const float>(kv), dview<float>(out), head_dim, n_rep);
+  else
+    hipLaunchKernelGGL(repeat_kv_kernel<bf16_t>, grid1d(n), dim3(256), 0, as_stream(stream),
+                       dview<const bf16_t>(kv), dview<bf16_t>(out), head_dim, n_rep);
+  BN_LAUNCH_CHECK();
+  return BN_OK;
+}
+
+int bn_binary(int op, const bn_view *a, const bn_view *b, const bn_view *y, void *stream) {
+  if (op < BN_ADD || op > BN_EQ) return fail(BN_ERR_INVALID_ARG, "bn_binary: unknown op");
+  const unsigned mask = (1u << BN_F32) | (1u << BN_U32);
+  int st;
+  if ((st = check_view(a, "elementwise", "a", mask))) return st;
+  if ((st = check_view(b, "elementwise", "b", mask))) return st;
+  if ((st = check_view(y, "elementwise", "out", mask))) return st;
+  if (!same_shape(a, y)) return fail(BN_ERR_SHAPE, "out, a tensor shape mismatch");
+  bool ok = (a->h == b->h && a->w == b->w) || (a->h == b->h && b->w == 1) ||
+            (a->w == b->w && b->h == 1);  // ensure_bcast_shape_device, op_elemwise.cuh:294-300
+  if (!ok) return fail(BN_ERR_SHAPE, "a,b shape mismatch");
+  if (a->dtype != b->dtype) return fail(BN_ERR_UNSUPPORTED, "elementwise: a and b dtypes differ");
+  const int want_out = (op == BN_EQ) ? BN_U32 : a->dtype;
+  if (y->dtype != want_out) return fail(BN_ERR_UNSUPPORTED, "elementwise: wrong output dtype");
+  if ((st = require_device("elementwise", {a, b, y}))) return st;
+  if ((st = ensure_device())) return st;
+  const int64_t n = (int64_t)a->h * a->w;
+  if (n == 0) return BN_OK;
+  hipStream_t s = as_stream(stream);
+  if (a->dtype == BN_F32) {
+    DView<float> yf = dview<float>(y);
+    DView<uint32_t> yu = dview<uint32_t>(y);
+    hipLaunchKernelGGL(binary_kernel, grid1d(n), dim3(256), 0, s, op, dview<const float>(a),
+                       dview<const float>(b), yf, yu);
+  } else {
+    hipLaunchKernelGGL(binary_u32_kernel, grid1d(n), dim3(256), 0, s, op,
+                       dview<const uint32_t>(a), dview<const uint32_t>(b), dview<uint32_t>(y));
+  }
+  BN_LAUNCH_CHECK();
+  return BN_OK;
+}
+
+int bn_unary(int op, const bn_view *x, float scalar, const bn_view *y, void *stream) {
+  if (op < BN_RELU || op > BN_MUL_SCALAR) return fail(BN_ERR_INVALID_ARG, "bn_unary: unknown op");
+  const unsigned mask = 1u << BN_F32;
+  int st;
+  if ((st = check_view(x, "elementwise", "input", mask))) return st;
+  if ((st = check_view(y, "elementwise", "output", mask))) return st;
+  if (!same_shape(x, y)) return fail(BN_ERR_SHAPE, "out, a tensor shape mismatch");
+  if ((st = require_device("elementwise", {x, y}))) return st;
+  if ((st = ensure_device())) return st;
+  const int64_t n = (int64_t)x->h * x->w;
+  if (n == 0) return BN_OK;
+  hipLaunchKernelGGL(unary_kernel, grid1d(n), dim3(256), 0, as_stream(stream), op,
+                     dview<const float>(x), scalar, dview<float>(y));
+  BN_LAUNCH_CHECK();
+  return BN_OK;
+}
+
+int bn_unary_backward(int op, const bn_view *x, const bn_view *dy, const bn_view *dx,
+                      void *stream) {
+  if (op != BN_RELU_BACK && op != BN_SILU_BACK)
+    return fail(BN_ERR_INVALID_ARG, "bn_unary_backward: unknown op");
+  const unsigned mask = 1u << BN_F32;
+  int st;
+  if ((st = check_view(x, "elementwise backward", "input", mask))) return st;
+  if ((st = check_view(dy, "elementwise backward", "grad_output", mask))) return st;
+  if ((st = check_view(dx, "elementwise backward", "grad_input", mask))) return st;
+  if (!same_shape(x, dy) || !same_shape(x, dx)) return fail(BN_ERR_SHAPE, "elementwise backward: shape mismatch");
+  if ((st = require_device("elementwise backward", {x, dy, dx}))) return st;
+  if ((st = ensure_device())) return st;
+  const int64_t n = (int64_t)x->h * x->w;
+  if (n == 0) return BN_OK;
+  hipLaunchKernelGGL(unary_backward_kernel, grid1d(n), dim3(256), 0, as_stream(stream), op,
+                     dview<const float>(x), dview<const float>(dy), dview<float>(dx));
+  BN_LAUNCH_CHECK();
+  return BN_OK;
+}
+
+int bn_fill(const bn_view *y, double value, void *stream) {
+  const unsigned mask = (1u << BN_F32) | (1u << BN_BF16) | (1u << BN_U32);
+  int st;
+  if ((st = check_view(y, "fill", "tensor", mask))) return st;
+  if ((st = require_device("fill", {y}))) return st;
+  if ((st = ensure_device())) return st;
+  const int64_t n = (int64_t)y->h * y->w;
+  if (n == 0) return BN_OK;
+  hipStream_t s = as_stream(stream);
+  if (y->dtype == BN_F32) {
+    hipLaunchKernelGGL(fill_kernel<float>, grid1d(n), dim3(256), 0, s, dview<float>(y), (float)value);
+  } else if (y->dtype == BN_U32) {
+    hipLaunchKernelGGL(fill_kernel<uint32_t>, grid1d(n), dim3(256), 0, s, dview<uint32_t>(y),
+                       (uint32_t)value);
+  } else {
+    float f = (float)value;
+    uint32_t u;
+    std::memcpy(&u, &f, 4);
+    u += 0x7fffu + ((u >> 16) & 1u);  // round to nearest even (finite values)
+    hipLaunchKernelGGL(fill_kernel<bf16_t>, grid1d(n), dim3(256), 0, s, dview<bf16_t>(y),
+                       (bf16_t)(u >> 16));
+  }
+  BN_LAUNCH_CHECK();
+  return BN_OK;
+}
+
+int bn_sum(const bn_view *x, const bn_view *y, int axis, void *stream) {
+  const unsigned mask = (1u << BN_F32) | (1u << BN_U32);
+  int st;
+  if ((st = check_view(x, "sum", "input", mask))) return st;
+  if ((st = check_view(y, "sum", "output", mask))) return st;
+  if (axis != 0 && axis != 1) return fail(BN_ERR_INVALID_ARG, "Invalid axis, must be 0 or 1");
+  if (x->dtype != y->dtype) return fail(BN_ERR_UNSUPPORTED, "sum: dtypes differ");
+  if ((axis == 0 && (y->h != 1 || y->w != x->w)) || (axis == 1 && (y->w != 1 || y->h != x->h)))
+    return fail(BN_ERR_SHAPE, "sum: output shape mismatch");
+  if ((st = require_device("sum", {x, y}))) return st;
+  if ((st = ensure_device())) return st;
+  const int n = axis == 0 ? x->w : x->h;
+  if (n == 0 || x->h == 0 || x->w == 0) return BN_OK;
+  if (x->dtype == BN_F32)
+    hipLaunchKernelGGL(sum_kernel<float>, grid1d(n), dim3(256), 0, as_stream(stream),
+                       dview<const float>(x), dview<float>(y), axis);
+  else
+    hipLaunchKernelGGL(sum_kernel<uint32_t>, grid1d(n), dim3(256), 0, as_stream(stream),
+                       dview<const uint32_t>(x), dview<uint32_t>(y), axis);
+  BN_LAUNCH_CHECK();
+  return BN_OK;
+}
+
+int bn_argmax(const bn_view *x, const bn_view *y, void *stream) {
+  int st;
+  if ((st = check_view(x, "argmax", "input", (1u << BN_F32) | (1u << BN_U32)))) return st;
+  if ((st = check_view(y, "argmax", "output", 1u << BN_U32))) return st;
+  if (y->h != x->h || y->w != 1) return fail(BN_ERR_SHAPE, "argmax: output must be (rows, 1)");
+  if ((st = require_device("argmax", {x, y}))) return st;
+  if ((st = ensure_device())) return st;
+  if (x->h == 0 || x->w == 0) return BN_OK;
+  if (x->dtype == BN_F32)
+    hipLaunchKernelGGL(argmax_kernel<float>, grid1d(x->h), dim3(256), 0, as_stream(stream),
+                       dview<const float>(x), dview<uint32_t>(y));
+  else
+    hipLaunchKernelGGL(argmax_kernel<uint32_t>, grid1d(x->h), dim3(256), 0, as_stream(stream),
+                       dview<const uint32_t>(x), dview<uint32_t>(y));
+  BN_LAUNCH_CHECK();
+  return BN_OK;
+}
+
+int bn_copy(const bn_view *x, const bn_view *y, void *stream) {
+  const unsigned mask = (1u << BN_F32) | (1u << BN_BF16) | (1u << BN_U32);
+  int st;
+  if ((st = check_view(x, "copy", "input", mask))) return st;
+  if ((st = check_view(y, "copy", "output", mask))) return st;
+  if (!same_shape(x, y)) return fail(BN_ERR_SHAPE, "copy: shape mismatch");
+  if ((x->dtype == BN_U32) != (y->dtype == BN_U32))
+    return fail(BN_ERR_UNSUPPORTED, "copy: U32 converts to U32 only");
+  if ((st = require_device("copy", {x, y}))) return st;
+  if ((st = ensure_device())) return st;
+  const int64_t n = (int64_t)x->h * x->w;
+  if (n == 0) return BN_OK;
+  hipStream_t s = as_stream(stream);
+  dim3 g = grid1d(n);
+  if (x->dtype == BN_U32)
+    hipLaunchKernelGGL((copy_kernel<uint32_t, uint32_t>), g, dim3(256), 0, s,
+                       dview<const uint32_t>(x), dview<uint32_t>(y));
+  else if (x->dtype == BN_F32 && y->dtype == BN_F32)
+    hipLaunchKernelGGL((copy_kernel<float, float>), g, dim3(256), 0, s, dview<const float>(x),
+                       dview<float>(y));
+  else if (x->dtype == BN_F32)
+    hipLaunchKernelGGL((copy_kernel<float, bf16_t>), g, dim3(256), 0, s, dview<const float>(x),
+                       dview<bf16_t>(y));
+  else if (y->dtype == BN_F32)
+    hipLaunchKernelGGL((copy_kernel<bf16_t, float>), g, dim3(256), 0, s, dview<const bf16_t>(x),
+                       dview<float>(y));
+  else
+    hipLaunchKernelGGL((copy_kernel<bf16_t, bf16_t>), g, dim3(256), 0, s,
+                       dview<const bf16_t>(x), dview<bf16_t>(y));
+  BN_LAUNCH_CHECK();
+  return BN_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,435 @@
+// bn_prefill.hip -- causal GQA prefill attention on gfx950 MFMA.
+//
+// Replaces, per query head h and its KV head g = h / (n_heads/n_kv_heads),
+// the reference chain  Q_h K_g^T -> *scale -> causal softmax(seq_offset) ->
+// @ V_g  (llama_layers.py:174-183, llama_layers.hpp:96-109, with the
+// repeat_kv mapping of llama_layers.hpp:159-163 done by indexing instead of
+// copying) with one flash-style kernel: O(S) memory, K/V blocks staged
+// through LDS, online softmax in fp32.
+//
+// Work decomposition: a 256-thread workgroup (4 waves) owns 128 query rows
+// of one (batch, head); each wave owns 32 rows.  Key blocks of 64 are staged
+// in LDS (K row-major, V transposed) with the next block's global loads in
+// flight while the current block is computed.
+//
+// Per wave and 32-key tile the score tile is computed transposed,
+//   S^T[key][query] = K[key][:] . Q[query][:]      (v_mfma_f32_32x32x16_bf16 /
+//                                                   v_mfma_f32_32x32x2f32)
+// so that each lane holds 16 keys of ONE query: the softmax row max and row
+// sum are in-lane plus a single exchange between the two half-waves.  The
+// output is accumulated transposed as well,
+//   O^T[d][query] += V^T[d][key] . P^T[key][query],
+// whose B operand is exactly the P^T registers the softmax produced (no
+// shuffles), and whose per-query rescale is a per-lane scalar.
+//
+// Causal work is unbalanced (row tile m needs m+1 key blocks); workgroups are
+// issued heaviest-first.  Fully masked key blocks of a wave are skipped; only
+// diagonal / tail blocks evaluate the mask.  Mask: key j is visible to query
+// row i iff j <= i + seq_offset (op_softmax.cuh:89-99) and j < seq_kv.
+#include "bn_common.hpp"
+
+namespace bn {
+namespace {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+constexpr int BM = 128;  // query rows per workgroup
+constexpr int BN = 64;   // keys per LDS block
+constexpr int HD = 64;   // head_dim
+
+struct PrefillParams {
+  const void *q, *k, *v;
+  void *o;
+  int64_t q_bs, q_rs, kv_bs, kv_rs, o_bs, o_rs;
+  int batch, seq_q, seq_kv, n_heads, group, n_mt;
+  int causal, seq_offset;
+  float c;  // scale * log2(e): softmax evaluated as exp2(s*c - m*c)
+};
+
+struct Work {
+  int b, h, g, mt;
+};
+
+__device__ __forceinline__ Work decode_work(const PrefillParams &p) {
+  const int per_m = p.batch * p.n_heads;
+  const int L = blockIdx.x;
+  Work w;
+  w.mt = p.n_mt - 1 - L / per_m;  // heaviest (last) row tiles first
+  const int rem = L - (L / per_m) * per_m;
+  w.b = rem / p.n_heads;
+  w.h = rem - w.b * p.n_heads;
+  w.g = w.h / p.group;
+  return w;
+}
+
+// Key range [0, kend) a set of rows [.., last_row] may see.
+__device__ __forceinline__ int key_end(const PrefillParams &p, int last_row) {
+  if (!p.causal) return p.seq_kv;
+  long e = (long)last_row + p.seq_offset + 1;
+  if (e < 0) e = 0;
+  return e < p.seq_kv ? (int)e : p.seq_kv;
+}
+
+// Online-softmax update of one 64-key block for this lane's query.
+// s[kt][i] holds key kb + kt*32 + (i/4)*8 + hf*4 + (i%4).
+__device__ __forceinline__ void softmax_block(f32x16_t (&s)[2], float &m, float &l,
+                                              f32x16_t (&o)[2], float c, bool need_mask,
+                                              int kb, int hf, long qlimit, int seq_kv) {
+  if (need_mask) {
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int key = kb + kt * 32 + (i >> 2) * 8 + hf * 4 + (i & 3);
+        if (key >= seq_kv || (long)key > qlimit) s[kt][i] = -INFINITY;
+      }
+  }
+  float mx = s[0][0];
+#pragma unroll
+  for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[kt][i]);
+  mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+  const float m_new = fmaxf(m, mx);
+  const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
+  const float mc = m_use * c;
+  const float alpha = __builtin_amdgcn_exp2f(m * c - mc);  // m = -inf -> 0
+  float rs = 0.f;
+#pragma unroll
+  for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const float e = __builtin_amdgcn_exp2f(fmaf(s[kt][i], c, -mc));
+      s[kt][i] = e;
+      rs += e;
+    }
+  l = l * alpha + rs;  // per half-wave partial; halves are summed at the end
+  m = m_new;
+#pragma unroll
+  for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) o[dt][i] *= alpha;
+}
+
+// ------------------------------------------------------------------ bf16
+constexpr int KP16 = HD + 8;  // K row pitch (elements): 144 B, conflict-free b128 reads
+constexpr int VP16 = BN + 4;  // V^T row pitch: 136 B, conflict-free b64 reads
+
+__global__ __launch_bounds__(256, 2) void prefill_bf16_kernel(PrefillParams p) {
+  __shared__ __attribute__((aligned(16))) bf16_t Ks[BN * KP16];
+  __shared__ __attribute__((aligned(16))) bf16_t Vt[HD * VP16];
+
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int r32 = lane & 31, hf = lane >> 5;
+  const Work w = decode_work(p);
+  const bf16_t *Q = (const bf16_t *)p.q + w.b * p.q_bs + (int64_t)w.h * HD;
+  const bf16_t *K = (const bf16_t *)p.k + w.b * p.kv_bs + (int64_t)w.g * HD;
+  const bf16_t *V = (const bf16_t *)p.v + w.b * p.kv_bs + (int64_t)w.g * HD;
+  bf16_t *O = (bf16_t *)p.o + w.b * p.o_bs + (int64_t)w.h * HD;
+
+  const int q_wave0 = w.mt * BM + wave * 32;
+  const int qrow = q_wave0 + r32;
+  const bool row_ok = qrow < p.seq_q;
+
+  // Q^T operand: lane holds Q[qrow][16t + 8hf .. +7] for t = 0..3
+  bf16x8_t qreg[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    if (row_ok)
+      qreg[t] = *(const bf16x8_t *)(Q + (int64_t)qrow * p.q_rs + 16 * t + 8 * hf);
+    else
+      qreg[t] = bf16x8_t{};
+  }
+
+  const int wg_last = min(w.mt * BM + BM, p.seq_q) - 1;
+  const int kend = key_end(p, wg_last);
+  const int nblk = (kend + BN - 1) / BN;
+  const int wave_last = min(q_wave0 + 31, p.seq_q - 1);
+  const int wave_kend = (wave_last < q_wave0) ? 0 : key_end(p, wave_last);
+  const long qlimit = p.causal ? (long)qrow + p.seq_offset : (long)p.seq_kv;
+
+  // global -> register prefetch of one K and V block: 2 x 16 B of each per thread
+  uint4 kreg[2], vreg[2];
+  auto gload = [&](int kb) {
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      const int idx = tid + 256 * c, key = idx >> 3, dc = idx & 7;
+      const int kk = kb + key;
+      if (kk < p.seq_kv) {
+        kreg[c] = *(const uint4 *)(K + (int64_t)kk * p.kv_rs + dc * 8);
+        vreg[c] = *(const uint4 *)(V + (int64_t)kk * p.kv_rs + dc * 8);
+      } else {
+        kreg[c] = make_uint4(0, 0, 0, 0);
+        vreg[c] = make_uint4(0, 0, 0, 0);
+      }
+    }
+  };
+  auto lstore = [&]() {
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      const int idx = tid + 256 * c, key = idx >> 3, dc = idx & 7;
+      *(uint4 *)(Ks + key * KP16 + dc * 8) = kreg[c];
+      const uint32_t u[4] = {vreg[c].x, vreg[c].y, vreg[c].z, vreg[c].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        Vt[(dc * 8 + 2 * e) * VP16 + key] = (bf16_t)(u[e] & 0xffffu);
+        Vt[(dc * 8 + 2 * e + 1) * VP16 + key] = (bf16_t)(u[e] >> 16);
+      }
+    }
+  };
+
+  float m = -INFINITY, l = 0.f;
+  f32x16_t o[2] = {f32x16_t{}, f32x16_t{}};
+
+  if (nblk > 0) gload(0);
+  for (int blk = 0; blk < nblk; ++blk) {
+    const int kb = blk * BN;
+    __syncthreads();
+    lstore();
+    __syncthreads();
+    if (blk + 1 < nblk) gload(kb + BN);
+    if (kb >= wave_kend) continue;  // every row of this wave masks the block
+
+    f32x16_t s[2];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+      s[kt] = f32x16_t{};
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const bf16x8_t a = *(const bf16x8_t *)(Ks + (kt * 32 + r32) * KP16 + 16 * t + 8 * hf);
+        s[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qreg[t], s[kt], 0, 0, 0);
+      }
+    }
+    const bool need_mask =
+        (kb + BN > p.seq_kv) || (p.causal && (long)kb + BN - 1 > (long)q_wave0 + p.seq_offset);
+    softmax_block(s, m, l, o, p.c, need_mask, kb, hf, qlimit, p.seq_kv);
+
+    // O^T += V^T P^T, 16 keys per MFMA.  k-slot (hf, j) of slice u of tile kt
+    // is key kt*32 + 16u + (j/4)*8 + hf*4 + j%4, which is register 8u+j of s[kt].
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        bf16x8_t pb;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) pb[j] = (__bf16)s[kt][8 * u + j];
+        const int kbase = kt * 32 + 16 * u + hf * 4;
+#pragma unroll
+        for (int dt = 0; dt < 2; ++dt) {
+          const bf16_t *vrow = Vt + (dt * 32 + r32) * VP16 + kbase;
+          const bf16x4_t lo = *(const bf16x4_t *)(vrow);
+          const bf16x4_t hi = *(const bf16x4_t *)(vrow + 8);
+          const bf16x8_t a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+          o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb, o[dt], 0, 0, 0);
+        }
+      }
+  }
+
+  const float lt = l + __shfl_xor(l, 32, 64);
+  const float inv = lt > 0.f ? 1.0f / lt : 0.f;  // no visible key -> zeros
+  if (row_ok) {
+    bf16_t *orow = O + (int64_t)qrow * p.o_rs;
+#pragma unroll
+    for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+      for (int gi = 0; gi < 4; ++gi) {
+        const int d0 = dt * 32 + gi * 8 + hf * 4;
+        const uint32_t lo = (uint32_t)f32_to_bf16(o[dt][4 * gi] * inv) |
+                            ((uint32_t)f32_to_bf16(o[dt][4 * gi + 1] * inv) << 16);
+        const uint32_t hi = (uint32_t)f32_to_bf16(o[dt][4 * gi + 2] * inv) |
+                            ((uint32_t)f32_to_bf16(o[dt][4 * gi + 3] * inv) << 16);
+        *(uint2 *)(orow + d0) = make_uint2(lo, hi);
+      }
+  }
+}
+
+// ------------------------------------------------------------------- fp32
+constexpr int KP32 = HD + 4;  // 272 B pitch
+constexpr int VP32 = BN + 4;
+
+__global__ __launch_bounds__(256, 2) void prefill_f32_kernel(PrefillParams p) {
+  __shared__ __attribute__((aligned(16))) float Ks[BN * KP32];
+  __shared__ __attribute__((aligned(16))) float Vt[HD * VP32];
+
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int r32 = lane & 31, hf = lane >> 5;
+  const Work w = decode_work(p);
+  const float *Q = (const float *)p.q + w.b * p.q_bs + (int64_t)w.h * HD;
+  const float *K = (const float *)p.k + w.b * p.kv_bs + (int64_t)w.g * HD;
+  const float *V = (const float *)p.v + w.b * p.kv_bs + (int64_t)w.g * HD;
+  float *O = (float *)p.o + w.b * p.o_bs + (int64_t)w.h * HD;
+
+  const int q_wave0 = w.mt * BM + wave * 32;
+  const int qrow = q_wave0 + r32;
+  const bool row_ok = qrow < p.seq_q;
+
+  // k-slot (hf, t) of the QK^T contraction is d = hf*32 + t
+  float qreg[32];
+#pragma unroll
+  for (int t = 0; t < 32; t += 4) {
+    float4 v4 = row_ok ? *(const float4 *)(Q + (int64_t)qrow * p.q_rs + hf * 32 + t)
+                       : make_float4(0.f, 0.f, 0.f, 0.f);
+    qreg[t] = v4.x; qreg[t + 1] = v4.y; qreg[t + 2] = v4.z; qreg[t + 3] = v4.w;
+  }
+
+  const int wg_last = min(w.mt * BM + BM, p.seq_q) - 1;
+  const int kend = key_end(p, wg_last);
+  const int nblk = (kend + BN - 1) / BN;
+  const int wave_last = min(q_wave0 + 31, p.seq_q - 1);
+  const int wave_kend = (wave_last < q_wave0) ? 0 : key_end(p, wave_last);
+  const long qlimit = p.causal ? (long)qrow + p.seq_offset : (long)p.seq_kv;
+
+  float4 kreg[4], vreg[4];
+  auto gload = [&](int kb) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int idx = tid + 256 * c, key = idx >> 4, dc = idx & 15;
+      const int kk = kb + key;
+      if (kk < p.seq_kv) {
+        kreg[c] = *(const float4 *)(K + (int64_t)kk * p.kv_rs + dc * 4);
+        vreg[c] = *(const float4 *)(V + (int64_t)kk * p.kv_rs + dc * 4);
+      } else {
+        kreg[c] = make_float4(0.f, 0.f, 0.f, 0.f);
+        vreg[c] = make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+    }
+  };
+  auto lstore = [&]() {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int idx = tid + 256 * c, key = idx >> 4, dc = idx & 15;
+      *(float4 *)(Ks + key * KP32 + dc * 4) = kreg[c];
+      Vt[(dc * 4 + 0) * VP32 + key] = vreg[c].x;
+      Vt[(dc * 4 + 1) * VP32 + key] = vreg[c].y;
+      Vt[(dc * 4 + 2) * VP32 + key] = vreg[c].z;
+      Vt[(dc * 4 + 3) * VP32 + key] = vreg[c].w;
+    }
+  };
+
+  float m = -INFINITY, l = 0.f;
+  f32x16_t o[2] = {f32x16_t{}, f32x16_t{}};
+
+  if (nblk > 0) gload(0);
+  for (int blk = 0; blk < nblk; ++blk) {
+    const int kb = blk * BN;
+    __syncthreads();
+    lstore();
+    __syncthreads();
+    if (blk + 1 < nblk) gload(kb + BN);
+    if (kb >= wave_kend) continue;
+
+    f32x16_t s[2];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+      s[kt] = f32x16_t{};
+      const float *krow = Ks + (kt * 32 + r32) * KP32 + hf * 32;
+#pragma unroll
+      for (int t = 0; t < 32; t += 4) {
+        const float4 a = *(const float4 *)(krow + t);
+        s[kt] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.x, qreg[t], s[kt], 0, 0, 0);
+        s[kt] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.y, qreg[t + 1], s[kt], 0, 0, 0);
+        s[kt] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.z, qreg[t + 2], s[kt], 0, 0, 0);
+        s[kt] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.w, qreg[t + 3], s[kt], 0, 0, 0);
+      }
+    }
+    const bool need_mask =
+        (kb + BN > p.seq_kv) || (p.causal && (long)kb + BN - 1 > (long)q_wave0 + p.seq_offset);
+    softmax_block(s, m, l, o, p.c, need_mask, kb, hf, qlimit, p.seq_kv);
+
+    // register i of s[kt] is k-slot hf of key kt*32 + (i/4)*8 + hf*4 + i%4
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int gi = 0; gi < 4; ++gi) {
+        const int kbase = kt * 32 + gi * 8 + hf * 4;
+#pragma unroll
+        for (int dt = 0; dt < 2; ++dt) {
+          const float4 a = *(const float4 *)(Vt + (dt * 32 + r32) * VP32 + kbase);
+          o[dt] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.x, s[kt][4 * gi], o[dt], 0, 0, 0);
+          o[dt] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.y, s[kt][4 * gi + 1], o[dt], 0, 0, 0);
+          o[dt] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.z, s[kt][4 * gi + 2], o[dt], 0, 0, 0);
+          o[dt] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.w, s[kt][4 * gi + 3], o[dt], 0, 0, 0);
+        }
+      }
+  }
+
+  const float lt = l + __shfl_xor(l, 32, 64);
+  const float inv = lt > 0.f ? 1.0f / lt : 0.f;
+  if (row_ok) {
+    float *orow = O + (int64_t)qrow * p.o_rs;
+#pragma unroll
+    for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+      for (int gi = 0; gi < 4; ++gi) {
+        const int d0 = dt * 32 + gi * 8 + hf * 4;
+        *(float4 *)(orow + d0) = make_float4(o[dt][4 * gi] * inv, o[dt][4 * gi + 1] * inv,
+                                             o[dt][4 * gi + 2] * inv, o[dt][4 * gi + 3] * inv);
+      }
+  }
+}
+
+bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace
+}  // namespace bn
+
+using namespace bn;
+
+extern "C" int bn_gqa_prefill(int dtype, const void *q, const void *k, const void *v, void *o,
+                              int batch, int seq_q, int seq_kv, int n_heads, int n_kv_heads,
+                              int head_dim, int64_t q_batch_stride, int64_t q_row_stride,
+                              int64_t kv_batch_stride, int64_t kv_row_stride,
+                              int64_t o_batch_stride, int64_t o_row_stride, float scale,
+                              int causal, int seq_offset, void *stream) {
+  const char *op = "GQA prefill";
+  if (dtype != BN_F32 && dtype != BN_BF16)
+    return fail(BN_ERR_UNSUPPORTED, std::string(op) + ": dtype must be F32 or BF16");
+  if (batch < 0 || seq_q < 0 || seq_kv < 0)
+    return fail(BN_ERR_SHAPE, std::string(op) + ": negative batch or sequence length");
+  if (n_heads <= 0 || n_kv_heads <= 0 || n_heads % n_kv_heads != 0)
+    return fail(BN_ERR_SHAPE, std::string(op) + ": num_heads must be a positive multiple of num_kv_heads");
+  if (head_dim != HD)
+    return fail(BN_ERR_UNSUPPORTED, std::string(op) + ": head_dim must be 64");
+  if (!(scale > 0.f) || !std::isfinite(scale))
+    return fail(BN_ERR_INVALID_ARG, std::string(op) + ": scale must be positive and finite");
+  if (batch == 0 || seq_q == 0) return BN_OK;
+  if (!q || !o || (seq_kv > 0 && (!k || !v)))
+    return fail(BN_ERR_INVALID_ARG, std::string(op) + ": NULL tensor pointer");
+  if (q_row_stride < (int64_t)n_heads * HD || o_row_stride < (int64_t)n_heads * HD ||
+      kv_row_stride < (int64_t)n_kv_heads * HD)
+    return fail(BN_ERR_SHAPE, std::string(op) + ": row stride smaller than heads*head_dim");
+  if (batch > 1 && (q_batch_stride < (int64_t)seq_q * q_row_stride ||
+                    o_batch_stride < (int64_t)seq_q * o_row_stride ||
+                    kv_batch_stride < (int64_t)seq_kv * kv_row_stride))
+    return fail(BN_ERR_SHAPE, std::string(op) + ": batch stride smaller than seq*row_stride");
+  const int64_t vec = dtype == BN_F32 ? 4 : 8;  // elements per 16 bytes
+  if (!aligned16(q) || !aligned16(o) || (seq_kv > 0 && (!aligned16(k) || !aligned16(v))) ||
+      q_row_stride % vec || kv_row_stride % vec || o_row_stride % vec || q_batch_stride % vec ||
+      kv_batch_stride % vec || o_batch_stride % vec)
+    return fail(BN_ERR_UNSUPPORTED,
+                std::string(op) + ": pointers must be 16-byte aligned and strides multiples of 16 bytes");
+  const int n_mt = (seq_q + BM - 1) / BM;
+  const int64_t n_wg = (int64_t)batch * n_heads * n_mt;
+  if (n_wg > 0x7fffffff) return fail(BN_ERR_UNSUPPORTED, std::string(op) + ": problem too large");
+  int st = ensure_device();
+  if (st) return st;
+
+  PrefillParams p;
+  p.q = q; p.k = k; p.v = v; p.o = o;
+  p.q_bs = q_batch_stride; p.q_rs = q_row_stride;
+  p.kv_bs = kv_batch_stride; p.kv_rs = kv_row_stride;
+  p.o_bs = o_batch_stride; p.o_rs = o_row_stride;
+  p.batch = batch; p.seq_q = seq_q; p.seq_kv = seq_kv; p.n_heads = n_heads;
+  p.group = n_heads / n_kv_heads; p.n_mt = n_mt;
+  p.causal = causal ? 1 : 0; p.seq_offset = seq_offset;
+  p.c = scale * 1.4426950408889634f;
+  hipStream_t s = as_stream(stream);
+  if (dtype == BN_BF16)
+    hipLaunchKernelGGL(prefill_bf16_kernel, dim3((unsigned)n_wg), dim3(256), 0, s, p);
+  else
+    hipLaunchKernelGGL(prefill_f32_kernel, dim3((unsigned)n_wg), dim3(256), 0, s, p);
+  BN_LAUNCH_CHECK();
+  return BN_OK;
+}

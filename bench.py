@@ -1,0 +1,238 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X GQA attention path (one JSON line on stdout).
+
+Headline (``value``): causal GQA prefill, BASELINE config 2 in bf16
+(B=4, S=2048, 32 query / 4 KV heads, head_dim 64, scale 1/8), in TFLOP/s of
+algorithmic work 4*B*H*D*S(S+1)/2 (unmasked QK^T and PV MACs x 2).
+One step = one prefill launch over the whole batch, inputs resident in HBM.
+
+Also measured in the same run and reported as sub-objects:
+  decode        config 3: B=64 one-token decode over a bf16 cache of 4096
+                (uniform), in GB/s of K/V + q + o bytes; two cache sets are
+                rotated so the 268 MB cache cannot sit in the 256 MB MALL
+  decode_ragged config 3 with lengths uniform in [512, 4096]
+  prefill_fp32  config 2 in fp32
+  rmsnorm_rope  config 5's fused RMSNorm+RoPE on [16384, 2048] bf16, GB/s
+  prefill_long  config 5's prefill, B=1, S=16384, bf16
+Each carries a ``roofline`` object priced against MI355X peaks (bf16 MFMA
+2.5 PFLOP/s dense, fp32 MFMA 157.3 TFLOP/s, HBM 8 TB/s).  ``cpu_baseline``
+times the CPU oracle (a single-threaded C restatement of the reference
+kernels, test infrastructure) on a bounded sample of the same workload.
+
+Timing: hip events recorded on the stream the kernels are launched on (the
+current torch stream, passed to the C ABI), around K back-to-back launches
+after W warm-up launches, with torch.cuda.synchronize() on both sides.
+"""
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "baranet-bdml_amd"))
+sys.path.insert(0, ROOT)
+
+PEAK_BF16_TFLOPS = 2500.0
+PEAK_FP32_TFLOPS = 157.3
+PEAK_HBM_GBS = 8000.0
+METRIC = "GQA prefill attention TFLOP/s + % MFMA peak; decode KV GB/s + % HBM peak"
+
+
+def prefill_flops(B, S, H, D):
+    return 4 * B * H * D * S * (S + 1) // 2
+
+
+def decode_bytes(lens, Hkv, D, B, H, elem):
+    return int(sum(2 * int(L) * Hkv * D * elem for L in lens) + 2 * B * H * D * elem)
+
+
+def time_launches(fn, steps, warmup):
+    """Average launch duration (ms) of fn() over `steps` back-to-back calls."""
+    import torch
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for i in range(steps):
+        fn(i)
+    e.record()
+    torch.cuda.synchronize()
+    return s.elapsed_time(e) / steps
+
+
+def roofline(bound, achieved, peak, unit, traffic=None):
+    return {"bound": bound, "achieved": round(achieved, 3), "peak": peak, "unit": unit,
+            "frac": round(achieved / peak, 4), "traffic": traffic}
+
+
+def bench_prefill(B_, S, H, Hkv, dtype, steps, warmup, seed=0):
+    import torch
+    import bnhip
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    td = torch.bfloat16 if dtype == "bf16" else torch.float32
+    q = torch.randn((B_, S, H, 64), generator=g, device="cuda").to(td)
+    k = torch.randn((B_, S, Hkv, 64), generator=g, device="cuda").to(td)
+    v = torch.randn((B_, S, Hkv, 64), generator=g, device="cuda").to(td)
+    o = torch.empty_like(q)
+    ms = time_launches(lambda i: bnhip.gqa_prefill(q, k, v, o, scale=0.125), steps, warmup)
+    fl = prefill_flops(B_, S, H, 64)
+    tflops = fl / (ms * 1e-3) / 1e12
+    peak = PEAK_BF16_TFLOPS if dtype == "bf16" else PEAK_FP32_TFLOPS
+    return {"value": round(tflops, 3), "unit": "TFLOP/s", "ms_per_launch": round(ms, 5),
+            "flops_per_launch": fl,
+            "roofline": roofline("mfma", tflops, peak, "TFLOP/s")}
+
+
+def bench_decode(ragged, steps, warmup, seed=2):
+    import numpy as np
+    import torch
+    import bnhip
+    B_, L, H, Hkv = 64, 4096, 32, 4
+    r = np.random.default_rng(seed)
+    lens = r.integers(512, 4097, B_).astype(np.int32) if ragged else np.full(B_, L, np.int32)
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    sets = []
+    for _ in range(2):  # 2 x 268 MB > 256 MB MALL: every launch streams from HBM
+        sets.append((torch.randn((B_, H, 64), generator=g, device="cuda").bfloat16(),
+                     torch.randn((B_, L, Hkv, 64), generator=g, device="cuda").bfloat16(),
+                     torch.randn((B_, L, Hkv, 64), generator=g, device="cuda").bfloat16()))
+    ld = torch.from_numpy(lens).cuda()
+    ws = bnhip.decode_workspace(B_, L, H)
+    o = torch.empty((B_, H, 64), device="cuda", dtype=torch.bfloat16)
+
+    def run(i):
+        q, kc, vc = sets[i % 2]
+        bnhip.gqa_decode(q, kc, vc, ld, o, scale=0.125, workspace=ws)
+
+    ms = time_launches(run, steps, warmup)
+    nb = decode_bytes(lens, Hkv, 64, B_, H, 2)
+    gbs = nb / (ms * 1e-3) / 1e9
+    return {"value": round(gbs, 2), "unit": "GB/s", "ms_per_launch": round(ms, 5),
+            "bytes_per_launch": nb, "lengths": "uniform 4096" if not ragged else
+            f"ragged U[512,4096] seed {seed}, sum {int(lens.sum())}",
+            "roofline": roofline("hbm", gbs, PEAK_HBM_GBS, "GB/s")}
+
+
+def bench_rmsnorm_rope(steps, warmup):
+    import ctypes as C
+    import torch
+    import bnhip
+    rows, w = 16384, 2048
+    g = torch.Generator(device="cuda").manual_seed(5)
+    xs = [torch.randn((rows, w), generator=g, device="cuda").bfloat16() for _ in range(2)]
+    ys = [torch.empty_like(xs[0]) for _ in range(2)]
+    wt = torch.ones((1, w), device="cuda", dtype=torch.bfloat16)
+    wv = bnhip.view(wt)
+    views = [(bnhip.view(x), bnhip.view(y)) for x, y in zip(xs, ys)]
+    st = bnhip.stream_of()
+
+    def run(i):
+        xv, yv = views[i % 2]
+        bnhip.call("bn_rmsnorm_rope", C.byref(xv), C.byref(wv), C.byref(yv), 1e-5, 0, 64,
+                   1e4, st)
+
+    ms = time_launches(run, steps, warmup)
+    nb = 2 * rows * w * 2 + w * 2
+    gbs = nb / (ms * 1e-3) / 1e9
+    return {"value": round(gbs, 2), "unit": "GB/s", "ms_per_launch": round(ms, 5),
+            "bytes_per_launch": nb, "roofline": roofline("hbm", gbs, PEAK_HBM_GBS, "GB/s")}
+
+
+def cpu_baseline_prefill(budget_s=12.0):
+    """CPU oracle (single thread) on whole (batch, head) pairs of config 2."""
+    import numpy as np
+    from oracle import oracle as O
+    S, D = 2048, 64
+    r = np.random.default_rng(0)
+    done, fl, t0 = 0, 0, time.perf_counter()
+    while done < 128 and (time.perf_counter() - t0) < budget_s:
+        q = r.standard_normal((1, S, 1, D)).astype(np.float32)
+        k = r.standard_normal((1, S, 1, D)).astype(np.float32)
+        v = r.standard_normal((1, S, 1, D)).astype(np.float32)
+        O.gqa_prefill(q, k, v, 0.125, True, 0)
+        done += 1
+        fl += prefill_flops(1, S, 1, D)
+    el = time.perf_counter() - t0
+    return {"value": round(fl / el / 1e12, 6), "unit": "TFLOP/s", "cores": 1, "kind": "port",
+            "sample": f"{done} of 128 (batch, head) pairs of config 2 (S=2048, D=64, causal), "
+                      f"fp32 oracle, {el:.1f} s; the oracle computes full S x S scores as the "
+                      f"reference chain does, so only the causal half is counted as work"}
+
+
+def cpu_baseline_decode(budget_s=6.0):
+    import numpy as np
+    from oracle import oracle as O
+    L, H, Hkv, D = 4096, 32, 4, 64
+    r = np.random.default_rng(2)
+    done, nb, t0 = 0, 0, time.perf_counter()
+    while done < 64 and (time.perf_counter() - t0) < budget_s:
+        q = r.standard_normal((1, H, D)).astype(np.float32)
+        kc = r.standard_normal((1, L, Hkv, D)).astype(np.float32)
+        vc = r.standard_normal((1, L, Hkv, D)).astype(np.float32)
+        O.gqa_decode(q, kc, vc, np.array([L], np.int32), 0.125)
+        done += 1
+        nb += decode_bytes([L], Hkv, D, 1, H, 2)
+    el = time.perf_counter() - t0
+    return {"value": round(nb / el / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"{done} of 64 sequences of config 3 (L=4096), fp32 oracle, {el:.1f} s, "
+                      f"bytes counted at bf16 size"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
+    ap.add_argument("--only", default="", help="comma list: prefill,decode,fp32,norm,long")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
+              "(the attention path has no multi-GPU code; see DESIGN.md for how it would shard)",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        sys.exit(1)
+    only = set(filter(None, args.only.split(",")))
+    want = lambda k: not only or k in only
+    K, W = args.steps, args.warmup
+
+    head = bench_prefill(4, 2048, 32, 4, "bf16", K, W)
+    out = {"metric": METRIC, "value": head["value"], "unit": "TFLOP/s", "n_gpus": 1,
+           "steps": K, "warmup": W, "ms_per_step": head["ms_per_launch"],
+           "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+           "data": "synthetic N(0,1) from a fixed seed (torch.Generator 0)",
+           "config": {"workload": "causal GQA prefill (BASELINE config 2)", "batch": 4,
+                      "seq_len": 2048, "n_heads": 32, "n_kv_heads": 4, "head_dim": 64,
+                      "scale": 0.125, "flops_per_step": head["flops_per_launch"]},
+           "roofline": head["roofline"]}
+    print(f"prefill bf16: {head['value']} TFLOP/s ({head['ms_per_launch']} ms)", file=sys.stderr,
+          flush=True)
+    if want("decode"):
+        out["decode"] = bench_decode(False, K, W)
+        out["decode_ragged"] = bench_decode(True, K, W)
+        print(f"decode: {out['decode']['value']} GB/s", file=sys.stderr, flush=True)
+    if want("fp32"):
+        out["prefill_fp32"] = bench_prefill(4, 2048, 32, 4, "fp32", max(K // 2, 3), 2)
+        print(f"prefill fp32: {out['prefill_fp32']['value']} TFLOP/s", file=sys.stderr, flush=True)
+    if want("norm"):
+        out["rmsnorm_rope"] = bench_rmsnorm_rope(K, W)
+        print(f"rmsnorm_rope: {out['rmsnorm_rope']['value']} GB/s", file=sys.stderr, flush=True)
+    if want("long"):
+        out["prefill_long"] = bench_prefill(1, 16384, 32, 4, "bf16", max(K // 4, 3), 1)
+        print(f"prefill S=16384: {out['prefill_long']['value']} TFLOP/s", file=sys.stderr,
+              flush=True)
+    if not args.no_cpu:
+        out["cpu_baseline"] = cpu_baseline_prefill()
+        if "decode" in out:
+            out["decode"]["cpu_baseline"] = cpu_baseline_decode()
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,194 @@
+/*
+ * bn_hip.h -- C ABI of the MI355X (gfx950) attention-path library libbnhip.so.
+ *
+ * This is the boundary between host code (the pybind11 module `bten`, or any
+ * FFI) and the HIP kernels.  Signatures carry plain pointers, sizes and POD
+ * views only; no HIP, torch or C++ types cross it.  Every entry point returns
+ * a bn_status; on failure bn_last_error() returns a thread-local message with
+ * the same stem the reference throws as std::runtime_error (for example
+ * "RMSNorm: weight shape must be (1, hidden_dim)", op_rmsnorm.cuh:146).
+ * All arguments are validated on the host before anything is launched.
+ *
+ * Streams are opaque (`void *` holding a hipStream_t; NULL = the legacy
+ * default stream, which is what the reference launches on).  Kernels are
+ * asynchronous with respect to the host, like the reference's launches.
+ *
+ * Views: bn_view restates the reference's 2-D strided Tensor<T>
+ * (src/utils/tensor.cuh:41-52): element (r, c) lives at
+ * data[offset + r*stride_h + c*stride_w].  Transposes and slices are views
+ * (tensor.cuh:133-171) and every op accepts them.
+ */
+#ifndef BN_HIP_H
+#define BN_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define BN_ABI_VERSION 1
+
+typedef enum bn_status {
+  BN_OK = 0,
+  BN_ERR_INVALID_ARG = 1, /* null pointer, bad enum, negative size */
+  BN_ERR_SHAPE = 2,       /* shape mismatch, divisibility (reference runtime_error) */
+  BN_ERR_UNSUPPORTED = 3, /* valid request outside what the kernels implement */
+  BN_ERR_HIP = 4,         /* HIP runtime error: "HIP Error: <msg> (<code>) at file:line" */
+  BN_ERR_OOM = 5,         /* memory pool could not satisfy an allocation */
+  BN_ERR_NOT_DEVICE = 6   /* host tensor given to a GPU op ("only GPU implementation available") */
+} bn_status;
+
+typedef enum bn_dtype { BN_F32 = 0, BN_BF16 = 1, BN_U32 = 2 } bn_dtype;
+
+typedef struct bn_view {
+  void *data;        /* base of the allocation */
+  int64_t offset;    /* element offset of element (0, 0) */
+  int32_t h, w;      /* rows, columns */
+  int32_t stride_h;  /* elements between rows */
+  int32_t stride_w;  /* elements between columns */
+  int32_t dtype;     /* bn_dtype */
+  int32_t on_device; /* 1: device memory, 0: host memory */
+} bn_view;
+
+/* ------------------------------------------------------------------ runtime */
+int bn_abi_version(void);
+const char *bn_last_error(void);
+/* Select the device and configure its stream-ordered pool.  Called implicitly
+ * by the first allocation; explicit calls pick another device. */
+int bn_init(int device);
+int bn_device_count(int *count);
+int bn_stream_create(void **stream);
+int bn_stream_destroy(void *stream);
+int bn_stream_synchronize(void *stream);
+int bn_device_synchronize(void);
+
+/* ------------------------------------------------------------- memory pool
+ * Replaces CudaMemoryPool / PooledMemory (src/utils/memory_pool.cuh:15-125)
+ * and the per-tensor cudaMalloc/cudaFree of Tensor<T> (tensor.cuh:15-26,
+ * 59-77).  Allocations are stream-ordered (hipMallocAsync on the device's
+ * memory pool with an unbounded release threshold), so a free never
+ * synchronises the device; memory returns to the driver only through
+ * bn_pool_trim. */
+typedef struct bn_pool_stats {
+  uint64_t bytes_in_use;      /* live bytes handed out (requested sizes) */
+  uint64_t peak_bytes_in_use; /* high-water mark since the last reset */
+  uint64_t bytes_reserved;    /* bytes the driver pool currently holds */
+  uint64_t n_allocs;          /* successful bn_alloc calls */
+  uint64_t n_frees;           /* successful bn_free calls */
+  uint64_t n_live;            /* allocations not yet freed */
+} bn_pool_stats;
+
+int bn_alloc(void **ptr, size_t bytes, void *stream);
+int bn_free(void *ptr, void *stream);
+int bn_pool_get_stats(bn_pool_stats *out);
+int bn_pool_reset_peak(void);
+int bn_pool_trim(size_t min_bytes_to_keep);
+/* Test hook: make allocations fail with BN_ERR_OOM once more than
+ * `limit_bytes` are in use (0 = no limit). */
+int bn_pool_set_limit(size_t limit_bytes);
+
+/* kind: 0 host->device, 1 device->host, 2 device->device, 3 host->host.
+ * Host<->device copies are synchronous with respect to the host, like
+ * cudaMemcpy in Tensor::toHost/toDevice (tensor.cuh:80-131). */
+int bn_memcpy(void *dst, const void *src, size_t bytes, int kind, void *stream);
+
+/* --------------------------------------------------------------- path ops */
+/* op_rmsnorm (src/ops/op_rmsnorm.cuh:135-159): y = x / sqrt(mean(x^2)+eps) * w.
+ * x, y: [rows, hidden]; weight: [1, hidden].  F32 or BF16 (all the same). */
+int bn_rmsnorm(const bn_view *x, const bn_view *weight, const bn_view *y,
+               float eps, void *stream);
+/* op_rmsnorm_backward (op_rmsnorm.cuh:161-187); dweight is overwritten. */
+int bn_rmsnorm_backward(const bn_view *x, const bn_view *weight,
+                        const bn_view *dy, const bn_view *dx,
+                        const bn_view *dweight, float eps, void *stream);
+/* op_rope (src/ops/op_rope.cuh:101-126): interleaved-pair rotation of every
+ * head_dim-wide column block, position = row + position_offset. */
+int bn_rope(const bn_view *x, const bn_view *y, int position_offset,
+            int head_dim, float theta, void *stream);
+/* op_rope_backward (op_rope.cuh:158-193). */
+int bn_rope_backward(const bn_view *dy, const bn_view *dx, int position_offset,
+                     int head_dim, float theta, void *stream);
+/* No single reference counterpart: replaces op_rmsnorm followed by op_rope
+ * on its output (one HBM read and one write instead of two each). */
+int bn_rmsnorm_rope(const bn_view *x, const bn_view *weight, const bn_view *y,
+                    float eps, int position_offset, int head_dim, float theta,
+                    void *stream);
+/* op_softmax (src/ops/op_softmax.cuh:153-180): row softmax; with causal,
+ * column i of row r is kept iff i <= r + seq_offset, masked outputs are 0. */
+int bn_softmax(const bn_view *x, const bn_view *y, int causal, int seq_offset,
+               void *stream);
+/* op_softmax_backward (op_softmax.cuh:226-246). */
+int bn_softmax_backward(const bn_view *y, const bn_view *dy, const bn_view *dx,
+                        void *stream);
+/* op_mm (src/ops/op_mm.cuh:39-57): c = a @ b, fp32, any strides. */
+int bn_matmul(const bn_view *a, const bn_view *b, const bn_view *c, void *stream);
+/* repeat_kv (src/llama/llama_layers.hpp:131-175, llama_layers.py:105-138):
+ * out column block kv_h*n_rep + r = kv column block kv_h, on the device. */
+int bn_repeat_kv(const bn_view *kv, const bn_view *out, int head_dim, int n_rep,
+                 void *stream);
+
+/* Elementwise surface used by the layers (src/ops/op_elemwise.cuh:326-507,
+ * op_silu.cuh, op_reduction.cuh).  Binary ops broadcast b along a unit
+ * dimension as op_elemwise_binary_w_bcast_kernel does (:221-243). */
+typedef enum bn_binop { BN_ADD = 0, BN_SUB = 1, BN_MUL = 2, BN_EQ = 3 } bn_binop;
+typedef enum bn_unop {
+  BN_RELU = 0, BN_SILU = 1, BN_ADD_SCALAR = 2, BN_MUL_SCALAR = 3
+} bn_unop;
+typedef enum bn_gradop { BN_RELU_BACK = 0, BN_SILU_BACK = 1 } bn_gradop;
+int bn_binary(int op, const bn_view *a, const bn_view *b, const bn_view *y,
+              void *stream);
+int bn_unary(int op, const bn_view *x, float scalar, const bn_view *y,
+             void *stream);
+int bn_unary_backward(int op, const bn_view *x, const bn_view *dy,
+                      const bn_view *dx, void *stream);
+/* op_const_fill; value is reinterpreted for U32 views. */
+int bn_fill(const bn_view *y, double value, void *stream);
+/* op_sum (axis 0 -> [1, w], axis 1 -> [h, 1]) and op_argmax (row-wise, U32). */
+int bn_sum(const bn_view *x, const bn_view *y, int axis, void *stream);
+int bn_argmax(const bn_view *x, const bn_view *y, void *stream);
+/* Converting copy between views of the same shape (F32 <-> BF16, same dtype). */
+int bn_copy(const bn_view *x, const bn_view *y, void *stream);
+
+/* ----------------------------------------------------- fused GQA attention
+ * No single reference counterpart: replaces the per-head chain
+ *   Q_h @ K_g^T (op_mm) -> * scale (op_multiply) -> op_softmax(causal,
+ *   seq_offset) -> @ V_g (op_mm),       g = h / (n_heads / n_kv_heads)
+ * (llama_layers.py:174-183 / llama_layers.hpp:96-109 applied per head,
+ * repeat_kv mapping of llama_layers.hpp:159-163).
+ *
+ * Layout "bshd": element (b, s, head, d) at base[b*batch_stride +
+ * s*row_stride + head*head_dim + d], strides in elements; the reference's
+ * [S, heads*head_dim] row per token is the b = 0 slice.  dtype is BN_F32 or
+ * BN_BF16 for q, k, v and o alike; accumulation is fp32.  head_dim must be 64.
+ * With causal, key j is visible to query row i iff j <= i + seq_offset
+ * (op_softmax.cuh:89-99); a row with no visible key produces zeros. */
+int bn_gqa_prefill(int dtype, const void *q, const void *k, const void *v,
+                   void *o, int batch, int seq_q, int seq_kv, int n_heads,
+                   int n_kv_heads, int head_dim, int64_t q_batch_stride,
+                   int64_t q_row_stride, int64_t kv_batch_stride,
+                   int64_t kv_row_stride, int64_t o_batch_stride,
+                   int64_t o_row_stride, float scale, int causal,
+                   int seq_offset, void *stream);
+
+/* KV-cache decode: one new query token per sequence.  The reference has no
+ * KV cache (llama_model.py:135-141 recomputes the prefix); this is the last
+ * row of bn_gqa_prefill with seq_offset = seq_lens[b]-1 over keys
+ * [0, seq_lens[b]).  q, o: [batch, n_heads, head_dim] contiguous; caches:
+ * [batch, max_len, n_kv_heads, head_dim] contiguous; seq_lens: device int32
+ * [batch], each in [1, max_len] (checked on the device: out-of-range lengths
+ * are clamped and reported as zeros).  workspace: device memory of
+ * bn_gqa_decode_workspace_size() bytes (NULL: taken from the pool). */
+size_t bn_gqa_decode_workspace_size(int batch, int max_len, int n_heads,
+                                    int head_dim);
+int bn_gqa_decode(int dtype, const void *q, const void *k_cache,
+                  const void *v_cache, const int32_t *seq_lens, void *o,
+                  int batch, int max_len, int n_heads, int n_kv_heads,
+                  int head_dim, float scale, void *workspace,
+                  size_t workspace_bytes, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* BN_HIP_H */

@@ -1,0 +1,146 @@
+"""C-ABI checks that need no GPU: the library loads, exports every symbol the
+public header declares, and rejects malformed requests during host-side
+validation (before anything could be launched) with the reference's error
+stems and the documented status codes."""
+import ctypes as C
+
+import pytest
+
+import bnhip as B
+
+
+def test_library_exports_every_declared_symbol():
+    L = B.lib()
+    names = B.declared_symbols()
+    assert len(names) >= 30
+    missing = [n for n in names if not hasattr(L, n)]
+    assert not missing, missing
+    assert L.bn_abi_version() == 1
+
+
+def st(name, *args):
+    return B.status_of(name, *args)
+
+
+def V(*a, **k):
+    return C.byref(B.host_view(*a, **k))
+
+
+def test_rmsnorm_validation_order_matches_reference():
+    # shape errors first (op_rmsnorm.cuh:142-147), then the device (:148-150)
+    s, m = st("bn_rmsnorm", V(4, 64), V(1, 32), V(4, 64), 1e-6, None)
+    assert s == B.BN_ERR_SHAPE and m == "RMSNorm: weight shape must be (1, hidden_dim)"
+    s, m = st("bn_rmsnorm", V(4, 64), V(1, 64), V(4, 63), 1e-6, None)
+    assert s == B.BN_ERR_SHAPE and m == "RMSNorm: input/output shape mismatch"
+    s, m = st("bn_rmsnorm", V(4, 64), V(1, 64), V(4, 64), 1e-6, None)
+    assert s == B.BN_ERR_NOT_DEVICE and m == "RMSNorm: only GPU implementation available"
+
+
+def test_rope_validation():
+    s, m = st("bn_rope", V(4, 96), V(4, 96), 0, 64, 1e4, None)
+    assert s == B.BN_ERR_SHAPE and m == "RoPE: hidden_dim must be divisible by head_dim"
+    s, m = st("bn_rope", V(4, 64), V(3, 64), 0, 64, 1e4, None)
+    assert s == B.BN_ERR_SHAPE and m == "RoPE: input/output shape mismatch"
+    s, m = st("bn_rope", V(4, 63), V(4, 63), 0, 63, 1e4, None)
+    assert s == B.BN_ERR_SHAPE  # odd head_dim has no pairs
+    s, m = st("bn_rope", V(4, 64), V(4, 64), 0, 64, 1e4, None)
+    assert s == B.BN_ERR_NOT_DEVICE and m == "RoPE: only GPU implementation available"
+    s, _ = st("bn_rmsnorm_rope", V(4, 64), V(1, 64), V(4, 64), 1e-6, 0, 48, 1e4, None)
+    assert s == B.BN_ERR_SHAPE
+
+
+def test_softmax_and_matmul_validation():
+    s, m = st("bn_softmax", V(4, 64), V(4, 65), 1, 0, None)
+    assert s == B.BN_ERR_SHAPE and m == "Softmax: input/output shape mismatch"
+    s, m = st("bn_softmax", V(4, 64), V(4, 64), 1, 0, None)
+    assert s == B.BN_ERR_NOT_DEVICE and m == "Softmax: only GPU implementation available"
+    s, m = st("bn_matmul", V(4, 8), V(9, 3), V(4, 3), None)
+    assert s == B.BN_ERR_SHAPE and m.startswith("a,b,out tensor shape mismatch")
+    s, m = st("bn_matmul", V(4, 8), V(8, 3), V(4, 3), None)
+    assert s == B.BN_ERR_NOT_DEVICE
+
+
+def test_dtype_and_null_checks():
+    s, _ = st("bn_rmsnorm", None, V(1, 64), V(4, 64), 1e-6, None)
+    assert s == B.BN_ERR_INVALID_ARG
+    s, _ = st("bn_matmul", V(4, 8, dtype=B.BN_BF16), V(8, 3), V(4, 3), None)
+    assert s == B.BN_ERR_UNSUPPORTED
+    s, _ = st("bn_rmsnorm", V(4, 64, dtype=B.BN_BF16), V(1, 64), V(4, 64), 1e-6, None)
+    assert s == B.BN_ERR_UNSUPPORTED
+    s, _ = st("bn_binary", 9, V(2, 2), V(2, 2), V(2, 2), None)
+    assert s == B.BN_ERR_INVALID_ARG
+    s, m = st("bn_binary", B.BN_ADD, V(2, 3), V(3, 2), V(2, 3), None)
+    assert s == B.BN_ERR_SHAPE and m == "a,b shape mismatch"
+
+
+def prefill_args(**kw):
+    a = dict(dtype=B.BN_BF16, q=0x1000, k=0x2000, v=0x3000, o=0x4000, batch=4, seq_q=2048,
+             seq_kv=2048, H=32, Hkv=4, D=64, qbs=2048 * 2048, qrs=2048, kvbs=2048 * 256,
+             kvrs=256, obs=2048 * 2048, ors=2048, scale=0.125, causal=1, off=0)
+    a.update(kw)
+    return (a["dtype"], a["q"], a["k"], a["v"], a["o"], a["batch"], a["seq_q"], a["seq_kv"],
+            a["H"], a["Hkv"], a["D"], a["qbs"], a["qrs"], a["kvbs"], a["kvrs"], a["obs"],
+            a["ors"], a["scale"], a["causal"], a["off"], None)
+
+
+@pytest.mark.parametrize("kw,status", [
+    (dict(H=30), B.BN_ERR_SHAPE),               # H % Hkv != 0
+    (dict(Hkv=0), B.BN_ERR_SHAPE),
+    (dict(D=128), B.BN_ERR_UNSUPPORTED),
+    (dict(dtype=B.BN_U32), B.BN_ERR_UNSUPPORTED),
+    (dict(seq_q=-1), B.BN_ERR_SHAPE),
+    (dict(qrs=1024), B.BN_ERR_SHAPE),           # row stride < H*D
+    (dict(kvbs=100), B.BN_ERR_SHAPE),           # batch stride < S*row stride
+    (dict(q=0x1004), B.BN_ERR_UNSUPPORTED),     # misaligned
+    (dict(kvrs=260, kvbs=2048 * 264), B.BN_ERR_UNSUPPORTED),  # stride not 16-byte multiple
+    (dict(q=0), B.BN_ERR_INVALID_ARG),
+    (dict(scale=-1.0), B.BN_ERR_INVALID_ARG),
+    (dict(scale=float("nan")), B.BN_ERR_INVALID_ARG),
+])
+def test_prefill_validation(kw, status):
+    s, m = st("bn_gqa_prefill", *prefill_args(**kw))
+    assert s == status, m
+    assert m.startswith("GQA prefill:")
+
+
+def test_prefill_empty_is_noop():
+    assert st("bn_gqa_prefill", *prefill_args(batch=0))[0] == B.BN_OK
+    assert st("bn_gqa_prefill", *prefill_args(seq_q=0))[0] == B.BN_OK
+
+
+@pytest.mark.parametrize("kw,status", [
+    (dict(H=24), B.BN_ERR_UNSUPPORTED),   # 6 heads per KV head
+    (dict(H=30), B.BN_ERR_SHAPE),
+    (dict(D=32), B.BN_ERR_UNSUPPORTED),
+    (dict(L=0), B.BN_ERR_SHAPE),
+    (dict(lens=0), B.BN_ERR_INVALID_ARG),
+    (dict(q=0x1008), B.BN_ERR_UNSUPPORTED),
+    (dict(ws=0x9000, wsb=16), B.BN_ERR_INVALID_ARG),  # workspace too small
+])
+def test_decode_validation(kw, status):
+    a = dict(dt=B.BN_BF16, q=0x1000, k=0x2000, v=0x3000, lens=0x5000, o=0x4000, B=64,
+             L=4096, H=32, Hkv=4, D=64, sc=0.125, ws=None, wsb=0)
+    a.update(kw)
+    s, m = st("bn_gqa_decode", a["dt"], a["q"], a["k"], a["v"], a["lens"], a["o"], a["B"],
+              a["L"], a["H"], a["Hkv"], a["D"], a["sc"], a["ws"], a["wsb"], None)
+    assert s == status, m
+    assert m.startswith("GQA decode:")
+
+
+def test_decode_workspace_size():
+    L = B.lib()
+    n = L.bn_gqa_decode_workspace_size(64, 4096, 32, 64)
+    assert n == 64 * 32 * 32 * 66 * 4
+    assert L.bn_gqa_decode_workspace_size(64, 4096, 32, 128) == 0
+
+
+def test_pool_bookkeeping_without_device():
+    s = B.BnPoolStats()
+    B.call("bn_pool_get_stats", C.byref(s))
+    assert s.n_live == s.n_allocs - s.n_frees
+    # freeing a pointer the pool never handed out is an argument error
+    code, msg = st("bn_free", C.c_void_p(0x1234), None)
+    assert code == B.BN_ERR_INVALID_ARG and "not allocated" in msg
+    assert st("bn_free", None, None)[0] == B.BN_OK
+    assert st("bn_memcpy", None, C.c_void_p(8), 8, 0, None)[0] == B.BN_ERR_INVALID_ARG
+    assert st("bn_memcpy", C.c_void_p(8), C.c_void_p(8), 8, 7, None)[0] == B.BN_ERR_INVALID_ARG

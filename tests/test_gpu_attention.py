@@ -1,0 +1,181 @@
+"""GPU parity of the fused GQA prefill and KV-cache decode kernels.
+
+Small shapes are compared with the CPU oracle element for element (every
+head, every row); the BASELINE shapes (B=4, S=2048 prefill; B=64, L=4096
+decode) are checked on sampled (batch, head) pairs against the oracle and on
+size-independent properties (Q=0 gives prefix means of V; constant-per-head
+V exposes the GQA head mapping; decode equals the prefill's last row).
+Tolerances are the north star's: max relative error 1e-4 (fp32), 2e-2 (bf16).
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import bnhip as B
+from oracle import oracle as O
+from gpu_util import BF16_TOL, FP32_TOL, assert_close, bf16_round, dev, host, require_gpu
+
+pytestmark = pytest.mark.gpu
+TD = {"f32": torch.float32, "bf16": torch.bfloat16}
+TOL = {"f32": FP32_TOL, "bf16": BF16_TOL}
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    require_gpu()
+
+
+def draw(shape, seed, dtype):
+    a = np.random.default_rng(seed).standard_normal(shape).astype(np.float32)
+    return bf16_round(a) if dtype == "bf16" else a
+
+
+PREFILL_CASES = [
+    # B, Sq, Skv, H, Hkv, causal, off
+    (2, 128, 128, 8, 2, 1, 0),
+    (1, 200, 200, 32, 4, 1, 0),     # ragged last row tile, TinyLLaMA heads
+    (1, 64, 64, 4, 4, 0, 0),        # non-causal, no grouping
+    (1, 50, 250, 8, 1, 1, 200),     # query rows at the end of a longer key range
+    (2, 70, 70, 2, 1, 1, -5),       # negative offset: first rows see no key -> 0
+    (1, 1, 300, 8, 2, 1, 299),      # one query row (decode as prefill)
+    (3, 257, 257, 16, 4, 1, 0),
+    (1, 130, 90, 4, 2, 0, 0),       # non-causal, Skv not a multiple of 64
+]
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("case", PREFILL_CASES)
+def test_prefill_vs_oracle(case, dtype):
+    Bn, Sq, Skv, H, Hkv, causal, off = case
+    q = draw((Bn, Sq, H, 64), 1, dtype)
+    k = draw((Bn, Skv, Hkv, 64), 2, dtype)
+    v = draw((Bn, Skv, Hkv, 64), 3, dtype)
+    o = B.gqa_prefill(dev(q, TD[dtype]), dev(k, TD[dtype]), dev(v, TD[dtype]), scale=0.125,
+                      causal=bool(causal), seq_offset=off)
+    ref = O.gqa_prefill(q, k, v, 0.125, bool(causal), off)
+    got = host(o)
+    assert_close(got, ref, TOL[dtype], f"prefill {case} {dtype}")
+    if off < 0:  # rows with no visible key are exactly zero, as the reference's P @ V
+        assert np.all(got[:, :-off] == 0.0)
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_prefill_strided_rows(dtype):
+    # q/k/v as column slices of wider rows (e.g. a fused QKV projection output)
+    Bn, S, H, Hkv = 2, 96, 8, 2
+    qkv = draw((Bn, S, (H + 2 * Hkv) * 64), 4, dtype)
+    t = dev(qkv, TD[dtype])
+    q = t[:, :, :H * 64].unflatten(2, (H, 64))
+    k = t[:, :, H * 64:(H + Hkv) * 64].unflatten(2, (Hkv, 64))
+    v = t[:, :, (H + Hkv) * 64:].unflatten(2, (Hkv, 64))
+    o = B.gqa_prefill(q, k, v, scale=0.125)
+    qn = qkv[:, :, :H * 64].reshape(Bn, S, H, 64)
+    kn = qkv[:, :, H * 64:(H + Hkv) * 64].reshape(Bn, S, Hkv, 64)
+    vn = qkv[:, :, (H + Hkv) * 64:].reshape(Bn, S, Hkv, 64)
+    assert_close(host(o), O.gqa_prefill(qn, kn, vn, 0.125, True, 0), TOL[dtype])
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_prefill_head_mapping(dtype):
+    # V of KV head g is the constant g+1: query head h must return h//G + 1
+    Bn, S, H, Hkv = 1, 192, 32, 4
+    q = draw((Bn, S, H, 64), 5, dtype)
+    k = draw((Bn, S, Hkv, 64), 6, dtype)
+    v = np.broadcast_to(np.arange(1, Hkv + 1, dtype=np.float32)[None, None, :, None],
+                        (Bn, S, Hkv, 64)).copy()
+    got = host(B.gqa_prefill(dev(q, TD[dtype]), dev(k, TD[dtype]), dev(v, TD[dtype])))
+    for h in range(H):
+        want = h // (H // Hkv) + 1
+        np.testing.assert_array_equal(np.rint(got[0, :, h]), want)
+        assert np.max(np.abs(got[0, :, h] - want)) < (1e-5 if dtype == "f32" else 2e-2 * want)
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+def test_prefill_baseline_shape(dtype):
+    """B=4, S=2048, 32/4 heads, D=64, causal, scale 1/8."""
+    Bn, S, H, Hkv = 4, 2048, 32, 4
+    rngs = np.random.default_rng(0)
+    q = rngs.standard_normal((Bn, S, H, 64)).astype(np.float32)
+    k = rngs.standard_normal((Bn, S, Hkv, 64)).astype(np.float32)
+    v = rngs.standard_normal((Bn, S, Hkv, 64)).astype(np.float32)
+    if dtype == "bf16":
+        q, k, v = bf16_round(q), bf16_round(k), bf16_round(v)
+    got = host(B.gqa_prefill(dev(q, TD[dtype]), dev(k, TD[dtype]), dev(v, TD[dtype]),
+                             scale=0.125))
+    assert np.all(np.isfinite(got))
+    for b, h in [(0, 0), (3, 31), (1, 13)]:   # sampled heads, full length, every row
+        g = h // 8
+        ref = O.gqa_prefill(q[b:b + 1, :, h:h + 1], k[b:b + 1, :, g:g + 1],
+                            v[b:b + 1, :, g:g + 1], 0.125, True, 0)
+        assert_close(got[b:b + 1, :, h:h + 1], ref, TOL[dtype], f"b={b} h={h}")
+
+
+def test_prefill_zero_query_prefix_means():
+    # size-independent property at the full shape: Q = 0 -> row i is mean(V[0..i])
+    Bn, S, H, Hkv = 4, 2048, 32, 4
+    v = np.random.default_rng(7).standard_normal((Bn, S, Hkv, 64)).astype(np.float32)
+    k = np.random.default_rng(8).standard_normal((Bn, S, Hkv, 64)).astype(np.float32)
+    q = torch.zeros((Bn, S, H, 64), device="cuda")
+    got = host(B.gqa_prefill(q, dev(k), dev(v), scale=0.125))
+    means = np.cumsum(v.astype(np.float64), axis=1) / np.arange(1, S + 1)[None, :, None, None]
+    ref = np.repeat(means, H // Hkv, axis=2)
+    assert_close(got, ref, FP32_TOL, "prefix means")
+
+
+# ------------------------------------------------------------------- decode
+DECODE_CASES = [
+    # B, Lmax, H, Hkv, lens
+    (8, 1000, 32, 4, [1000, 1, 513, 64, 999, 2, 700, 128]),
+    (3, 300, 8, 8, [300, 17, 150]),
+    (5, 4096, 32, 4, [4096, 512, 3000, 1, 4095]),
+    (2, 77, 4, 2, [77, 40]),
+    (4, 256, 16, 4, [0, 256, 300, 5]),   # 0 -> zeros; above max_len -> clamped
+]
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("case", DECODE_CASES)
+def test_decode_vs_oracle(case, dtype):
+    Bn, L, H, Hkv, lens = case
+    q = draw((Bn, H, 64), 11, dtype)
+    kc = draw((Bn, L, Hkv, 64), 12, dtype)
+    vc = draw((Bn, L, Hkv, 64), 13, dtype)
+    lens = np.array(lens, np.int32)
+    got = host(B.gqa_decode(dev(q, TD[dtype]), dev(kc, TD[dtype]), dev(vc, TD[dtype]),
+                            torch.from_numpy(lens).cuda(), scale=0.125))
+    for b in range(Bn):
+        Lb = int(min(max(lens[b], 0), L))
+        if Lb == 0:
+            assert np.all(got[b] == 0.0)
+            continue
+        ref = O.gqa_decode(q[b:b + 1], kc[b:b + 1, :Lb], vc[b:b + 1, :Lb],
+                           np.array([Lb], np.int32), 0.125)
+        assert_close(got[b:b + 1], ref, TOL[dtype], f"decode b={b} len={Lb}")
+
+
+@pytest.mark.parametrize("ragged", [False, True])
+def test_decode_baseline_shape(ragged):
+    """B=64, bf16 cache of 4096, 32/4 heads; ragged lengths in [512, 4096]."""
+    Bn, L, H, Hkv = 64, 4096, 32, 4
+    r = np.random.default_rng(2)
+    lens = r.integers(512, 4097, Bn).astype(np.int32) if ragged else np.full(Bn, L, np.int32)
+    q = bf16_round(r.standard_normal((Bn, H, 64)).astype(np.float32))
+    kc = bf16_round(r.standard_normal((Bn, L, Hkv, 64)).astype(np.float32))
+    vc = bf16_round(r.standard_normal((Bn, L, Hkv, 64)).astype(np.float32))
+    qd, kd, vd = dev(q, torch.bfloat16), dev(kc, torch.bfloat16), dev(vc, torch.bfloat16)
+    ld = torch.from_numpy(lens).cuda()
+    ws = B.decode_workspace(Bn, L, H)
+    got = host(B.gqa_decode(qd, kd, vd, ld, scale=0.125, workspace=ws))
+    for b in (0, 17, 63):
+        Lb = int(lens[b])
+        ref = O.gqa_decode(q[b:b + 1], kc[b:b + 1, :Lb], vc[b:b + 1, :Lb],
+                           np.array([Lb], np.int32), 0.125)
+        assert_close(got[b:b + 1], ref, BF16_TOL, f"b={b}")
+    # decode == the last row of the (independent) prefill kernel, every sequence
+    for b in range(0, Bn, 9):
+        Lb = int(lens[b])
+        last = B.gqa_prefill(qd[b:b + 1, None], kd[b:b + 1, :Lb], vd[b:b + 1, :Lb],
+                             scale=0.125, causal=True, seq_offset=Lb - 1)
+        assert_close(got[b], host(last)[0, 0], BF16_TOL, f"decode vs prefill b={b}")

@@ -1,0 +1,221 @@
+"""GPU parity of the op-surface kernels (RMSNorm, RoPE, fused RMSNorm+RoPE,
+softmax, matmul, repeat_kv, elementwise, backward ops) against the CPU
+oracle, called through the C ABI on torch-allocated device buffers."""
+import ctypes as C
+
+import numpy as np
+import pytest
+import torch
+
+import bnhip as B
+from oracle import oracle as O
+from gpu_util import BF16_TOL, FP32_TOL, assert_close, bf16_round, dev, host, require_gpu
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    require_gpu()
+
+
+def rng(s):
+    return np.random.default_rng(s)
+
+
+def V(t):
+    return C.byref(B.view(t))
+
+
+S0 = None  # legacy default stream
+
+
+@pytest.mark.parametrize("rows,w,dtype", [(7, 2048, "f32"), (5, 300, "f32"), (64, 2048, "bf16"),
+                                          (3, 4096, "f32"), (2, 6000, "f32"), (1, 2048, "bf16")])
+def test_rmsnorm(rows, w, dtype):
+    r = rng(1)
+    x = r.standard_normal((rows, w)).astype(np.float32)
+    wt = r.standard_normal((1, w)).astype(np.float32)
+    td = torch.bfloat16 if dtype == "bf16" else torch.float32
+    if dtype == "bf16":
+        x, wt = bf16_round(x), bf16_round(wt)
+    xd, wd = dev(x, td), dev(wt, td)
+    yd = torch.empty_like(xd)
+    B.call("bn_rmsnorm", V(xd), V(wd), V(yd), 1e-5, S0)
+    assert_close(host(yd), O.rmsnorm(x, wt, 1e-5), BF16_TOL if dtype == "bf16" else FP32_TOL,
+                 "rmsnorm")
+
+
+def test_rmsnorm_strided_view():
+    r = rng(2)
+    big = r.standard_normal((10, 600)).astype(np.float32)
+    wt = r.standard_normal((1, 256)).astype(np.float32)
+    bd = dev(big)
+    xv = bd[2:9, 100:356]                       # column slice: strided rows
+    yd = torch.empty((7, 256), device="cuda")
+    B.call("bn_rmsnorm", V(xv), V(dev(wt)), V(yd), 1e-6, S0)
+    assert_close(host(yd), O.rmsnorm(big[2:9, 100:356], wt, 1e-6), FP32_TOL)
+
+
+@pytest.mark.parametrize("rows,w,D,off,dtype", [(16, 2048, 64, 0, "f32"), (3, 256, 64, 511, "f32"),
+                                                (4, 64, 32, 7, "f32"), (8, 2048, 64, 16383, "f32"),
+                                                (32, 2048, 64, 100, "bf16")])
+def test_rope(rows, w, D, off, dtype):
+    x = rng(3).standard_normal((rows, w)).astype(np.float32)
+    td = torch.bfloat16 if dtype == "bf16" else torch.float32
+    if dtype == "bf16":
+        x = bf16_round(x)
+    xd = dev(x, td)
+    yd = torch.empty_like(xd)
+    B.call("bn_rope", V(xd), V(yd), off, D, 1e4, S0)
+    ref = O.rope(x, off, D, 1e4)
+    assert_close(host(yd), ref, BF16_TOL if dtype == "bf16" else FP32_TOL, "rope")
+    back = torch.empty_like(xd)
+    B.call("bn_rope_backward", V(yd), V(back), off, D, 1e4, S0)
+    assert_close(host(back), O.rope_backward(host(yd), off, D, 1e4),
+                 BF16_TOL if dtype == "bf16" else FP32_TOL, "rope_back")
+
+
+def test_rope_transposed_view():
+    x = rng(4).standard_normal((128, 6)).astype(np.float32)   # stored transposed
+    xd = dev(x)
+    xt = xd.t()                                               # [6, 128] view, stride_w != 1
+    yd = torch.empty((6, 128), device="cuda")
+    B.call("bn_rope", V(xt), V(yd), 3, 64, 1e4, S0)
+    assert_close(host(yd), O.rope(np.ascontiguousarray(x.T), 3, 64, 1e4), FP32_TOL)
+
+
+@pytest.mark.parametrize("rows,w,off,dtype", [(32, 2048, 0, "f32"), (9, 2048, 77, "f32"),
+                                              (64, 2048, 1000, "bf16"), (5, 512, 3, "bf16"),
+                                              (3, 320, 0, "f32")])
+def test_rmsnorm_rope(rows, w, off, dtype):
+    r = rng(5)
+    x = r.standard_normal((rows, w)).astype(np.float32)
+    wt = (1 + 0.1 * r.standard_normal((1, w))).astype(np.float32)
+    td = torch.bfloat16 if dtype == "bf16" else torch.float32
+    if dtype == "bf16":
+        x, wt = bf16_round(x), bf16_round(wt)
+    xd, wd = dev(x, td), dev(wt, td)
+    yd = torch.empty_like(xd)
+    B.call("bn_rmsnorm_rope", V(xd), V(wd), V(yd), 1e-5, off, 64, 1e4, S0)
+    assert_close(host(yd), O.rmsnorm_rope(x, wt, 1e-5, off, 64, 1e4),
+                 BF16_TOL if dtype == "bf16" else FP32_TOL, "rmsnorm_rope")
+
+
+@pytest.mark.parametrize("rows,w,causal,off", [(33, 300, 1, 10), (8, 8, 1, 0), (16, 1000, 0, 0),
+                                               (4, 128, 1, -2), (1, 4096, 1, 4095)])
+def test_softmax(rows, w, causal, off):
+    x = (3 * rng(6).standard_normal((rows, w))).astype(np.float32)
+    xd = dev(x)
+    yd = torch.empty_like(xd)
+    B.call("bn_softmax", V(xd), V(yd), causal, off, S0)
+    got, ref = host(yd), O.softmax(x, causal, off)
+    assert_close(got, ref, FP32_TOL, "softmax")
+    np.testing.assert_array_equal(got == 0, ref == 0)   # masked entries exactly 0
+    dy = rng(7).standard_normal((rows, w)).astype(np.float32)
+    dx = torch.empty_like(xd)
+    B.call("bn_softmax_backward", V(yd), V(dev(dy)), V(dx), S0)
+    assert_close(host(dx), O.softmax_backward(ref, dy), 1e-3, "softmax_back")
+
+
+def test_softmax_known_answer():
+    xd = dev(np.array([[1, 2, 3, 4]], np.float32))   # test_llama.py:96
+    yd = torch.empty_like(xd)
+    B.call("bn_softmax", V(xd), V(yd), 0, 0, S0)
+    e = np.exp(np.arange(4) - 3.0)
+    np.testing.assert_allclose(host(yd)[0], e / e.sum(), rtol=1e-6)
+
+
+@pytest.mark.parametrize("m,k,n", [(70, 130, 50), (128, 2048, 256), (5, 7, 3), (256, 64, 256)])
+def test_matmul(m, k, n):
+    r = rng(8)
+    a = r.standard_normal((m, k)).astype(np.float32)
+    b = r.standard_normal((k, n)).astype(np.float32)
+    cd = torch.empty((m, n), device="cuda")
+    B.call("bn_matmul", V(dev(a)), V(dev(b)), V(cd), S0)
+    assert_close(host(cd), a.astype(np.float64) @ b, FP32_TOL, "matmul")
+    # B given as the transpose view of a [n, k] buffer (the key.T of the layers)
+    bt = dev(np.ascontiguousarray(b.T))
+    B.call("bn_matmul", V(dev(a)), V(bt.t()), V(cd), S0)
+    assert_close(host(cd), O.matmul(a, b), FP32_TOL, "matmul(T view)")
+
+
+def test_repeat_kv_exact():
+    kv = rng(9).standard_normal((33, 256)).astype(np.float32)
+    out = torch.empty((33, 2048), device="cuda")
+    B.call("bn_repeat_kv", V(dev(kv)), V(out), 64, 8, S0)
+    np.testing.assert_array_equal(host(out), O.repeat_kv(kv, 64, 8))
+
+
+def test_elementwise_surface():
+    r = rng(10)
+    a = r.standard_normal((6, 9)).astype(np.float32)
+    b = r.standard_normal((6, 9)).astype(np.float32)
+    row = r.standard_normal((1, 9)).astype(np.float32)
+    col = r.standard_normal((6, 1)).astype(np.float32)
+    ad = dev(a)
+    y = torch.empty_like(ad)
+    for op, f in [(B.BN_ADD, np.add), (B.BN_SUB, np.subtract), (B.BN_MUL, np.multiply)]:
+        for other in (b, row, col):
+            B.call("bn_binary", op, V(ad), V(dev(other)), V(y), S0)
+            np.testing.assert_array_equal(host(y), f(a, other).astype(np.float32))
+    eq = torch.empty((6, 9), dtype=torch.int32, device="cuda")
+    B.call("bn_binary", B.BN_EQ, V(ad), V(dev(np.where(a > 0, a, 0))), V(eq), S0)
+    np.testing.assert_array_equal(host(eq), (a > 0).astype(np.float32))
+    B.call("bn_unary", B.BN_RELU, V(ad), 0.0, V(y), S0)
+    np.testing.assert_array_equal(host(y), np.maximum(a, 0))
+    B.call("bn_unary", B.BN_MUL_SCALAR, V(ad), 0.125, V(y), S0)
+    np.testing.assert_array_equal(host(y), a * np.float32(0.125))
+    B.call("bn_unary", B.BN_SILU, V(ad), 0.0, V(y), S0)
+    np.testing.assert_allclose(host(y), a / (1 + np.exp(-a.astype(np.float64))), rtol=1e-5, atol=1e-6)
+    s0 = torch.empty((1, 9), device="cuda")
+    B.call("bn_sum", V(ad), V(s0), 0, S0)
+    np.testing.assert_allclose(host(s0), a.sum(0, keepdims=True), rtol=1e-5)
+    am = torch.empty((6, 1), dtype=torch.int32, device="cuda")
+    B.call("bn_argmax", V(ad), V(am), S0)
+    np.testing.assert_array_equal(host(am)[:, 0], a.argmax(1))
+    B.call("bn_fill", V(y), 2.5, S0)
+    assert np.all(host(y) == 2.5)
+
+
+def test_rmsnorm_backward():
+    r = rng(11)
+    x = r.standard_normal((6, 300)).astype(np.float32)
+    wt = r.standard_normal((1, 300)).astype(np.float32)
+    dy = r.standard_normal((6, 300)).astype(np.float32)
+    dx = torch.empty((6, 300), device="cuda")
+    dw = torch.full((1, 300), 5.0, device="cuda")   # overwritten, not accumulated into
+    B.call("bn_rmsnorm_backward", V(dev(x)), V(dev(wt)), V(dev(dy)), V(dx), V(dw), 1e-6, S0)
+    rdx, rdw = O.rmsnorm_backward(x, wt, dy, 1e-6)
+    assert_close(host(dx), rdx, FP32_TOL, "dx")
+    assert_close(host(dw), rdw, FP32_TOL, "dw")
+
+
+def test_pool_stream_ordered_alloc_free():
+    s0 = B.BnPoolStats()
+    B.call("bn_pool_get_stats", C.byref(s0))
+    ptrs = []
+    for n in (1 << 20, 3 << 20, 123):
+        p = C.c_void_p()
+        B.call("bn_alloc", C.byref(p), n, None)
+        ptrs.append(p)
+    s1 = B.BnPoolStats()
+    B.call("bn_pool_get_stats", C.byref(s1))
+    assert s1.bytes_in_use - s0.bytes_in_use == (1 << 20) + (3 << 20) + 123
+    assert s1.n_live == s0.n_live + 3 and s1.bytes_reserved >= s1.bytes_in_use
+    for p in ptrs:
+        B.call("bn_free", p, None)
+    B.call("bn_stream_synchronize", None)
+    s2 = B.BnPoolStats()
+    B.call("bn_pool_get_stats", C.byref(s2))
+    assert s2.bytes_in_use == s0.bytes_in_use and s2.n_live == s0.n_live
+    # the freed blocks stay cached in the pool (release threshold = never)
+    assert s2.bytes_reserved >= (4 << 20)
+    # injected limit -> BN_ERR_OOM, and the pool keeps working afterwards
+    B.call("bn_pool_set_limit", s2.bytes_in_use + 1000)
+    p = C.c_void_p()
+    code, msg = B.status_of("bn_alloc", C.byref(p), 4096, None)
+    assert code == B.BN_ERR_OOM and "limit" in msg
+    B.call("bn_pool_set_limit", 0)
+    B.call("bn_alloc", C.byref(p), 4096, None)
+    B.call("bn_free", p, None)
