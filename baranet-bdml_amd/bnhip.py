@@ -58,6 +58,10 @@ def lib():
         return _lib
     if not os.path.exists(LIB_PATH):
         raise RuntimeError(f"libbnhip.so not built ({LIB_PATH}); run __graft_entry__.build()")
+    try:  # share torch's HIP runtime when torch is present (one runtime per process)
+        import torch  # noqa: F401
+    except ImportError:
+        pass
     L = C.CDLL(LIB_PATH)
     vp, V = C.c_void_p, C.POINTER(BnView)
     i, f, i64, sz = C.c_int, C.c_float, C.c_int64, C.c_size_t

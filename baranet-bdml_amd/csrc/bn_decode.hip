@@ -220,6 +220,187 @@ __global__ __launch_bounds__(256) void decode_split_kernel(DecodeParams p) {
   }
 }
 
+// bf16 cache: matrix-core version.  Per wave, tiles of 32 keys:
+//   S^T[key][head] = K[key][:] . Q[head][:]   two v_mfma_f32_16x16x32_bf16 per
+//     16 keys; the K tile is the A operand straight from HBM (lane: key l%16,
+//     16 bytes of d), the G query heads are the B operand columns (padded to 16);
+//   online softmax per head column (4 keys per lane, 4 lane groups);
+//   O^T[d][head] += V^T[d][key] . P^T[key][head]  one MFMA per 16 d; V^T comes
+//     from a per-wave LDS tile written transposed, P^T straight from registers.
+// The next tile's K/V loads are issued before the current tile is computed.
+typedef __bf16 dbf16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 dbf16x4_t __attribute__((ext_vector_type(4)));
+typedef float df32x4_t __attribute__((ext_vector_type(4)));
+constexpr int TK = 32;   // keys per wave tile
+constexpr int VTP = 36;  // V^T LDS pitch (elements): conflict-free writes and b64 reads
+
+template <int G>
+__global__ __launch_bounds__(256) void decode_bf16_mfma_kernel(DecodeParams p) {
+  __shared__ __attribute__((aligned(16))) bf16_t Vt[4][HD * VTP];
+  __shared__ float red_m[4][G], red_l[4][G];
+  __shared__ float red_o[4][G][HD];
+
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int l16 = lane & 15, grp = lane >> 4;
+  const int split = blockIdx.x % p.n_split;
+  const int bg = blockIdx.x / p.n_split;
+  const int b = bg / p.n_kv_heads, g = bg % p.n_kv_heads;
+
+  int len = p.lens[b];
+  len = len < 0 ? 0 : (len > p.max_len ? p.max_len : len);
+  const int k_begin = split * p.chunk;
+  if (k_begin >= len) return;  // the combine kernel ignores chunks past len
+  const int k_end = min(k_begin + p.chunk, len);
+  const int ntiles = (k_end - k_begin + TK - 1) / TK;
+
+  const int64_t kv_rs = (int64_t)p.n_kv_heads * HD;
+  const bf16_t *Kb = (const bf16_t *)p.k + (int64_t)b * p.max_len * kv_rs + (int64_t)g * HD + 8 * grp;
+  const bf16_t *Vb = (const bf16_t *)p.v + (int64_t)b * p.max_len * kv_rs + (int64_t)g * HD + 8 * grp;
+
+  // B operand of S^T: column l16 = query head g*G + l16 (zero past G), d = 8grp + 32t + 0..7
+  dbf16x8_t qb[2];
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    if (l16 < G)
+      qb[t] = *(const dbf16x8_t *)((const bf16_t *)p.q +
+                                   ((int64_t)b * p.n_heads + g * G + l16) * HD + 8 * grp + 32 * t);
+    else
+      qb[t] = dbf16x8_t{};
+  }
+
+  uint4 kr[2][2], vr[2][2];  // [16-key half u][d half t], this lane: key 16u + l16
+  auto gload = [&](int kb) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int key = kb + 16 * u + l16;
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        if (key < k_end) {
+          kr[u][t] = *(const uint4 *)(Kb + (int64_t)key * kv_rs + 32 * t);
+          vr[u][t] = *(const uint4 *)(Vb + (int64_t)key * kv_rs + 32 * t);
+        } else {  // zeros: a masked key must not bring NaN/Inf into P.V
+          kr[u][t] = make_uint4(0, 0, 0, 0);
+          vr[u][t] = make_uint4(0, 0, 0, 0);
+        }
+      }
+    }
+  };
+
+  float m = -INFINITY, l = 0.f;
+  df32x4_t o[4] = {df32x4_t{}, df32x4_t{}, df32x4_t{}, df32x4_t{}};
+  bf16_t *vt = Vt[wave];
+  const float c = p.c;
+
+  if (wave < ntiles) gload(k_begin + TK * wave);
+  for (int ti = wave; ti < ntiles; ti += 4) {
+    const int kb = k_begin + TK * ti;
+    uint4 kc[2][2], vc[2][2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        kc[u][t] = kr[u][t];
+        vc[u][t] = vr[u][t];
+      }
+    if (ti + 4 < ntiles) gload(kb + 4 * TK);
+
+    // V tile -> LDS, transposed: vt[d][key], d = 8grp + 32t + e, key = 16u + l16.
+    // The tile is private to this wave; LDS operations of a wave complete in order.
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const uint32_t w4[4] = {vc[u][t].x, vc[u][t].y, vc[u][t].z, vc[u][t].w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          vt[(8 * grp + 32 * t + 2 * e) * VTP + 16 * u + l16] = (bf16_t)(w4[e] & 0xffffu);
+          vt[(8 * grp + 32 * t + 2 * e + 1) * VTP + 16 * u + l16] = (bf16_t)(w4[e] >> 16);
+        }
+      }
+
+    // S^T: s[u][i] = key kb + 16u + 4grp + i, head column l16
+    df32x4_t s[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      s[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(dbf16x8_t, kc[u][0]),
+                                                     qb[0], df32x4_t{}, 0, 0, 0);
+      s[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(dbf16x8_t, kc[u][1]),
+                                                     qb[1], s[u], 0, 0, 0);
+    }
+    if (kb + TK > k_end) {
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (kb + 16 * u + 4 * grp + i >= k_end) s[u][i] = -INFINITY;
+    }
+    float mx = fmaxf(fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3])),
+                     fmaxf(fmaxf(s[1][0], s[1][1]), fmaxf(s[1][2], s[1][3])));
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float m_new = fmaxf(m, mx);
+    const float m_use = m_new == -INFINITY ? 0.f : m_new;
+    const float mc = m_use * c;
+    const float alpha = __builtin_amdgcn_exp2f(m * c - mc);
+    float rs = 0.f;
+    dbf16x8_t pb;
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float e = __builtin_amdgcn_exp2f(fmaf(s[u][i], c, -mc));
+        rs += e;
+        pb[4 * u + i] = (__bf16)e;  // k-slot (grp, 4u+i) = key 16u + 4grp + i
+      }
+    l = l * alpha + rs;  // this lane group's keys; groups are summed at the end
+    m = m_new;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+      o[dt] *= alpha;
+      const bf16_t *row = vt + (16 * dt + l16) * VTP + 4 * grp;
+      const dbf16x4_t lo = *(const dbf16x4_t *)(row);       // keys 4grp .. +3
+      const dbf16x4_t hi = *(const dbf16x4_t *)(row + 16);  // keys 16 + 4grp .. +3
+      const dbf16x8_t a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb, o[dt], 0, 0, 0);
+    }
+  }
+
+  // o[dt][i] = O^T[d = 16dt + 4grp + i][head l16]; m is uniform over lane groups
+  l += __shfl_xor(l, 16, 64);
+  l += __shfl_xor(l, 32, 64);
+  if (l16 < G) {
+    if (grp == 0) {
+      red_m[wave][l16] = m;
+      red_l[wave][l16] = l;
+    }
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) red_o[wave][l16][16 * dt + 4 * grp + i] = o[dt][i];
+  }
+  __syncthreads();
+  for (int idx = tid; idx < G * HD; idx += 256) {
+    const int h = idx / HD, d = idx % HD;
+    float M = red_m[0][h];
+#pragma unroll
+    for (int w2 = 1; w2 < 4; ++w2) M = fmaxf(M, red_m[w2][h]);
+    const float Mu = M == -INFINITY ? 0.f : M;
+    float L = 0.f, A = 0.f;
+#pragma unroll
+    for (int w2 = 0; w2 < 4; ++w2) {
+      const float f = __builtin_amdgcn_exp2f((red_m[w2][h] - Mu) * c);
+      L += red_l[w2][h] * f;
+      A += red_o[w2][h][d] * f;
+    }
+    float *part = p.ws + (((int64_t)b * p.n_heads + g * G + h) * p.n_split + split) * (HD + 2);
+    part[2 + d] = A;
+    if (d == 0) {
+      part[0] = M * c;  // partials carry the max in the log2 domain
+      part[1] = L;
+    }
+  }
+}
+
 // One thread per (b, head, d): merge the chunks [0, ceil(len/chunk)).
 template <typename T>
 __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeParams p) {
@@ -255,14 +436,22 @@ int choose_chunk(int batch, int max_len, int n_kv_heads) {
   return chunk;
 }
 
+template <typename T, int G>
+void launch_split(const DecodeParams &p, dim3 grid, hipStream_t s) {
+  if constexpr (std::is_same<T, bf16_t>::value)
+    hipLaunchKernelGGL((decode_bf16_mfma_kernel<G>), grid, dim3(256), 0, s, p);
+  else
+    hipLaunchKernelGGL((decode_split_kernel<T, G>), grid, dim3(256), 0, s, p);
+}
+
 template <typename T>
 int launch_decode(const DecodeParams &p, int G, hipStream_t s) {
-  const int64_t nwg = (int64_t)p.batch * p.n_kv_heads * p.n_split;
+  const dim3 grid((unsigned)((int64_t)p.batch * p.n_kv_heads * p.n_split));
   switch (G) {
-    case 1: hipLaunchKernelGGL((decode_split_kernel<T, 1>), dim3((unsigned)nwg), dim3(256), 0, s, p); break;
-    case 2: hipLaunchKernelGGL((decode_split_kernel<T, 2>), dim3((unsigned)nwg), dim3(256), 0, s, p); break;
-    case 4: hipLaunchKernelGGL((decode_split_kernel<T, 4>), dim3((unsigned)nwg), dim3(256), 0, s, p); break;
-    default: hipLaunchKernelGGL((decode_split_kernel<T, 8>), dim3((unsigned)nwg), dim3(256), 0, s, p); break;
+    case 1: launch_split<T, 1>(p, grid, s); break;
+    case 2: launch_split<T, 2>(p, grid, s); break;
+    case 4: launch_split<T, 4>(p, grid, s); break;
+    default: launch_split<T, 8>(p, grid, s); break;
   }
   BN_LAUNCH_CHECK();
   const int64_t n = (int64_t)p.batch * p.n_heads * HD;

@@ -8,6 +8,10 @@ import sys
 
 import pytest
 
+# PyTorch-ROCm ships its own HIP runtime.  Loading torch before anything that
+# links the system libamdhip64 (bten, libbnhip) keeps one runtime per process.
+import torch  # noqa: F401
+
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 PKG = os.path.join(ROOT, "baranet-bdml_amd")
 for p in (ROOT, PKG):
