@@ -141,6 +141,19 @@ def bench_rmsnorm_rope(steps, warmup):
             "bytes_per_launch": nb, "roofline": roofline("hbm", gbs, PEAK_HBM_GBS, "GB/s")}
 
 
+def bench_copy(steps, warmup):
+    """Plain device copy of a known size: the calibration point that turns the
+    FETCH_SIZE / WRITE_SIZE counters into HBM bytes (bytes per launch known)."""
+    import torch
+    n = 64 << 20  # 64 Mi fp32 = 256 MiB read + 256 MiB written per launch
+    xs = [torch.ones(n, device="cuda") for _ in range(2)]
+    y = torch.empty(n, device="cuda")
+    ms = time_launches(lambda i: y.copy_(xs[i % 2]), steps, warmup)
+    nb = 2 * 4 * n
+    return {"value": round(nb / (ms * 1e-3) / 1e9, 2), "unit": "GB/s",
+            "ms_per_launch": round(ms, 5), "bytes_read": 4 * n, "bytes_written": 4 * n}
+
+
 def cpu_baseline_prefill(budget_s=12.0):
     """CPU oracle (single thread) on whole (batch, head) pairs of config 2."""
     import numpy as np
@@ -187,7 +200,9 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
-    ap.add_argument("--only", default="", help="comma list: prefill,decode,fp32,norm,long")
+    ap.add_argument("--only", default="",
+                    help="comma list of extra workloads (default: all but copy): "
+                         "decode,ragged,fp32,norm,long,copy; 'head' = headline prefill only")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
@@ -215,8 +230,10 @@ def main():
           flush=True)
     if want("decode"):
         out["decode"] = bench_decode(False, K, W)
-        out["decode_ragged"] = bench_decode(True, K, W)
         print(f"decode: {out['decode']['value']} GB/s", file=sys.stderr, flush=True)
+    if want("ragged"):
+        out["decode_ragged"] = bench_decode(True, K, W)
+        print(f"decode ragged: {out['decode_ragged']['value']} GB/s", file=sys.stderr, flush=True)
     if want("fp32"):
         out["prefill_fp32"] = bench_prefill(4, 2048, 32, 4, "fp32", max(K // 2, 3), 2)
         print(f"prefill fp32: {out['prefill_fp32']['value']} TFLOP/s", file=sys.stderr, flush=True)
@@ -227,6 +244,9 @@ def main():
         out["prefill_long"] = bench_prefill(1, 16384, 32, 4, "bf16", max(K // 4, 3), 1)
         print(f"prefill S=16384: {out['prefill_long']['value']} TFLOP/s", file=sys.stderr,
               flush=True)
+    if "copy" in only:
+        out["copy"] = bench_copy(K, W)
+        print(f"copy: {out['copy']['value']} GB/s", file=sys.stderr, flush=True)
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline_prefill()
         if "decode" in out:
