@@ -63,6 +63,17 @@ def time_launches(fn, steps, warmup):
     return s.elapsed_time(e) / steps
 
 
+def measured_traffic(key):
+    """HBM bytes per launch of the workload's dominant kernel, from the
+    calibrated FETCH_SIZE + WRITE_SIZE counter passes kept in
+    profiles/traffic.json (rocprofv3 cannot run inside this process)."""
+    try:
+        with open(os.path.join(ROOT, "profiles", "traffic.json")) as f:
+            return json.load(f)[key]["total"]
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def roofline(bound, achieved, peak, unit, traffic=None):
     return {"bound": bound, "achieved": round(achieved, 3), "peak": peak, "unit": unit,
             "frac": round(achieved / peak, 4), "traffic": traffic}
@@ -83,7 +94,9 @@ def bench_prefill(B_, S, H, Hkv, dtype, steps, warmup, seed=0):
     peak = PEAK_BF16_TFLOPS if dtype == "bf16" else PEAK_FP32_TFLOPS
     return {"value": round(tflops, 3), "unit": "TFLOP/s", "ms_per_launch": round(ms, 5),
             "flops_per_launch": fl,
-            "roofline": roofline("mfma", tflops, peak, "TFLOP/s")}
+            "roofline": roofline("mfma", tflops, peak, "TFLOP/s",
+                                 measured_traffic("prefill_bf16") if (dtype == "bf16" and S == 2048)
+                                 else None)}
 
 
 def bench_decode(ragged, steps, warmup, seed=2):
@@ -113,7 +126,8 @@ def bench_decode(ragged, steps, warmup, seed=2):
     return {"value": round(gbs, 2), "unit": "GB/s", "ms_per_launch": round(ms, 5),
             "bytes_per_launch": nb, "lengths": "uniform 4096" if not ragged else
             f"ragged U[512,4096] seed {seed}, sum {int(lens.sum())}",
-            "roofline": roofline("hbm", gbs, PEAK_HBM_GBS, "GB/s")}
+            "roofline": roofline("hbm", gbs, PEAK_HBM_GBS, "GB/s",
+                                 measured_traffic("decode_ragged" if ragged else "decode"))}
 
 
 def bench_rmsnorm_rope(steps, warmup):
@@ -138,7 +152,8 @@ def bench_rmsnorm_rope(steps, warmup):
     nb = 2 * rows * w * 2 + w * 2
     gbs = nb / (ms * 1e-3) / 1e9
     return {"value": round(gbs, 2), "unit": "GB/s", "ms_per_launch": round(ms, 5),
-            "bytes_per_launch": nb, "roofline": roofline("hbm", gbs, PEAK_HBM_GBS, "GB/s")}
+            "bytes_per_launch": nb,
+            "roofline": roofline("hbm", gbs, PEAK_HBM_GBS, "GB/s", measured_traffic("rmsnorm_rope"))}
 
 
 def bench_copy(steps, warmup):
