@@ -234,17 +234,38 @@ typedef float df32x4_t __attribute__((ext_vector_type(4)));
 constexpr int TK = 32;   // keys per wave tile
 constexpr int VTP = 36;  // V^T LDS pitch (elements): conflict-free writes and b64 reads
 
+#ifndef BN_DECODE_G_FASTEST
+#define BN_DECODE_G_FASTEST 0
+#endif
+#ifndef BN_DECODE_NBUF
+#define BN_DECODE_NBUF 2
+#endif
+constexpr int NBUF = BN_DECODE_NBUF;
+#ifndef BN_DECODE_WAVES_PER_EU
+#define BN_DECODE_WAVES_PER_EU 3
+#endif
 template <int G>
-__global__ __launch_bounds__(256) void decode_bf16_mfma_kernel(DecodeParams p) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(BN_DECODE_WAVES_PER_EU)))
+void decode_bf16_mfma_kernel(DecodeParams p) {
+  // per-wave V^T tile; after the wave's last tile the same bytes hold its
+  // (acc) merge values, so the workgroup needs no second LDS array
   __shared__ __attribute__((aligned(16))) bf16_t Vt[4][HD * VTP];
   __shared__ float red_m[4][G], red_l[4][G];
-  __shared__ float red_o[4][G][HD];
+  static_assert(G * HD * sizeof(float) <= HD * VTP * sizeof(bf16_t), "merge area");
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int l16 = lane & 15, grp = lane >> 4;
+#if BN_DECODE_G_FASTEST
+  // the n_kv_heads workgroups of one (sequence, chunk) are dispatched together:
+  // together they stream whole 512-byte cache rows
+  const int g = blockIdx.x % p.n_kv_heads;
+  const int bs = blockIdx.x / p.n_kv_heads;
+  const int b = bs / p.n_split, split = bs % p.n_split;
+#else
   const int split = blockIdx.x % p.n_split;
   const int bg = blockIdx.x / p.n_split;
   const int b = bg / p.n_kv_heads, g = bg % p.n_kv_heads;
+#endif
 
   int len = p.lens[b];
   len = len < 0 ? 0 : (len > p.max_len ? p.max_len : len);
@@ -268,20 +289,21 @@ __global__ __launch_bounds__(256) void decode_bf16_mfma_kernel(DecodeParams p) {
       qb[t] = dbf16x8_t{};
   }
 
-  uint4 kr[2][2], vr[2][2];  // [16-key half u][d half t], this lane: key 16u + l16
-  auto gload = [&](int kb) {
+  // NBUF register tile buffers used in turn: while one tile is computed, the
+  // loads of the other NBUF-1 (and the refill of this one) are in flight
+  uint4 kr[NBUF][2][2], vr[NBUF][2][2];  // [buffer][16-key half u][d half t]; lane: key 16u + l16
+  // Branch-free loads: a key past the end reads the last valid key instead
+  // (its score is masked to -inf, so P = 0 multiplies finite cache data).  A
+  // conditional load would make the compiler wait for every outstanding load
+  // at the first use, serialising the two buffers.
+  auto gload = [&](int buf, int kb) {
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
-      const int key = kb + 16 * u + l16;
+      const int key = min(kb + 16 * u + l16, k_end - 1);
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
-        if (key < k_end) {
-          kr[u][t] = *(const uint4 *)(Kb + (int64_t)key * kv_rs + 32 * t);
-          vr[u][t] = *(const uint4 *)(Vb + (int64_t)key * kv_rs + 32 * t);
-        } else {  // zeros: a masked key must not bring NaN/Inf into P.V
-          kr[u][t] = make_uint4(0, 0, 0, 0);
-          vr[u][t] = make_uint4(0, 0, 0, 0);
-        }
+        kr[buf][u][t] = *(const uint4 *)(Kb + (int64_t)key * kv_rs + 32 * t);
+        vr[buf][u][t] = *(const uint4 *)(Vb + (int64_t)key * kv_rs + 32 * t);
       }
     }
   };
@@ -291,40 +313,28 @@ __global__ __launch_bounds__(256) void decode_bf16_mfma_kernel(DecodeParams p) {
   bf16_t *vt = Vt[wave];
   const float c = p.c;
 
-  if (wave < ntiles) gload(k_begin + TK * wave);
-  for (int ti = wave; ti < ntiles; ti += 4) {
-    const int kb = k_begin + TK * ti;
-    uint4 kc[2][2], vc[2][2];
-#pragma unroll
-    for (int u = 0; u < 2; ++u)
-#pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        kc[u][t] = kr[u][t];
-        vc[u][t] = vr[u][t];
-      }
-    if (ti + 4 < ntiles) gload(kb + 4 * TK);
-
+  auto compute = [&](int buf, int kb) {
     // V tile -> LDS, transposed: vt[d][key], d = 8grp + 32t + e, key = 16u + l16.
     // The tile is private to this wave; LDS operations of a wave complete in order.
 #pragma unroll
     for (int u = 0; u < 2; ++u)
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
-        const uint32_t w4[4] = {vc[u][t].x, vc[u][t].y, vc[u][t].z, vc[u][t].w};
+        const uint4 vv = vr[buf][u][t];
+        const uint32_t w4[4] = {vv.x, vv.y, vv.z, vv.w};
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           vt[(8 * grp + 32 * t + 2 * e) * VTP + 16 * u + l16] = (bf16_t)(w4[e] & 0xffffu);
           vt[(8 * grp + 32 * t + 2 * e + 1) * VTP + 16 * u + l16] = (bf16_t)(w4[e] >> 16);
         }
       }
-
     // S^T: s[u][i] = key kb + 16u + 4grp + i, head column l16
     df32x4_t s[2];
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
-      s[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(dbf16x8_t, kc[u][0]),
+      s[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(dbf16x8_t, kr[buf][u][0]),
                                                      qb[0], df32x4_t{}, 0, 0, 0);
-      s[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(dbf16x8_t, kc[u][1]),
+      s[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(dbf16x8_t, kr[buf][u][1]),
                                                      qb[1], s[u], 0, 0, 0);
     }
     if (kb + TK > k_end) {
@@ -363,11 +373,28 @@ __global__ __launch_bounds__(256) void decode_bf16_mfma_kernel(DecodeParams p) {
       const dbf16x8_t a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
       o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb, o[dt], 0, 0, 0);
     }
+  };
+
+  // This wave's tiles: wave, wave+4, wave+8, ... (the workgroup walks the chunk
+  // front to back).  Every gload is unconditional, with the tile index clamped
+  // to the last tile (a repeated tile is an L2 hit): the same number of loads
+  // is then in flight on every path, and the compiler waits for one buffer
+  // only (vmcnt(8)) instead of draining both.
+  auto tile_kb = [&](int ti) { return k_begin + TK * min(ti, ntiles - 1); };
+#pragma unroll
+  for (int j = 0; j < NBUF; ++j) gload(j, tile_kb(wave + 4 * j));
+  for (int ti = wave; ti < ntiles; ti += 4 * NBUF) {
+#pragma unroll
+    for (int j = 0; j < NBUF; ++j) {
+      if (ti + 4 * j < ntiles) compute(j, k_begin + TK * (ti + 4 * j));
+      gload(j, tile_kb(ti + 4 * j + 4 * NBUF));
+    }
   }
 
   // o[dt][i] = O^T[d = 16dt + 4grp + i][head l16]; m is uniform over lane groups
   l += __shfl_xor(l, 16, 64);
   l += __shfl_xor(l, 32, 64);
+  float *red_o = reinterpret_cast<float *>(vt);  // [G][HD], this wave's V^T tile is done
   if (l16 < G) {
     if (grp == 0) {
       red_m[wave][l16] = m;
@@ -376,7 +403,7 @@ __global__ __launch_bounds__(256) void decode_bf16_mfma_kernel(DecodeParams p) {
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) red_o[wave][l16][16 * dt + 4 * grp + i] = o[dt][i];
+      for (int i = 0; i < 4; ++i) red_o[l16 * HD + 16 * dt + 4 * grp + i] = o[dt][i];
   }
   __syncthreads();
   for (int idx = tid; idx < G * HD; idx += 256) {
@@ -390,7 +417,7 @@ __global__ __launch_bounds__(256) void decode_bf16_mfma_kernel(DecodeParams p) {
     for (int w2 = 0; w2 < 4; ++w2) {
       const float f = __builtin_amdgcn_exp2f((red_m[w2][h] - Mu) * c);
       L += red_l[w2][h] * f;
-      A += red_o[w2][h][d] * f;
+      A += reinterpret_cast<const float *>(Vt[w2])[h * HD + d] * f;
     }
     float *part = p.ws + (((int64_t)b * p.n_heads + g * G + h) * p.n_split + split) * (HD + 2);
     part[2 + d] = A;
@@ -401,7 +428,185 @@ __global__ __launch_bounds__(256) void decode_bf16_mfma_kernel(DecodeParams p) {
   }
 }
 
-// One thread per (b, head, d): merge the chunks [0, ceil(len/chunk)).
+// bf16 cache, n_kv_heads a multiple of 4: whole-row streaming version.
+// A workgroup = (sequence, 4 consecutive KV heads, chunk).  Its 256 threads
+// load each 32-key tile as contiguous 16-byte chunks of the cache rows (one
+// load instruction covers 1 KB: two token rows of the 4 heads), which
+// streams HBM far better than per-head 64-byte pieces, into registers two
+// tiles ahead, then write it row-major to LDS.  Wave w is KV head g0 + w:
+// K fragments come from LDS with ds_read_b128, V^T fragments with the gfx950
+// transpose read ds_read_b64_tr_b16, and the wave writes its own partials.
+typedef short ds4_t __attribute__((ext_vector_type(4)));
+#ifndef BN_DECODE_ROWS_WAVES
+#define BN_DECODE_ROWS_WAVES 2
+#endif
+constexpr int RKP = 4 * HD + 8;   // K tile row pitch (elements): 528 B, 16 rows hit 64 distinct banks
+constexpr int RVP = 4 * HD + 16;  // V tile row pitch: 544 B, 4 rows x 32 B transpose reads conflict-free
+constexpr int RCH = TK * 4 * HD * 2 / 16 / 256;  // 16-byte chunks per thread per array per tile
+
+__device__ __forceinline__ dbf16x4_t lds_read_tr16(const bf16_t *p) {
+  const ds4_t r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) ds4_t *)(__attribute__((address_space(3))) void *)p);
+  return __builtin_bit_cast(dbf16x4_t, r);
+}
+
+template <int G>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(BN_DECODE_ROWS_WAVES))) void decode_bf16_rows_kernel(DecodeParams p) {
+  __shared__ __attribute__((aligned(16))) bf16_t KL[TK * RKP];
+  __shared__ __attribute__((aligned(16))) bf16_t VL[TK * RVP];
+
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int l16 = lane & 15, grp = lane >> 4;
+  const int hblocks = p.n_kv_heads >> 2;
+  const int split = blockIdx.x % p.n_split;
+  const int bh = blockIdx.x / p.n_split;
+  const int b = bh / hblocks, g0 = (bh % hblocks) * 4;
+  const int g = g0 + wave;
+
+  int len = p.lens[b];
+  len = len < 0 ? 0 : (len > p.max_len ? p.max_len : len);
+  const int k_begin = split * p.chunk;
+  if (k_begin >= len) return;  // the combine kernel ignores chunks past len
+  const int k_end = min(k_begin + p.chunk, len);
+  const int ntiles = (k_end - k_begin + TK - 1) / TK;
+
+  const int64_t kv_rs = (int64_t)p.n_kv_heads * HD;
+  const bf16_t *Kr = (const bf16_t *)p.k + (int64_t)b * p.max_len * kv_rs + (int64_t)g0 * HD;
+  const bf16_t *Vr = (const bf16_t *)p.v + (int64_t)b * p.max_len * kv_rs + (int64_t)g0 * HD;
+
+  dbf16x8_t qb[2];
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    if (l16 < G)
+      qb[t] = *(const dbf16x8_t *)((const bf16_t *)p.q +
+                                   ((int64_t)b * p.n_heads + g * G + l16) * HD + 8 * grp + 32 * t);
+    else
+      qb[t] = dbf16x8_t{};
+  }
+
+  // chunk c = tid + 256*i of a tile: row c / 32 (key), column (c % 32) * 8 elements.
+  // Two register tiles (A, B) hold the next two tiles' K and V chunks.
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));  // native vector: stays in VGPRs
+  struct RegTile {
+    u32x4 k0, k1, k2, k3, v0, v1, v2, v3;
+  };
+  static_assert(RCH == 4, "register tile holds 4 chunks per array");
+  const int crow = tid >> 5, ccol = (tid & 31) * 8;  // chunk i adds 8 rows
+  auto gload = [&](RegTile &r, int ti) __attribute__((always_inline)) {
+    const int kb = k_begin + TK * min(ti, ntiles - 1);  // clamped: same load count on every path
+    const int last = k_end - 1;  // past the end: a valid row, masked to P = 0
+    const int64_t o0 = (int64_t)min(kb + crow, last) * kv_rs + ccol;
+    const int64_t o1 = (int64_t)min(kb + crow + 8, last) * kv_rs + ccol;
+    const int64_t o2 = (int64_t)min(kb + crow + 16, last) * kv_rs + ccol;
+    const int64_t o3 = (int64_t)min(kb + crow + 24, last) * kv_rs + ccol;
+    r.k0 = *(const u32x4 *)(Kr + o0); r.v0 = *(const u32x4 *)(Vr + o0);
+    r.k1 = *(const u32x4 *)(Kr + o1); r.v1 = *(const u32x4 *)(Vr + o1);
+    r.k2 = *(const u32x4 *)(Kr + o2); r.v2 = *(const u32x4 *)(Vr + o2);
+    r.k3 = *(const u32x4 *)(Kr + o3); r.v3 = *(const u32x4 *)(Vr + o3);
+  };
+  auto lstore = [&](const RegTile &r) __attribute__((always_inline)) {
+    *(u32x4 *)(KL + crow * RKP + ccol) = r.k0;
+    *(u32x4 *)(KL + (crow + 8) * RKP + ccol) = r.k1;
+    *(u32x4 *)(KL + (crow + 16) * RKP + ccol) = r.k2;
+    *(u32x4 *)(KL + (crow + 24) * RKP + ccol) = r.k3;
+    *(u32x4 *)(VL + crow * RVP + ccol) = r.v0;
+    *(u32x4 *)(VL + (crow + 8) * RVP + ccol) = r.v1;
+    *(u32x4 *)(VL + (crow + 16) * RVP + ccol) = r.v2;
+    *(u32x4 *)(VL + (crow + 24) * RVP + ccol) = r.v3;
+  };
+  RegTile ta, tb;
+
+  float m = -INFINITY, l = 0.f;
+  df32x4_t o[4] = {df32x4_t{}, df32x4_t{}, df32x4_t{}, df32x4_t{}};
+  const float c = p.c;
+  const bf16_t *kl = KL + wave * HD + 8 * grp;  // this wave's head inside the tile
+  const bf16_t *vl = VL + wave * HD;
+
+  auto compute = [&](int kb) __attribute__((always_inline)) {
+    df32x4_t s[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const bf16_t *kp = kl + (16 * u + l16) * RKP;
+      s[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*(const dbf16x8_t *)(kp), qb[0], df32x4_t{},
+                                                     0, 0, 0);
+      s[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*(const dbf16x8_t *)(kp + 32), qb[1], s[u],
+                                                     0, 0, 0);
+    }
+    if (kb + TK > k_end) {
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (kb + 16 * u + 4 * grp + i >= k_end) s[u][i] = -INFINITY;
+    }
+    float mx = fmaxf(fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3])),
+                     fmaxf(fmaxf(s[1][0], s[1][1]), fmaxf(s[1][2], s[1][3])));
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float m_new = fmaxf(m, mx);
+    const float m_use = m_new == -INFINITY ? 0.f : m_new;
+    const float mc = m_use * c;
+    const float alpha = __builtin_amdgcn_exp2f(m * c - mc);
+    float rs = 0.f;
+    dbf16x8_t pb;
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float e = __builtin_amdgcn_exp2f(fmaf(s[u][i], c, -mc));
+        rs += e;
+        pb[4 * u + i] = (__bf16)e;  // k-slot (grp, 4u+i) = key 16u + 4grp + i
+      }
+    l = l * alpha + rs;
+    m = m_new;
+    // V^T operand: slot j of lane (grp, l16) = V[key 16(j/4) + 4grp + j%4][16dt + l16];
+    // transpose read: local lane n supplies V[key 4grp + n/4 (+16)][16dt + 4(n%4) .. +3]
+    const bf16_t *vp = vl + (4 * grp + (l16 >> 2)) * RVP + 4 * (l16 & 3);
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+      o[dt] *= alpha;
+      const dbf16x4_t lo = lds_read_tr16(vp + 16 * dt);
+      const dbf16x4_t hi = lds_read_tr16(vp + 16 * RVP + 16 * dt);
+      const dbf16x8_t a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb, o[dt], 0, 0, 0);
+    }
+  };
+
+  gload(ta, 0);
+  gload(tb, 1);
+  for (int ti = 0; ti < ntiles; ti += 2) {
+    __syncthreads();  // every wave is done with the previous tile
+    lstore(ta);
+    __syncthreads();
+    gload(ta, ti + 2);
+    compute(k_begin + TK * ti);
+    if (ti + 1 < ntiles) {  // workgroup-uniform
+      __syncthreads();
+      lstore(tb);
+      __syncthreads();
+      compute(k_begin + TK * (ti + 1));
+    }
+    gload(tb, ti + 3);
+  }
+
+  // o[dt][i] = O^T[d = 16dt + 4grp + i][query head g*G + l16]; m is uniform over lane groups
+  l += __shfl_xor(l, 16, 64);
+  l += __shfl_xor(l, 32, 64);
+  if (l16 < G) {
+    float *part = p.ws + (((int64_t)b * p.n_heads + g * G + l16) * p.n_split + split) * (HD + 2);
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) part[2 + 16 * dt + 4 * grp + i] = o[dt][i];
+    if (grp == 0) {
+      part[0] = m * c;  // log2 domain, as the other split kernels
+      part[1] = l;
+    }
+  }
+}
+
+// One thread per (b, head, d): merge the chunks [0, ceil(len/chunk)) in one
+// pass (running log-sum-exp), four chunks' loads in flight at a time.
 template <typename T>
 __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeParams p) {
   const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -413,40 +618,77 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeParams p) {
   len = len < 0 ? 0 : (len > p.max_len ? p.max_len : len);
   const int nvalid = (len + p.chunk - 1) / p.chunk;
   const float *part = p.ws + bh * p.n_split * (HD + 2);
-  float M = -INFINITY;
-  for (int s = 0; s < nvalid; ++s) M = fmaxf(M, part[s * (HD + 2)]);
-  const float Mu = M == -INFINITY ? 0.f : M;
-  float L = 0.f, A = 0.f;
-  for (int s = 0; s < nvalid; ++s) {
+  // every chunk below nvalid holds at least one key, so its max is finite
+  float M = -INFINITY, L = 0.f, A = 0.f;
+  int s = 0;
+  for (; s + 4 <= nvalid; s += 4) {
+    float ms[4], ls[4], as[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float *ps = part + (s + j) * (HD + 2);
+      ms[j] = ps[0];
+      ls[j] = ps[1];
+      as[j] = ps[2 + d];
+    }
+    const float Mn = fmaxf(fmaxf(M, fmaxf(ms[0], ms[1])), fmaxf(ms[2], ms[3]));
+    const float fo = __builtin_amdgcn_exp2f(M - Mn);  // M = -inf -> 0
+    L *= fo;
+    A *= fo;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float f = __builtin_amdgcn_exp2f(ms[j] - Mn);
+      L += ls[j] * f;
+      A += as[j] * f;
+    }
+    M = Mn;
+  }
+  for (; s < nvalid; ++s) {
     const float *ps = part + s * (HD + 2);
-    const float f = __builtin_amdgcn_exp2f(ps[0] - Mu);
-    L += ps[1] * f;
-    A += ps[2 + d] * f;
+    const float ms = ps[0];
+    const float Mn = fmaxf(M, ms);
+    const float fo = __builtin_amdgcn_exp2f(M - Mn), f = __builtin_amdgcn_exp2f(ms - Mn);
+    L = L * fo + ps[1] * f;
+    A = A * fo + ps[2 + d] * f;
+    M = Mn;
   }
   const float out = L > 0.f ? A / L : 0.f;  // empty sequence -> zeros
   Elem<T>::store((T *)p.o + idx, out);
 }
 
-int choose_chunk(int batch, int max_len, int n_kv_heads) {
-  // enough workgroups to cover 256 CUs several times, chunks >= 128 keys
+#ifndef BN_DECODE_MIN_WG
+#define BN_DECODE_MIN_WG 2048
+#endif
+#ifndef BN_DECODE_ROWS_MIN_WG
+#define BN_DECODE_ROWS_MIN_WG 512
+#endif
+int choose_chunk(int batch, int max_len, int units, int min_wg) {
+  // enough workgroups to cover the 256 CUs several times over (a partial last
+  // round of resident workgroups costs a whole round), chunks >= 128 keys
   int chunk = 1024;
-  while (chunk > 128 &&
-         (int64_t)batch * n_kv_heads * ((max_len + chunk - 1) / chunk) < 1024)
+  while (chunk > 128 && (int64_t)batch * units * ((max_len + chunk - 1) / chunk) < min_wg)
     chunk >>= 1;
   return chunk;
 }
 
 template <typename T, int G>
 void launch_split(const DecodeParams &p, dim3 grid, hipStream_t s) {
-  if constexpr (std::is_same<T, bf16_t>::value)
-    hipLaunchKernelGGL((decode_bf16_mfma_kernel<G>), grid, dim3(256), 0, s, p);
-  else
+  if constexpr (std::is_same<T, bf16_t>::value) {
+    if (p.n_kv_heads % 4 == 0)
+      hipLaunchKernelGGL((decode_bf16_rows_kernel<G>), grid, dim3(256), 0, s, p);
+    else
+      hipLaunchKernelGGL((decode_bf16_mfma_kernel<G>), grid, dim3(256), 0, s, p);
+  } else {
     hipLaunchKernelGGL((decode_split_kernel<T, G>), grid, dim3(256), 0, s, p);
+  }
 }
+
+bool rows_path(const DecodeParams &p, bool bf16) { return bf16 && p.n_kv_heads % 4 == 0; }
 
 template <typename T>
 int launch_decode(const DecodeParams &p, int G, hipStream_t s) {
-  const dim3 grid((unsigned)((int64_t)p.batch * p.n_kv_heads * p.n_split));
+  const bool rows = rows_path(p, std::is_same<T, bf16_t>::value);
+  const dim3 grid((unsigned)((int64_t)p.batch * (rows ? p.n_kv_heads / 4 : p.n_kv_heads) *
+                             p.n_split));
   switch (G) {
     case 1: launch_split<T, 1>(p, grid, s); break;
     case 2: launch_split<T, 2>(p, grid, s); break;
@@ -502,7 +744,10 @@ int bn_gqa_decode(int dtype, const void *q, const void *k_cache, const void *v_c
   DecodeParams p;
   p.q = q; p.k = k_cache; p.v = v_cache; p.lens = seq_lens; p.o = o;
   p.batch = batch; p.max_len = max_len; p.n_heads = n_heads; p.n_kv_heads = n_kv_heads;
-  p.chunk = choose_chunk(batch, max_len, n_kv_heads);
+  // the whole-row kernel gives each workgroup 4 KV heads: 1/4 of the workgroups per chunk
+  p.chunk = rows_path(p, dtype == BN_BF16)
+                ? choose_chunk(batch, max_len, n_kv_heads / 4, BN_DECODE_ROWS_MIN_WG)
+                : choose_chunk(batch, max_len, n_kv_heads, BN_DECODE_MIN_WG);
   p.n_split = (max_len + p.chunk - 1) / p.chunk;
   p.c = scale * 1.4426950408889634f;
   const size_t need = (size_t)batch * n_heads * p.n_split * (HD + 2) * sizeof(float);
