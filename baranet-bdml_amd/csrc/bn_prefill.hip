@@ -114,16 +114,52 @@ __device__ __forceinline__ void softmax_block(f32x16_t (&s)[2], float &m, float 
 }
 
 // ------------------------------------------------------------------ bf16
-constexpr int KP16 = HD + 8;  // K row pitch (elements): 144 B, conflict-free b128 reads
-constexpr int VP16 = BN + 4;  // V^T row pitch: 136 B, conflict-free b64 reads
+// K and V blocks are staged row-major in a double-buffered LDS ring (one
+// barrier per block).  K fragments (A of S^T) are ds_read_b128 of K rows; V^T
+// fragments (A of O^T) come from the gfx950 transpose read ds_read_b64_tr_b16:
+// within each 16-lane group, output lane i slot j is element i%4 of the 8 bytes
+// at the address local lane 4j + i/4 supplied, so lanes point at 4 consecutive
+// d of one key row and receive one d for 4 consecutive keys.
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+constexpr int KP16 = HD + 8;   // K row pitch: 144 B, conflict-free b128 fragment reads
+constexpr int VP16 = HD + 32;  // V row pitch: 192 B, transpose reads of 8 rows x 64 B in 2 passes
+constexpr int KBUF = BN * KP16, VBUF = BN * VP16;
+constexpr float kRescaleLog2 = 8.f;  // keep a stale row max until the true one is 2^8 larger
+
+__device__ __forceinline__ bf16x4_t tr16(const bf16_t *lds) {
+  const s16x4_t r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) s16x4_t *)(__attribute__((address_space(3))) void *)lds);
+  return __builtin_bit_cast(bf16x4_t, r);
+}
+
+// XCD-aware order: consecutive workgroup ids go round-robin to the 8 XCDs
+// (each with its own L2); all G query heads of a (batch, KV head) group and
+// all its row tiles are placed on one XCD so the group's K/V stays in that
+// L2.  Heaviest row tiles first inside each XCD's queue.
+__device__ __forceinline__ Work decode_work_xcd(const PrefillParams &p) {
+  const int n_kv = p.n_heads / p.group;
+  const int NG = p.batch * n_kv;
+  if (NG % 8 != 0) return decode_work(p);
+  const int L = blockIdx.x, x = L & 7, j = L >> 3;
+  const int per_mt = (NG >> 3) * p.group;
+  Work w;
+  w.mt = p.n_mt - 1 - j / per_mt;
+  const int r = j % per_mt;
+  const int gi = (r / p.group) * 8 + x;
+  w.b = gi / n_kv;
+  w.g = gi % n_kv;
+  w.h = w.g * p.group + r % p.group;
+  return w;
+}
 
 __global__ __launch_bounds__(256, 2) void prefill_bf16_kernel(PrefillParams p) {
-  __shared__ __attribute__((aligned(16))) bf16_t Ks[BN * KP16];
-  __shared__ __attribute__((aligned(16))) bf16_t Vt[HD * VP16];
+  __shared__ __attribute__((aligned(16))) bf16_t smem[2 * (KBUF + VBUF)];
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int r32 = lane & 31, hf = lane >> 5;
-  const Work w = decode_work(p);
+  const Work w = decode_work_xcd(p);
   const bf16_t *Q = (const bf16_t *)p.q + w.b * p.q_bs + (int64_t)w.h * HD;
   const bf16_t *K = (const bf16_t *)p.k + w.b * p.kv_bs + (int64_t)w.g * HD;
   const bf16_t *V = (const bf16_t *)p.v + w.b * p.kv_bs + (int64_t)w.g * HD;
@@ -135,12 +171,13 @@ __global__ __launch_bounds__(256, 2) void prefill_bf16_kernel(PrefillParams p) {
 
   // Q^T operand: lane holds Q[qrow][16t + 8hf .. +7] for t = 0..3
   bf16x8_t qreg[4];
+  {
+    const bf16_t *qp = Q + (int64_t)min(qrow, p.seq_q - 1) * p.q_rs + 8 * hf;
 #pragma unroll
-  for (int t = 0; t < 4; ++t) {
-    if (row_ok)
-      qreg[t] = *(const bf16x8_t *)(Q + (int64_t)qrow * p.q_rs + 16 * t + 8 * hf);
-    else
-      qreg[t] = bf16x8_t{};
+    for (int t = 0; t < 4; ++t) {
+      qreg[t] = *(const bf16x8_t *)(qp + 16 * t);
+      if (!row_ok) qreg[t] = bf16x8_t{};
+    }
   }
 
   const int wg_last = min(w.mt * BM + BM, p.seq_q) - 1;
@@ -148,83 +185,114 @@ __global__ __launch_bounds__(256, 2) void prefill_bf16_kernel(PrefillParams p) {
   const int nblk = (kend + BN - 1) / BN;
   const int wave_last = min(q_wave0 + 31, p.seq_q - 1);
   const int wave_kend = (wave_last < q_wave0) ? 0 : key_end(p, wave_last);
-  const long qlimit = p.causal ? (long)qrow + p.seq_offset : (long)p.seq_kv;
+  const int qlimit = p.causal ? qrow + p.seq_offset : p.seq_kv;  // visible: key <= qlimit
 
-  // global -> register prefetch of one K and V block: 2 x 16 B of each per thread
-  uint4 kreg[2], vreg[2];
-  auto gload = [&](int kb) {
-#pragma unroll
-    for (int c = 0; c < 2; ++c) {
-      const int idx = tid + 256 * c, key = idx >> 3, dc = idx & 7;
-      const int kk = kb + key;
-      if (kk < p.seq_kv) {
-        kreg[c] = *(const uint4 *)(K + (int64_t)kk * p.kv_rs + dc * 8);
-        vreg[c] = *(const uint4 *)(V + (int64_t)kk * p.kv_rs + dc * 8);
-      } else {
-        kreg[c] = make_uint4(0, 0, 0, 0);
-        vreg[c] = make_uint4(0, 0, 0, 0);
-      }
-    }
+  // global -> register prefetch: 2 x 16 B of K and of V per thread and block;
+  // clamped rows (past seq_kv: a valid row whose score is masked, P = 0)
+  const int crow = tid >> 3, ccol = (tid & 7) * 8;  // chunk 1 adds 32 rows
+  u32x4_t k0, k1, v0, v1;
+  auto gload = [&](int blk) __attribute__((always_inline)) {
+    const int kb = BN * min(blk, nblk - 1);
+    const int64_t o0 = (int64_t)min(kb + crow, p.seq_kv - 1) * p.kv_rs + ccol;
+    const int64_t o1 = (int64_t)min(kb + crow + 32, p.seq_kv - 1) * p.kv_rs + ccol;
+    k0 = *(const u32x4_t *)(K + o0);
+    v0 = *(const u32x4_t *)(V + o0);
+    k1 = *(const u32x4_t *)(K + o1);
+    v1 = *(const u32x4_t *)(V + o1);
   };
-  auto lstore = [&]() {
-#pragma unroll
-    for (int c = 0; c < 2; ++c) {
-      const int idx = tid + 256 * c, key = idx >> 3, dc = idx & 7;
-      *(uint4 *)(Ks + key * KP16 + dc * 8) = kreg[c];
-      const uint32_t u[4] = {vreg[c].x, vreg[c].y, vreg[c].z, vreg[c].w};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        Vt[(dc * 8 + 2 * e) * VP16 + key] = (bf16_t)(u[e] & 0xffffu);
-        Vt[(dc * 8 + 2 * e + 1) * VP16 + key] = (bf16_t)(u[e] >> 16);
-      }
-    }
+  auto lstore = [&](int buf) __attribute__((always_inline)) {
+    bf16_t *ks = smem + buf * (KBUF + VBUF), *vs = ks + KBUF;
+    *(u32x4_t *)(ks + crow * KP16 + ccol) = k0;
+    *(u32x4_t *)(ks + (crow + 32) * KP16 + ccol) = k1;
+    *(u32x4_t *)(vs + crow * VP16 + ccol) = v0;
+    *(u32x4_t *)(vs + (crow + 32) * VP16 + ccol) = v1;
   };
 
   float m = -INFINITY, l = 0.f;
   f32x16_t o[2] = {f32x16_t{}, f32x16_t{}};
+  const float c = p.c;
+  const bf16x2_t ones = {(__bf16)1.0f, (__bf16)1.0f};
+  // transpose-read source: key row 4hf + n/4 (+8 for slots 4..7), d 16(q&1) + 4(n&3)
+  const int tr_off = (4 * hf + ((lane & 15) >> 2)) * VP16 + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
 
-  if (nblk > 0) gload(0);
+  if (nblk > 0) {
+    gload(0);
+    lstore(0);
+    gload(1);
+  }
+  __syncthreads();
   for (int blk = 0; blk < nblk; ++blk) {
     const int kb = blk * BN;
-    __syncthreads();
-    lstore();
-    __syncthreads();
-    if (blk + 1 < nblk) gload(kb + BN);
-    if (kb >= wave_kend) continue;  // every row of this wave masks the block
-
-    f32x16_t s[2];
+    const bf16_t *ks = smem + (blk & 1) * (KBUF + VBUF), *vs = ks + KBUF;
+    if (kb < wave_kend) {  // else every row of this wave masks the block
+      bf16x8_t ka[2][4];
 #pragma unroll
-    for (int kt = 0; kt < 2; ++kt) {
-      s[kt] = f32x16_t{};
+      for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const bf16x8_t a = *(const bf16x8_t *)(Ks + (kt * 32 + r32) * KP16 + 16 * t + 8 * hf);
-        s[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qreg[t], s[kt], 0, 0, 0);
+        for (int t = 0; t < 4; ++t)
+          ka[kt][t] = *(const bf16x8_t *)(ks + (kt * 32 + r32) * KP16 + 16 * t + 8 * hf);
+      f32x16_t s[2];
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt) {
+        s[kt] = f32x16_t{};
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+          s[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka[kt][t], qreg[t], s[kt], 0, 0, 0);
       }
-    }
-    const bool need_mask =
-        (kb + BN > p.seq_kv) || (p.causal && (long)kb + BN - 1 > (long)q_wave0 + p.seq_offset);
-    softmax_block(s, m, l, o, p.c, need_mask, kb, hf, qlimit, p.seq_kv);
-
-    // O^T += V^T P^T, 16 keys per MFMA.  k-slot (hf, j) of slice u of tile kt
-    // is key kt*32 + 16u + (j/4)*8 + hf*4 + j%4, which is register 8u+j of s[kt].
+      if (kb + BN > p.seq_kv || (p.causal && kb + BN - 1 > q_wave0 + p.seq_offset)) {
 #pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
+        for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        bf16x8_t pb;
+          for (int i = 0; i < 16; ++i) {
+            const int key = kb + kt * 32 + (i >> 2) * 8 + hf * 4 + (i & 3);
+            if (key >= p.seq_kv || key > qlimit) s[kt][i] = -INFINITY;
+          }
+      }
+      float mx = s[0][0];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) pb[j] = (__bf16)s[kt][8 * u + j];
-        const int kbase = kt * 32 + 16 * u + hf * 4;
+      for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-        for (int dt = 0; dt < 2; ++dt) {
-          const bf16_t *vrow = Vt + (dt * 32 + r32) * VP16 + kbase;
-          const bf16x4_t lo = *(const bf16x4_t *)(vrow);
-          const bf16x4_t hi = *(const bf16x4_t *)(vrow + 8);
-          const bf16x8_t a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-          o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb, o[dt], 0, 0, 0);
+        for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[kt][i]);
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      // lazy rescale: move the reference max only when it grew by > 2^8 in
+      // probability (exp2 units); p = exp2((s - m) c) then stays <= 2^8
+      const float m_new = fmaxf(m, mx);
+      const bool grow = (m_new - m) * c > kRescaleLog2;  // m = -inf, m_new finite -> true
+      if (__any(grow)) {
+        const float alpha = grow ? __builtin_amdgcn_exp2f((m - m_new) * c) : 1.f;
+        if (grow) m = m_new;
+        l *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) o[dt][i] *= alpha;
+      }
+      const float mc = (m == -INFINITY) ? 0.f : m * c;  // row with no visible key yet
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          bf16x8_t pb;
+#pragma unroll
+          for (int j = 0; j < 8; ++j)
+            pb[j] = (__bf16)__builtin_amdgcn_exp2f(fmaf(s[kt][8 * u + j], c, -mc));
+#pragma unroll
+          for (int j = 0; j < 4; ++j)  // row sum of the bf16 P the MFMA consumes
+            l = __builtin_amdgcn_fdot2_f32_bf16(bf16x2_t{pb[2 * j], pb[2 * j + 1]}, ones, l, false);
+          // O^T += V^T P^T over keys 32kt + 16u + (j/4)*8 + 4hf + j%4 (slot j)
+          const bf16_t *vsl = vs + (32 * kt + 16 * u) * VP16 + tr_off;
+#pragma unroll
+          for (int dt = 0; dt < 2; ++dt) {
+            const bf16x4_t lo = tr16(vsl + 32 * dt);
+            const bf16x4_t hi = tr16(vsl + 8 * VP16 + 32 * dt);
+            const bf16x8_t a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+            o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb, o[dt], 0, 0, 0);
+          }
         }
-      }
+    }
+    if (blk + 1 < nblk) lstore((blk + 1) & 1);  // that buffer was last read in block blk-1
+    gload(blk + 2);                             // clamped: same loads on every path
+    __syncthreads();
   }
 
   const float lt = l + __shfl_xor(l, 32, 64);
