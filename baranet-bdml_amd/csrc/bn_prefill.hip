@@ -126,7 +126,8 @@ typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 constexpr int KP16 = HD + 8;   // K row pitch: 144 B, conflict-free b128 fragment reads
 constexpr int VP16 = HD + 32;  // V row pitch: 192 B, transpose reads of 8 rows x 64 B in 2 passes
 constexpr int KBUF = BN * KP16, VBUF = BN * VP16;
-constexpr float kRescaleLog2 = 8.f;  // keep a stale row max until the true one is 2^8 larger
+constexpr float kRescaleLog2 = 8.f;
+  // keep a stale row max until the true one is 2^8 larger
 
 __device__ __forceinline__ bf16x4_t tr16(const bf16_t *lds) {
   const s16x4_t r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
@@ -154,8 +155,12 @@ __device__ __forceinline__ Work decode_work_xcd(const PrefillParams &p) {
   return w;
 }
 
+// RT = 32-row query tiles per wave: a workgroup owns 4*32*RT rows, and every
+// K and V^T fragment read from LDS feeds RT MFMAs.
+template <int RT>
 __global__ __launch_bounds__(256, 2) void prefill_bf16_kernel(PrefillParams p) {
   __shared__ __attribute__((aligned(16))) bf16_t smem[2 * (KBUF + VBUF)];
+  constexpr int WROWS = 32 * RT, WGROWS = 4 * WROWS;
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int r32 = lane & 31, hf = lane >> 5;
@@ -165,27 +170,28 @@ __global__ __launch_bounds__(256, 2) void prefill_bf16_kernel(PrefillParams p) {
   const bf16_t *V = (const bf16_t *)p.v + w.b * p.kv_bs + (int64_t)w.g * HD;
   bf16_t *O = (bf16_t *)p.o + w.b * p.o_bs + (int64_t)w.h * HD;
 
-  const int q_wave0 = w.mt * BM + wave * 32;
-  const int qrow = q_wave0 + r32;
-  const bool row_ok = qrow < p.seq_q;
+  const int q_wave0 = w.mt * WGROWS + wave * WROWS;
 
-  // Q^T operand: lane holds Q[qrow][16t + 8hf .. +7] for t = 0..3
-  bf16x8_t qreg[4];
-  {
+  // Q^T operands: row tile rt, lane holds Q[row][16t + 8hf .. +7] for t = 0..3
+  bf16x8_t qreg[RT][4];
+  int qlimit[RT];
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) {
+    const int qrow = q_wave0 + 32 * rt + r32;
     const bf16_t *qp = Q + (int64_t)min(qrow, p.seq_q - 1) * p.q_rs + 8 * hf;
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-      qreg[t] = *(const bf16x8_t *)(qp + 16 * t);
-      if (!row_ok) qreg[t] = bf16x8_t{};
+      qreg[rt][t] = *(const bf16x8_t *)(qp + 16 * t);
+      if (qrow >= p.seq_q) qreg[rt][t] = bf16x8_t{};
     }
+    qlimit[rt] = p.causal ? qrow + p.seq_offset : p.seq_kv;  // visible: key <= qlimit
   }
 
-  const int wg_last = min(w.mt * BM + BM, p.seq_q) - 1;
+  const int wg_last = min(w.mt * WGROWS + WGROWS, p.seq_q) - 1;
   const int kend = key_end(p, wg_last);
   const int nblk = (kend + BN - 1) / BN;
-  const int wave_last = min(q_wave0 + 31, p.seq_q - 1);
+  const int wave_last = min(q_wave0 + WROWS - 1, p.seq_q - 1);
   const int wave_kend = (wave_last < q_wave0) ? 0 : key_end(p, wave_last);
-  const int qlimit = p.causal ? qrow + p.seq_offset : p.seq_kv;  // visible: key <= qlimit
 
   // global -> register prefetch: 2 x 16 B of K and of V per thread and block;
   // clamped rows (past seq_kv: a valid row whose score is masked, P = 0)
@@ -208,8 +214,15 @@ __global__ __launch_bounds__(256, 2) void prefill_bf16_kernel(PrefillParams p) {
     *(u32x4_t *)(vs + (crow + 32) * VP16 + ccol) = v1;
   };
 
-  float m = -INFINITY, l = 0.f;
-  f32x16_t o[2] = {f32x16_t{}, f32x16_t{}};
+  float m[RT], l[RT];
+  f32x16_t o[RT][2];
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) {
+    m[rt] = -INFINITY;
+    l[rt] = 0.f;
+    o[rt][0] = f32x16_t{};
+    o[rt][1] = f32x16_t{};
+  }
   const float c = p.c;
   const bf16x2_t ones = {(__bf16)1.0f, (__bf16)1.0f};
   // transpose-read source: key row 4hf + n/4 (+8 for slots 4..7), d 16(q&1) + 4(n&3)
@@ -225,68 +238,86 @@ __global__ __launch_bounds__(256, 2) void prefill_bf16_kernel(PrefillParams p) {
     const int kb = blk * BN;
     const bf16_t *ks = smem + (blk & 1) * (KBUF + VBUF), *vs = ks + KBUF;
     if (kb < wave_kend) {  // else every row of this wave masks the block
-      bf16x8_t ka[2][4];
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-        for (int t = 0; t < 4; ++t)
-          ka[kt][t] = *(const bf16x8_t *)(ks + (kt * 32 + r32) * KP16 + 16 * t + 8 * hf);
-      f32x16_t s[2];
+      f32x16_t s[RT][2];
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt) {
-        s[kt] = f32x16_t{};
+        bf16x8_t ka[4];
 #pragma unroll
         for (int t = 0; t < 4; ++t)
-          s[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka[kt][t], qreg[t], s[kt], 0, 0, 0);
+          ka[t] = *(const bf16x8_t *)(ks + (kt * 32 + r32) * KP16 + 16 * t + 8 * hf);
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) {
+          s[rt][kt] = f32x16_t{};
+#pragma unroll
+          for (int t = 0; t < 4; ++t)
+            s[rt][kt] =
+                __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka[t], qreg[rt][t], s[rt][kt], 0, 0, 0);
+        }
       }
-      if (kb + BN > p.seq_kv || (p.causal && kb + BN - 1 > q_wave0 + p.seq_offset)) {
+      const bool masked = kb + BN > p.seq_kv || (p.causal && kb + BN - 1 > q_wave0 + p.seq_offset);
+      bf16x8_t pb[RT][2][2];  // [row tile][kt][u]
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) {
+        if (masked) {
+#pragma unroll
+          for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+              const int key = kb + kt * 32 + (i >> 2) * 8 + hf * 4 + (i & 3);
+              if (key >= p.seq_kv || key > qlimit[rt]) s[rt][kt][i] = -INFINITY;
+            }
+        }
+        float mx = s[rt][0][0];
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-          for (int i = 0; i < 16; ++i) {
-            const int key = kb + kt * 32 + (i >> 2) * 8 + hf * 4 + (i & 3);
-            if (key >= p.seq_kv || key > qlimit) s[kt][i] = -INFINITY;
+          for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[rt][kt][i]);
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        // lazy rescale: move the reference max only when it grew by > 2^8 in
+        // probability (exp2 units); p = exp2((s - m) c) then stays <= 2^8
+        const float m_new = fmaxf(m[rt], mx);
+        const bool grow = (m_new - m[rt]) * c > kRescaleLog2;  // m = -inf, m_new finite -> true
+        if (__any(grow)) {
+          const float alpha = grow ? __builtin_amdgcn_exp2f((m[rt] - m_new) * c) : 1.f;
+          if (grow) m[rt] = m_new;
+          l[rt] *= alpha;
+#pragma unroll
+          for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) o[rt][dt][i] *= alpha;
+        }
+        const float mc = (m[rt] == -INFINITY) ? 0.f : m[rt] * c;  // no visible key yet
+        float rs = 0.f;  // row sum of the bf16 P the MFMA consumes
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+              pb[rt][kt][u][j] =
+                  (__bf16)__builtin_amdgcn_exp2f(fmaf(s[rt][kt][8 * u + j], c, -mc));
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+              rs = __builtin_amdgcn_fdot2_f32_bf16(
+                  bf16x2_t{pb[rt][kt][u][2 * j], pb[rt][kt][u][2 * j + 1]}, ones, rs, false);
           }
+        l[rt] += rs;
       }
-      float mx = s[0][0];
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[kt][i]);
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      // lazy rescale: move the reference max only when it grew by > 2^8 in
-      // probability (exp2 units); p = exp2((s - m) c) then stays <= 2^8
-      const float m_new = fmaxf(m, mx);
-      const bool grow = (m_new - m) * c > kRescaleLog2;  // m = -inf, m_new finite -> true
-      if (__any(grow)) {
-        const float alpha = grow ? __builtin_amdgcn_exp2f((m - m_new) * c) : 1.f;
-        if (grow) m = m_new;
-        l *= alpha;
-#pragma unroll
-        for (int dt = 0; dt < 2; ++dt)
-#pragma unroll
-          for (int i = 0; i < 16; ++i) o[dt][i] *= alpha;
-      }
-      const float mc = (m == -INFINITY) ? 0.f : m * c;  // row with no visible key yet
+      // O^T += V^T P^T over keys 32kt + 16u + (j/4)*8 + 4hf + j%4 (slot j); each
+      // V^T fragment feeds the RT row tiles
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
-          bf16x8_t pb;
-#pragma unroll
-          for (int j = 0; j < 8; ++j)
-            pb[j] = (__bf16)__builtin_amdgcn_exp2f(fmaf(s[kt][8 * u + j], c, -mc));
-#pragma unroll
-          for (int j = 0; j < 4; ++j)  // row sum of the bf16 P the MFMA consumes
-            l = __builtin_amdgcn_fdot2_f32_bf16(bf16x2_t{pb[2 * j], pb[2 * j + 1]}, ones, l, false);
-          // O^T += V^T P^T over keys 32kt + 16u + (j/4)*8 + 4hf + j%4 (slot j)
           const bf16_t *vsl = vs + (32 * kt + 16 * u) * VP16 + tr_off;
 #pragma unroll
           for (int dt = 0; dt < 2; ++dt) {
             const bf16x4_t lo = tr16(vsl + 32 * dt);
             const bf16x4_t hi = tr16(vsl + 8 * VP16 + 32 * dt);
             const bf16x8_t a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-            o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb, o[dt], 0, 0, 0);
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt)
+              o[rt][dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb[rt][kt][u], o[rt][dt], 0, 0, 0);
           }
         }
     }
@@ -295,21 +326,25 @@ __global__ __launch_bounds__(256, 2) void prefill_bf16_kernel(PrefillParams p) {
     __syncthreads();
   }
 
-  const float lt = l + __shfl_xor(l, 32, 64);
-  const float inv = lt > 0.f ? 1.0f / lt : 0.f;  // no visible key -> zeros
-  if (row_ok) {
-    bf16_t *orow = O + (int64_t)qrow * p.o_rs;
 #pragma unroll
-    for (int dt = 0; dt < 2; ++dt)
+  for (int rt = 0; rt < RT; ++rt) {
+    const int qrow = q_wave0 + 32 * rt + r32;
+    const float lt = l[rt] + __shfl_xor(l[rt], 32, 64);
+    const float inv = lt > 0.f ? 1.0f / lt : 0.f;  // no visible key -> zeros
+    if (qrow < p.seq_q) {
+      bf16_t *orow = O + (int64_t)qrow * p.o_rs;
 #pragma unroll
-      for (int gi = 0; gi < 4; ++gi) {
-        const int d0 = dt * 32 + gi * 8 + hf * 4;
-        const uint32_t lo = (uint32_t)f32_to_bf16(o[dt][4 * gi] * inv) |
-                            ((uint32_t)f32_to_bf16(o[dt][4 * gi + 1] * inv) << 16);
-        const uint32_t hi = (uint32_t)f32_to_bf16(o[dt][4 * gi + 2] * inv) |
-                            ((uint32_t)f32_to_bf16(o[dt][4 * gi + 3] * inv) << 16);
-        *(uint2 *)(orow + d0) = make_uint2(lo, hi);
-      }
+      for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+        for (int gi = 0; gi < 4; ++gi) {
+          const int d0 = dt * 32 + gi * 8 + hf * 4;
+          const uint32_t lo = (uint32_t)f32_to_bf16(o[rt][dt][4 * gi] * inv) |
+                              ((uint32_t)f32_to_bf16(o[rt][dt][4 * gi + 1] * inv) << 16);
+          const uint32_t hi = (uint32_t)f32_to_bf16(o[rt][dt][4 * gi + 2] * inv) |
+                              ((uint32_t)f32_to_bf16(o[rt][dt][4 * gi + 3] * inv) << 16);
+          *(uint2 *)(orow + d0) = make_uint2(lo, hi);
+        }
+    }
   }
 }
 
@@ -478,7 +513,12 @@ extern "C" int bn_gqa_prefill(int dtype, const void *q, const void *k, const voi
       kv_batch_stride % vec || o_batch_stride % vec)
     return fail(BN_ERR_UNSUPPORTED,
                 std::string(op) + ": pointers must be 16-byte aligned and strides multiples of 16 bytes");
-  const int n_mt = (seq_q + BM - 1) / BM;
+  // bf16: two 32-row tiles per wave (every LDS fragment feeds two MFMAs) when
+  // that still leaves >= 2048 workgroups (8 per CU); one tile otherwise, so
+  // short sequences keep enough workgroups in flight
+  const int rt16 = ((int64_t)batch * n_heads * ((seq_q + 255) / 256) >= 2048) ? 2 : 1;
+  const int rows_per_wg = dtype == BN_BF16 ? 4 * 32 * rt16 : BM;
+  const int n_mt = (seq_q + rows_per_wg - 1) / rows_per_wg;
   const int64_t n_wg = (int64_t)batch * n_heads * n_mt;
   if (n_wg > 0x7fffffff) return fail(BN_ERR_UNSUPPORTED, std::string(op) + ": problem too large");
   int st = ensure_device();
@@ -495,7 +535,10 @@ extern "C" int bn_gqa_prefill(int dtype, const void *q, const void *k, const voi
   p.c = scale * 1.4426950408889634f;
   hipStream_t s = as_stream(stream);
   if (dtype == BN_BF16)
-    hipLaunchKernelGGL(prefill_bf16_kernel, dim3((unsigned)n_wg), dim3(256), 0, s, p);
+    if (rt16 == 2)
+      hipLaunchKernelGGL(prefill_bf16_kernel<2>, dim3((unsigned)n_wg), dim3(256), 0, s, p);
+    else
+      hipLaunchKernelGGL(prefill_bf16_kernel<1>, dim3((unsigned)n_wg), dim3(256), 0, s, p);
   else
     hipLaunchKernelGGL(prefill_f32_kernel, dim3((unsigned)n_wg), dim3(256), 0, s, p);
   BN_LAUNCH_CHECK();
