@@ -1,0 +1,189 @@
+"""TinyLLaMA-1.1B forward with a KV cache, built on the attention path.
+
+Drives BASELINE config 4: 22 layers, hidden 2048, 32/4 GQA heads, head_dim 64,
+SwiGLU 5632, vocab 32000, RMSNorm, RoPE theta 10000, fp32, random weights;
+a prompt prefill followed by greedy decode steps.
+
+The decoder layer follows the reference (src/llama/llama_layers.hpp:241-272,
+src/llama/llama_model.hpp:52-80): x -> RMSNorm -> GQA -> +x -> RMSNorm ->
+SwiGLU MLP -> +x, final RMSNorm, lm_head.  The reference keeps no KV cache
+(llama_model.py:135-141 reruns the prefix); this driver keeps one per layer
+([1, max_len, Hkv, 64]) and decodes the new token with the split-K decode
+kernel.  Per-head GQA semantics (query head h reads KV head h // 8).
+
+RMSNorm, RoPE, prefill attention and decode attention run on the HIP kernels
+through the C ABI (bnhip).  The dense projections, SwiGLU and the embedding
+gather are plain torch GPU operations (library GEMMs): they are not part of
+the attention path, and the config's metric times only the attention, RoPE
+and RMSNorm kernels.  ``path_ms`` accumulates hip-event time around those
+kernel launches (an upper bound on their device time; the rocprofv3 kernel
+trace gives the exact per-kernel durations).
+"""
+from __future__ import annotations
+
+import ctypes as C
+import math
+from dataclasses import dataclass
+
+import torch
+
+import bnhip
+
+
+@dataclass
+class TinyLlamaConfig:
+    vocab_size: int = 32000
+    hidden_size: int = 2048
+    intermediate_size: int = 5632
+    num_hidden_layers: int = 22
+    num_attention_heads: int = 32
+    num_key_value_heads: int = 4
+    rms_norm_eps: float = 1e-5
+    rope_theta: float = 10000.0
+
+    @property
+    def head_dim(self):
+        return self.hidden_size // self.num_attention_heads
+
+
+class TinyLlama:
+    def __init__(self, cfg: TinyLlamaConfig, max_len: int, seed: int = 1, std: float = 0.02,
+                 dtype=torch.float32):
+        if dtype != torch.float32:
+            raise ValueError("config 4 is fp32")
+        self.cfg = cfg
+        self.max_len = max_len
+        g = torch.Generator(device="cuda").manual_seed(seed)
+        h, kv, inter = cfg.hidden_size, cfg.num_key_value_heads * cfg.head_dim, cfg.intermediate_size
+
+        def w(*shape):
+            return torch.randn(shape, generator=g, device="cuda") * std
+
+        self.embed = w(cfg.vocab_size, h)
+        self.layers = []
+        for _ in range(cfg.num_hidden_layers):
+            self.layers.append(dict(
+                ln1=torch.ones((1, h), device="cuda"), wq=w(h, h), wk=w(h, kv), wv=w(h, kv),
+                wo=w(h, h), ln2=torch.ones((1, h), device="cuda"), wg=w(h, inter), wu=w(h, inter),
+                wd=w(inter, h),
+                k_cache=torch.zeros((1, max_len, cfg.num_key_value_heads, cfg.head_dim), device="cuda"),
+                v_cache=torch.zeros((1, max_len, cfg.num_key_value_heads, cfg.head_dim), device="cuda")))
+        self.ln_f = torch.ones((1, h), device="cuda")
+        self.lm_head = w(h, cfg.vocab_size)
+        self.length = 0
+        self.ws = bnhip.decode_workspace(1, max_len, cfg.num_attention_heads, cfg.head_dim)
+        self.path_ms = 0.0
+        self.timing = False
+        self.trace = None  # list of (kernel, inputs, output) when set
+
+    # ------------------------------------------------------------ path kernels
+    def _timed(self, fn):
+        if not self.timing:
+            return fn()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        out = fn()
+        e.record()
+        self._events.append((s, e))
+        return out
+
+    def _record(self, name, inputs, out, **kw):
+        if self.trace is not None:
+            torch.cuda.synchronize()
+            self.trace.append((name, [t.detach().cpu().numpy().copy() for t in inputs],
+                               out.detach().cpu().numpy().copy(), kw))
+
+    def rmsnorm(self, x, weight):
+        y = torch.empty_like(x)
+
+        def run():
+            bnhip.call("bn_rmsnorm", C.byref(bnhip.view(x)), C.byref(bnhip.view(weight)),
+                       C.byref(bnhip.view(y)), self.cfg.rms_norm_eps, bnhip.stream_of())
+        self._timed(run)
+        self._record("rmsnorm", [x, weight], y, eps=self.cfg.rms_norm_eps)
+        return y
+
+    def rope(self, x, offset):
+        y = torch.empty_like(x)
+
+        def run():
+            bnhip.call("bn_rope", C.byref(bnhip.view(x)), C.byref(bnhip.view(y)), offset,
+                       self.cfg.head_dim, self.cfg.rope_theta, bnhip.stream_of())
+        self._timed(run)
+        self._record("rope", [x], y, offset=offset, head_dim=self.cfg.head_dim,
+                     theta=self.cfg.rope_theta)
+        return y
+
+    def prefill_attention(self, q, k, v):
+        cfg = self.cfg
+        S = q.shape[0]
+        q4 = q.view(1, S, cfg.num_attention_heads, cfg.head_dim)
+        k4 = k.view(1, S, cfg.num_key_value_heads, cfg.head_dim)
+        v4 = v.view(1, S, cfg.num_key_value_heads, cfg.head_dim)
+        o = self._timed(lambda: bnhip.gqa_prefill(q4, k4, v4, scale=1.0 / math.sqrt(cfg.head_dim)))
+        self._record("prefill", [q4, k4, v4], o)
+        return o.view(S, cfg.hidden_size)
+
+    def decode_attention(self, q, layer, length):
+        cfg = self.cfg
+        q3 = q.view(1, cfg.num_attention_heads, cfg.head_dim)
+        lens = torch.tensor([length], dtype=torch.int32, device="cuda")
+        o = self._timed(lambda: bnhip.gqa_decode(q3, layer["k_cache"], layer["v_cache"], lens,
+                                                 scale=1.0 / math.sqrt(cfg.head_dim),
+                                                 workspace=self.ws))
+        self._record("decode", [q3, layer["k_cache"][:, :length], layer["v_cache"][:, :length]], o,
+                     length=length)
+        return o.view(1, cfg.hidden_size)
+
+    # ------------------------------------------------------------ model
+    def _layer(self, hdn, L, pos0):
+        cfg = self.cfg
+        n = hdn.shape[0]
+        x = self.rmsnorm(hdn, L["ln1"])
+        q, k, v = x @ L["wq"], x @ L["wk"], x @ L["wv"]
+        q, k = self.rope(q, pos0), self.rope(k, pos0)
+        L["k_cache"][0, pos0:pos0 + n] = k.view(n, cfg.num_key_value_heads, cfg.head_dim)
+        L["v_cache"][0, pos0:pos0 + n] = v.view(n, cfg.num_key_value_heads, cfg.head_dim)
+        if pos0 == 0:
+            o = self.prefill_attention(q, k, v)
+        else:
+            o = self.decode_attention(q, L, pos0 + 1)
+        hdn = hdn + o @ L["wo"]
+        x = self.rmsnorm(hdn, L["ln2"])
+        return hdn + (torch.nn.functional.silu(x @ L["wg"]) * (x @ L["wu"])) @ L["wd"]
+
+    def _logits(self, hdn):
+        return self.rmsnorm(hdn[-1:], self.ln_f) @ self.lm_head
+
+    def prefill(self, ids: torch.Tensor) -> torch.Tensor:
+        """Process the prompt (positions 0..S-1); returns last-row logits."""
+        assert self.length == 0 and ids.numel() <= self.max_len
+        hdn = self.embed[ids]
+        for L in self.layers:
+            hdn = self._layer(hdn, L, 0)
+        self.length = ids.numel()
+        return self._logits(hdn)
+
+    def step(self, token: torch.Tensor) -> torch.Tensor:
+        """Append one token at position `length`; returns its logits."""
+        assert self.length < self.max_len
+        hdn = self.embed[token.view(1)]
+        for L in self.layers:
+            hdn = self._layer(hdn, L, self.length)
+        self.length += 1
+        return self._logits(hdn)
+
+    def generate(self, ids: torch.Tensor, new_tokens: int, time_path: bool = False):
+        """Greedy decode; returns the generated ids and the path-kernel ms."""
+        self.timing, self._events, self.path_ms = time_path, [], 0.0
+        logits = self.prefill(ids)
+        out = []
+        for _ in range(new_tokens):
+            tok = torch.argmax(logits[-1])
+            out.append(tok)
+            logits = self.step(tok)
+        torch.cuda.synchronize()
+        if time_path:
+            self.path_ms = sum(s.elapsed_time(e) for s, e in self._events)
+        self.timing = False
+        return torch.stack(out), self.path_ms

@@ -169,6 +169,104 @@ def bench_copy(steps, warmup):
             "ms_per_launch": round(ms, 5), "bytes_read": 4 * n, "bytes_written": 4 * n}
 
 
+def bench_block(steps, warmup):
+    """Config 1: one TinyLLaMA attention block through the `bten` surface, fp32,
+    B=1 S=128: RMSNorm(1e-5) -> Q/K/V -> RoPE -> causal softmax(QK^T/8)V -> O.
+    fused_head = the reference's chain (one S x S probability matrix over the
+    2048-wide rows); per_head = GQA with the fused prefill kernel."""
+    import numpy as np
+    import torch
+    import bten
+    from llama_layers import GroupedQueryAttention, RMSNorm
+    S, hid = 128, 2048
+    x = np.random.default_rng(0).standard_normal((S, hid)).astype(np.float32)
+    rw = np.random.default_rng(1)
+    ws = [(rw.standard_normal(sh) * 0.02).astype(np.float32)
+          for sh in ((hid, hid), (hid, 256), (hid, 256), (hid, hid))]
+    xt = bten.TensorF(S, hid)
+    xt.copy_from_numpy(x)
+    out = {}
+    for mode in ("fused_head", "per_head"):
+        norm = RMSNorm(hid, eps=1e-5)
+        attn = GroupedQueryAttention(bten.LLaMAConfig(), mode=mode)
+        attn.load_weights(*ws)
+        ms = time_launches(lambda i: attn(norm(xt)), steps, warmup)
+        out[mode] = {"ms_per_block": round(ms, 4)}
+    out["note"] = ("bten launches on the legacy default stream, timed with events on the same "
+                   "stream; includes the per-op pool allocations of the op surface")
+    return out, (x, ws)
+
+
+def cpu_baseline_block(x, ws):
+    """Config 1 on the CPU oracle (single thread), the reference's fused-head chain."""
+    import numpy as np
+    from oracle import oracle as O
+    t0 = time.perf_counter()
+    xn = O.rmsnorm(x, np.ones((1, x.shape[1]), np.float32), 1e-5)
+    O.gqa_layer(xn, *ws, 32, 4, 10000.0, 0, per_head=False)
+    el = time.perf_counter() - t0
+    return {"value": round(el * 1e3, 2), "unit": "ms per block", "cores": 1, "kind": "port",
+            "sample": "the whole config-1 block once (RMSNorm + projections + fused-head "
+                      "attention + output projection), fp32 oracle"}
+
+
+def bench_tinyllama(prompt=512, new_tokens=128, cpu=True):
+    """Config 4: TinyLLaMA-1.1B (random init, fp32) prefill of a 512-token seeded
+    prompt + 128 greedy decode steps with a KV cache.  path_ms = hip-event time
+    around the attention, RoPE and RMSNorm launches (includes any launch gaps:
+    an upper bound on their device time)."""
+    import numpy as np
+    import torch
+    from tinyllama import TinyLlama, TinyLlamaConfig
+    cfg = TinyLlamaConfig()
+    m = TinyLlama(cfg, max_len=prompt + new_tokens, seed=1)
+    ids = torch.from_numpy(np.random.default_rng(3).integers(0, 32000, prompt)).cuda()
+    m.generate(ids, 2)  # warm-up (kernels, rocBLAS handles)
+    for L in m.layers:
+        L["k_cache"].zero_()
+        L["v_cache"].zero_()
+    m.length = 0
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    toks, path_ms = m.generate(ids, new_tokens, time_path=True)
+    wall = time.perf_counter() - t0
+    res = {"prompt": prompt, "new_tokens": new_tokens, "wall_s": round(wall, 3),
+           "path_ms": round(path_ms, 3),
+           "path_kernels": "RMSNorm, RoPE, GQA prefill, GQA decode (fp32)",
+           "first_tokens": [int(t) for t in toks[:8].cpu()], "cache_length_end": m.length}
+    if cpu:
+        res["cpu_baseline"] = cpu_baseline_tinyllama(m, ids)
+    return res
+
+
+def cpu_baseline_tinyllama(m, ids):
+    """Oracle on the layer-0 prefill path inputs of the GPU model (teacher-forced),
+    single thread, extrapolated x22 layers (labelled).  The projections that feed
+    RoPE are numpy GEMMs outside the timed regions."""
+    from oracle import oracle as O
+    cfg = m.cfg
+    L0 = m.layers[0]
+    x = m.embed[ids].cpu().numpy()
+    w = L0["ln1"].cpu().numpy()
+    t0 = time.perf_counter()
+    xn = O.rmsnorm(x, w, cfg.rms_norm_eps)
+    t_norm = time.perf_counter() - t0
+    q, k, v = xn @ L0["wq"].cpu().numpy(), xn @ L0["wk"].cpu().numpy(), xn @ L0["wv"].cpu().numpy()
+    S = x.shape[0]
+    t0 = time.perf_counter()
+    qr, kr = O.rope(q, 0, 64, 1e4), O.rope(k, 0, 64, 1e4)
+    O.gqa_prefill(qr.reshape(1, S, 32, 64), kr.reshape(1, S, 4, 64), v.reshape(1, S, 4, 64),
+                  0.125, True, 0)
+    t_attn = time.perf_counter() - t0
+    layer_s = 2 * t_norm + t_attn  # two RMSNorms per decoder layer
+    return {"value": round(layer_s * cfg.num_hidden_layers * 1e3, 1),
+            "unit": "ms (prefill path kernels, 22 layers, extrapolated from layer 0)",
+            "cores": 1, "kind": "port",
+            "sample": f"layer 0 of the prefill: 2 RMSNorm + RoPE(q, k) + per-head causal GQA "
+                      f"over {S} tokens on the GPU run's inputs, fp32 oracle, "
+                      f"{layer_s:.2f} s; decode steps not included"}
+
+
 def cpu_baseline_prefill(budget_s=12.0):
     """CPU oracle (single thread) on whole (batch, head) pairs of config 2."""
     import numpy as np
@@ -217,7 +315,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--only", default="",
                     help="comma list of extra workloads (default: all but copy): "
-                         "decode,ragged,fp32,norm,long,copy; 'head' = headline prefill only")
+                         "decode,ragged,fp32,norm,long,block,tinyllama,copy; "
+                         "'head' = headline prefill only")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
@@ -259,6 +358,14 @@ def main():
         out["prefill_long"] = bench_prefill(1, 16384, 32, 4, "bf16", max(K // 4, 3), 1)
         print(f"prefill S=16384: {out['prefill_long']['value']} TFLOP/s", file=sys.stderr,
               flush=True)
+    if want("block"):
+        out["attention_block"], blk_inputs = bench_block(K, W)
+        if not args.no_cpu:
+            out["attention_block"]["cpu_baseline"] = cpu_baseline_block(*blk_inputs)
+        print(f"config 1 block: {out['attention_block']}", file=sys.stderr, flush=True)
+    if want("tinyllama"):
+        out["tinyllama"] = bench_tinyllama(cpu=not args.no_cpu)
+        print(f"config 4: {out['tinyllama']}", file=sys.stderr, flush=True)
     if "copy" in only:
         out["copy"] = bench_copy(K, W)
         print(f"copy: {out['copy']['value']} GB/s", file=sys.stderr, flush=True)
