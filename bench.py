@@ -210,7 +210,7 @@ def cpu_baseline_block(x, ws):
                       "attention + output projection), fp32 oracle"}
 
 
-def bench_tinyllama(prompt=512, new_tokens=128, cpu=True):
+def bench_tinyllama(prompt=512, new_tokens=128, cpu=True, warmup_tokens=2):
     """Config 4: TinyLLaMA-1.1B (random init, fp32) prefill of a 512-token seeded
     prompt + 128 greedy decode steps with a KV cache.  path_ms = hip-event time
     around the attention, RoPE and RMSNorm launches (includes any launch gaps:
@@ -221,11 +221,12 @@ def bench_tinyllama(prompt=512, new_tokens=128, cpu=True):
     cfg = TinyLlamaConfig()
     m = TinyLlama(cfg, max_len=prompt + new_tokens, seed=1)
     ids = torch.from_numpy(np.random.default_rng(3).integers(0, 32000, prompt)).cuda()
-    m.generate(ids, 2)  # warm-up (kernels, rocBLAS handles)
-    for L in m.layers:
-        L["k_cache"].zero_()
-        L["v_cache"].zero_()
-    m.length = 0
+    if warmup_tokens:
+        m.generate(ids, warmup_tokens)  # warm-up (kernels, library handles)
+        for L in m.layers:
+            L["k_cache"].zero_()
+            L["v_cache"].zero_()
+        m.length = 0
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     toks, path_ms = m.generate(ids, new_tokens, time_path=True)
@@ -313,6 +314,9 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
+    ap.add_argument("--tl-warmup", type=int, default=2,
+                    help="config 4: warm-up decode tokens before the timed generate (0: none, "
+                         "so a kernel trace holds exactly one prefill + 128 steps)")
     ap.add_argument("--only", default="",
                     help="comma list of extra workloads (default: all but copy): "
                          "decode,ragged,fp32,norm,long,block,tinyllama,copy; "
@@ -364,7 +368,7 @@ def main():
             out["attention_block"]["cpu_baseline"] = cpu_baseline_block(*blk_inputs)
         print(f"config 1 block: {out['attention_block']}", file=sys.stderr, flush=True)
     if want("tinyllama"):
-        out["tinyllama"] = bench_tinyllama(cpu=not args.no_cpu)
+        out["tinyllama"] = bench_tinyllama(cpu=not args.no_cpu, warmup_tokens=args.tl_warmup)
         print(f"config 4: {out['tinyllama']}", file=sys.stderr, flush=True)
     if "copy" in only:
         out["copy"] = bench_copy(K, W)
