@@ -18,8 +18,15 @@ namespace {
 
 // 16-byte chunk <-> VEC floats
 template <typename T> struct Chunk;
+typedef uint32_t raw16_t __attribute__((ext_vector_type(4)));  // one 16-byte chunk
+__device__ __forceinline__ raw16_t load_raw(const void *p) { return *reinterpret_cast<const raw16_t *>(p); }
+
 template <> struct Chunk<float> {
   static constexpr int VEC = 4;
+  __device__ static __forceinline__ void cvt(raw16_t t, float (&v)[4]) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = __uint_as_float(t[i]);
+  }
   __device__ static __forceinline__ void load(const float *p, float (&v)[4]) {
     float4 t = *reinterpret_cast<const float4 *>(p);
     v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
@@ -30,6 +37,13 @@ template <> struct Chunk<float> {
 };
 template <> struct Chunk<bf16_t> {
   static constexpr int VEC = 8;
+  __device__ static __forceinline__ void cvt(raw16_t t, float (&v)[8]) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[2 * i] = __uint_as_float(t[i] << 16);
+      v[2 * i + 1] = __uint_as_float(t[i] & 0xffff0000u);
+    }
+  }
   __device__ static __forceinline__ void load(const bf16_t *p, float (&v)[8]) {
     uint4 t = *reinterpret_cast<const uint4 *>(p);
     uint32_t u[4] = {t.x, t.y, t.z, t.w};
@@ -49,11 +63,11 @@ template <> struct Chunk<bf16_t> {
 };
 
 constexpr int kRowsPerBlock = 4;  // 4 waves, one row each
-constexpr int kMaxChunks = 8;     // chunks per lane kept in registers
+constexpr int kMaxChunks = 8;     // chunks per lane kept in registers (at most)
 
-// y = rope?(x / rms * w); requires cols % VEC == 0, cols <= 64*kMaxChunks*VEC,
-// head_dim % VEC == 0 when ROPE.
-template <typename T, bool ROPE>
+// y = rope?(x / rms * w); requires cols % VEC == 0, cols <= 64*NCH*VEC,
+// head_dim % VEC == 0 when ROPE.  NCH = 16-byte chunks per lane.
+template <typename T, bool ROPE, int NCH>
 __global__ __launch_bounds__(256) void rmsnorm_rows_kernel(
     const T *__restrict__ x, int64_t x_rs, const T *__restrict__ w, int64_t w_off,
     T *__restrict__ y, int64_t y_rs, int rows, int cols, float eps, int pos_off,
@@ -64,13 +78,21 @@ __global__ __launch_bounds__(256) void rmsnorm_rows_kernel(
   if (row >= rows) return;
   const T *xr = x + (int64_t)row * x_rs;
   const int nchunks = cols / VEC;
-  float v[kMaxChunks][VEC];
+  // every x and weight chunk of the row is requested before the first use
+  // (clamped indices, no branch), so a short call pays one memory latency
+  raw16_t xraw[NCH], wraw[NCH];
+#pragma unroll
+  for (int i = 0; i < NCH; ++i) {
+    const int cc = min(lane + 64 * i, nchunks - 1);
+    xraw[i] = load_raw(xr + cc * VEC);
+    wraw[i] = load_raw(w + w_off + cc * VEC);
+  }
+  float v[NCH][VEC];
   float ss = 0.f;
 #pragma unroll
-  for (int i = 0; i < kMaxChunks; ++i) {
-    int c = lane + 64 * i;
-    if (c < nchunks) {
-      Chunk<T>::load(xr + c * VEC, v[i]);
+  for (int i = 0; i < NCH; ++i) {
+    Chunk<T>::cvt(xraw[i], v[i]);
+    if (lane + 64 * i < nchunks) {
 #pragma unroll
       for (int j = 0; j < VEC; ++j) ss += v[i][j] * v[i][j];
     }
@@ -84,11 +106,11 @@ __global__ __launch_bounds__(256) void rmsnorm_rows_kernel(
   int cached_p0 = -1;
   float cs[VEC / 2], sn[VEC / 2];
 #pragma unroll
-  for (int i = 0; i < kMaxChunks; ++i) {
+  for (int i = 0; i < NCH; ++i) {
     int c = lane + 64 * i;
     if (c < nchunks) {
       float wv[VEC];
-      Chunk<T>::load(w + w_off + c * VEC, wv);
+      Chunk<T>::cvt(wraw[i], wv);
       float o[VEC];
 #pragma unroll
       for (int j = 0; j < VEC; ++j) o[j] = (v[i][j] * inv_rms) * wv[j];
@@ -234,9 +256,14 @@ int launch_rmsnorm(const bn_view *x, const bn_view *weight, const bn_view *y, fl
     const T *wp = reinterpret_cast<const T *>(weight->data) + weight->offset;
     T *yp = reinterpret_cast<T *>(y->data) + y->offset;
     dim3 grid((rows + kRowsPerBlock - 1) / kRowsPerBlock);
-    hipLaunchKernelGGL((rmsnorm_rows_kernel<T, ROPE>), grid, dim3(256), 0, s, xp,
-                       (int64_t)x->stride_h, wp, (int64_t)0, yp, (int64_t)y->stride_h, rows,
-                       cols, eps, pos_off, head_dim, fr);
+    if (cols <= 64 * 4 * VEC)
+      hipLaunchKernelGGL((rmsnorm_rows_kernel<T, ROPE, 4>), grid, dim3(256), 0, s, xp,
+                         (int64_t)x->stride_h, wp, (int64_t)0, yp, (int64_t)y->stride_h, rows,
+                         cols, eps, pos_off, head_dim, fr);
+    else
+      hipLaunchKernelGGL((rmsnorm_rows_kernel<T, ROPE, kMaxChunks>), grid, dim3(256), 0, s, xp,
+                         (int64_t)x->stride_h, wp, (int64_t)0, yp, (int64_t)y->stride_h, rows,
+                         cols, eps, pos_off, head_dim, fr);
   } else {
     DView<const T> xv = dview<const T>(x), wv = dview<const T>(weight);
     DView<T> yv = dview<T>(y);

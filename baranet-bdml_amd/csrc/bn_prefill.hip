@@ -7,12 +7,13 @@
 // copying) with one flash-style kernel: O(S) memory, K/V blocks staged
 // through LDS, online softmax in fp32.
 //
-// Work decomposition: a 256-thread workgroup (4 waves) owns 128 query rows
-// of one (batch, head); each wave owns 32 rows.  Key blocks of 64 are staged
-// in LDS (K row-major, V transposed) with the next block's global loads in
-// flight while the current block is computed.
+// Work decomposition: a 256-thread workgroup (4 waves) owns 4 x 32*RT query
+// rows of one (batch, head); each wave owns 32*RT rows (fp32: RT = 1; bf16:
+// RT = 2 for long sequences, 1 otherwise).  Key blocks of 64 are staged in
+// LDS with the next blocks' global loads in flight while the current block
+// is computed.
 //
-// Per wave and 32-key tile the score tile is computed transposed,
+// Per wave and key tile the score tile is computed transposed,
 //   S^T[key][query] = K[key][:] . Q[query][:]      (v_mfma_f32_32x32x16_bf16 /
 //                                                   v_mfma_f32_32x32x2f32)
 // so that each lane holds 16 keys of ONE query: the softmax row max and row
@@ -23,10 +24,12 @@
 // shuffles), and whose per-query rescale is a per-lane scalar.
 //
 // Causal work is unbalanced (row tile m needs m+1 key blocks); workgroups are
-// issued heaviest-first.  Fully masked key blocks of a wave are skipped; only
-// diagonal / tail blocks evaluate the mask.  Mask: key j is visible to query
-// row i iff j <= i + seq_offset (op_softmax.cuh:89-99) and j < seq_kv.
+// issued heaviest-first.  Only diagonal / tail tiles evaluate the mask.
+// Mask: key j is visible to query row i iff j <= i + seq_offset
+// (op_softmax.cuh:89-99) and j < seq_kv.
 #include "bn_common.hpp"
+
+#include <type_traits>
 
 namespace bn {
 namespace {
@@ -155,24 +158,62 @@ __device__ __forceinline__ Work decode_work_xcd(const PrefillParams &p) {
   return w;
 }
 
-// RT = 32-row query tiles per wave: a workgroup owns 4*32*RT rows, and every
-// K and V^T fragment read from LDS feeds RT MFMAs.
-template <int RT>
-__global__ __launch_bounds__(256, 2) void prefill_bf16_kernel(PrefillParams p) {
-  __shared__ __attribute__((aligned(16))) bf16_t smem[2 * (KBUF + VBUF)];
+// Kernel structure -- the softmax does little VALU work per score and runs
+// while the matrix cores work:
+//   * the fast path is p = exp2(s * c - m * c), c = scale*log2(e), against a
+//     reference max m that is NOT recomputed per tile: one fma, one
+//     transcendental, half a bf16 pack and half a dot2 (row sum) per score;
+//   * m moves only in a rare exact fixup, taken when a tile's row sum exceeds
+//     2^16 (some p > 2^16, which includes inf and the NaN of the first tile,
+//     where m = -inf), and then only when it grew by more than 2^8;
+//   * software pipeline over 32-key tiles: step t issues O += V_{t-1}^T P_{t-1}
+//     and the scores of tile t+1 on the matrix cores, interleaved with the
+//     softmax of tile t on the VALU -- three independent pieces of work in
+//     one basic block.  Every wave runs the same steps (tiles past its causal
+//     range are all -inf, P = 0), so no branch separates them;
+//   * K/V blocks are staged with buffer loads whose descriptor starts at the
+//     block: the per-thread offset is fixed and rows past seq_kv read as 0.
+// LDS: 2-deep K and V rings of 64-key blocks.  Block iteration j runs steps
+// 2j+1 and 2j+2, which read only V_j and K_{j+1}; it stores K_{j+2} and
+// V_{j+1} (register-staged one iteration earlier) into the buffers of K_j and
+// V_{j-1}, last read in iteration j-1: one barrier per block orders them.
+constexpr float kSumLimit = 65536.f;
+#ifndef BN_PIPE_OCC1
+#define BN_PIPE_OCC1 2  // workgroups per CU the register budget is sized for (RT = 1)
+#endif
+#ifndef BN_PIPE_OCC2
+#define BN_PIPE_OCC2 2  // (RT = 2)
+#endif
+#ifndef BN_PIPE_SCHED
+#define BN_PIPE_SCHED 1
+#endif
+#ifndef BN_PIPE_V0
+#define BN_PIPE_V0 4  // VALU instructions ahead of the first MFMA of a step
+#endif
+#ifndef BN_PIPE_V1
+#define BN_PIPE_V1 5  // VALU instructions after each MFMA
+#endif
+
+template <int RT, int OCC>
+__global__ __launch_bounds__(256, OCC) void prefill_bf16_kernel(PrefillParams p) {
+  __shared__ __attribute__((aligned(16))) bf16_t smem[2 * KBUF + 2 * VBUF];
+  bf16_t *const kring = smem;
+  bf16_t *const vring = smem + 2 * KBUF;
   constexpr int WROWS = 32 * RT, WGROWS = 4 * WROWS;
 
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r32 = lane & 31, hf = lane >> 5;
   const Work w = decode_work_xcd(p);
   const bf16_t *Q = (const bf16_t *)p.q + w.b * p.q_bs + (int64_t)w.h * HD;
   const bf16_t *K = (const bf16_t *)p.k + w.b * p.kv_bs + (int64_t)w.g * HD;
   const bf16_t *V = (const bf16_t *)p.v + w.b * p.kv_bs + (int64_t)w.g * HD;
   bf16_t *O = (bf16_t *)p.o + w.b * p.o_bs + (int64_t)w.h * HD;
+  const float c = p.c;
 
   const int q_wave0 = w.mt * WGROWS + wave * WROWS;
 
-  // Q^T operands: row tile rt, lane holds Q[row][16t + 8hf .. +7] for t = 0..3
+  // Q^T operands: lane holds Q[row][16t + 8hf .. +7], t = 0..3
   bf16x8_t qreg[RT][4];
   int qlimit[RT];
 #pragma unroll
@@ -188,33 +229,43 @@ __global__ __launch_bounds__(256, 2) void prefill_bf16_kernel(PrefillParams p) {
   }
 
   const int wg_last = min(w.mt * WGROWS + WGROWS, p.seq_q) - 1;
-  const int kend = key_end(p, wg_last);
-  const int nblk = (kend + BN - 1) / BN;
+  const int nblk = (key_end(p, wg_last) + BN - 1) / BN;
   const int wave_last = min(q_wave0 + WROWS - 1, p.seq_q - 1);
-  const int wave_kend = (wave_last < q_wave0) ? 0 : key_end(p, wave_last);
+  const int ntw = (wave_last < q_wave0) ? 0 : (key_end(p, wave_last) + 31) / 32;  // tiles
 
-  // global -> register prefetch: 2 x 16 B of K and of V per thread and block;
-  // clamped rows (past seq_kv: a valid row whose score is masked, P = 0)
-  const int crow = tid >> 3, ccol = (tid & 7) * 8;  // chunk 1 adds 32 rows
+  // register staging: 2 x 16 B per thread of a K block and of a V block,
+  // rows crow and crow + 32 of the block; bytes past the last key row are
+  // outside the descriptor's range and read as 0 (their scores are masked)
+  const int crow = tid >> 3, ccol = (tid & 7) * 8;
+  const int voff0 = (crow * (int)p.kv_rs + ccol) * 2, voff1 = voff0 + 64 * (int)p.kv_rs;
   u32x4_t k0, k1, v0, v1;
-  auto gload = [&](int blk) __attribute__((always_inline)) {
-    const int kb = BN * min(blk, nblk - 1);
-    const int64_t o0 = (int64_t)min(kb + crow, p.seq_kv - 1) * p.kv_rs + ccol;
-    const int64_t o1 = (int64_t)min(kb + crow + 32, p.seq_kv - 1) * p.kv_rs + ccol;
-    k0 = *(const u32x4_t *)(K + o0);
-    v0 = *(const u32x4_t *)(V + o0);
-    k1 = *(const u32x4_t *)(K + o1);
-    v1 = *(const u32x4_t *)(V + o1);
+  auto rsrc = [&](const bf16_t *base, int blk) __attribute__((always_inline)) {
+    const int rows = min(max(p.seq_kv - BN * blk, 0), BN);
+    return __builtin_amdgcn_make_buffer_rsrc((void *)(base + (int64_t)BN * blk * p.kv_rs),
+                                             (short)0, rows * (int)p.kv_rs * 2, 0x00020000);
   };
-  auto lstore = [&](int buf) __attribute__((always_inline)) {
-    bf16_t *ks = smem + buf * (KBUF + VBUF), *vs = ks + KBUF;
+  auto gload_k = [&](int blk) __attribute__((always_inline)) {
+    const __amdgpu_buffer_rsrc_t r = rsrc(K, blk);
+    k0 = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, voff0, 0, 0));
+    k1 = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, voff1, 0, 0));
+  };
+  auto gload_v = [&](int blk) __attribute__((always_inline)) {
+    const __amdgpu_buffer_rsrc_t r = rsrc(V, blk);
+    v0 = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, voff0, 0, 0));
+    v1 = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, voff1, 0, 0));
+  };
+  auto lstore_k = [&](int buf) __attribute__((always_inline)) {
+    bf16_t *ks = kring + buf * KBUF;
     *(u32x4_t *)(ks + crow * KP16 + ccol) = k0;
     *(u32x4_t *)(ks + (crow + 32) * KP16 + ccol) = k1;
+  };
+  auto lstore_v = [&](int buf) __attribute__((always_inline)) {
+    bf16_t *vs = vring + buf * VBUF;
     *(u32x4_t *)(vs + crow * VP16 + ccol) = v0;
     *(u32x4_t *)(vs + (crow + 32) * VP16 + ccol) = v1;
   };
 
-  float m[RT], l[RT];
+  float m[RT], l[RT];  // reference max (raw score units), row-sum partial
   f32x16_t o[RT][2];
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
@@ -223,108 +274,199 @@ __global__ __launch_bounds__(256, 2) void prefill_bf16_kernel(PrefillParams p) {
     o[rt][0] = f32x16_t{};
     o[rt][1] = f32x16_t{};
   }
-  const float c = p.c;
   const bf16x2_t ones = {(__bf16)1.0f, (__bf16)1.0f};
-  // transpose-read source: key row 4hf + n/4 (+8 for slots 4..7), d 16(q&1) + 4(n&3)
   const int tr_off = (4 * hf + ((lane & 15) >> 2)) * VP16 + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
 
-  if (nblk > 0) {
-    gload(0);
-    lstore(0);
-    gload(1);
-  }
-  __syncthreads();
-  for (int blk = 0; blk < nblk; ++blk) {
-    const int kb = blk * BN;
-    const bf16_t *ks = smem + (blk & 1) * (KBUF + VBUF), *vs = ks + KBUF;
-    if (kb < wave_kend) {  // else every row of this wave masks the block
-      f32x16_t s[RT][2];
+  // --- pieces of a step
+  auto kfrags = [&](const bf16_t *ks, bf16x8_t (&ka)[4]) __attribute__((always_inline)) {
 #pragma unroll
-      for (int kt = 0; kt < 2; ++kt) {
-        bf16x8_t ka[4];
+    for (int t = 0; t < 4; ++t) ka[t] = *(const bf16x8_t *)(ks + r32 * KP16 + 16 * t + 8 * hf);
+  };
+  // V^T fragments of the 32 keys at LDS rows vs: key slot j of 16-key chunk u
+  // is key 16u + (j/4)*8 + 4hf + j%4, matching the S^T register order
+  auto vfrags = [&](const bf16_t *vs, bf16x8_t (&va)[2][2]) __attribute__((always_inline)) {
 #pragma unroll
-        for (int t = 0; t < 4; ++t)
-          ka[t] = *(const bf16x8_t *)(ks + (kt * 32 + r32) * KP16 + 16 * t + 8 * hf);
+    for (int u = 0; u < 2; ++u) {
+      const bf16_t *vsl = vs + 16 * u * VP16 + tr_off;
 #pragma unroll
-        for (int rt = 0; rt < RT; ++rt) {
-          s[rt][kt] = f32x16_t{};
-#pragma unroll
-          for (int t = 0; t < 4; ++t)
-            s[rt][kt] =
-                __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka[t], qreg[rt][t], s[rt][kt], 0, 0, 0);
-        }
+      for (int dt = 0; dt < 2; ++dt) {
+        const bf16x4_t lo = tr16(vsl + 32 * dt);
+        const bf16x4_t hi = tr16(vsl + 8 * VP16 + 32 * dt);
+        va[u][dt] = bf16x8_t{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
       }
-      const bool masked = kb + BN > p.seq_kv || (p.causal && kb + BN - 1 > q_wave0 + p.seq_offset);
-      bf16x8_t pb[RT][2][2];  // [row tile][kt][u]
+    }
+  };
+  auto scores = [&](const bf16x8_t (&ka)[4], f32x16_t (&s)[RT]) __attribute__((always_inline)) {
 #pragma unroll
-      for (int rt = 0; rt < RT; ++rt) {
-        if (masked) {
+    for (int rt = 0; rt < RT; ++rt) {
+      s[rt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka[0], qreg[rt][0], f32x16_t{}, 0, 0, 0);
 #pragma unroll
-          for (int kt = 0; kt < 2; ++kt)
+      for (int t = 1; t < 4; ++t)
+        s[rt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka[t], qreg[rt][t], s[rt], 0, 0, 0);
+    }
+  };
+  auto pv = [&](const bf16x8_t (&va)[2][2], const bf16x8_t (&pb)[RT][2])
+      __attribute__((always_inline)) {
 #pragma unroll
-            for (int i = 0; i < 16; ++i) {
-              const int key = kb + kt * 32 + (i >> 2) * 8 + hf * 4 + (i & 3);
-              if (key >= p.seq_kv || key > qlimit[rt]) s[rt][kt][i] = -INFINITY;
-            }
-        }
-        float mx = s[rt][0][0];
+    for (int u = 0; u < 2; ++u)
 #pragma unroll
-        for (int kt = 0; kt < 2; ++kt)
+      for (int dt = 0; dt < 2; ++dt)
 #pragma unroll
-          for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[rt][kt][i]);
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-        // lazy rescale: move the reference max only when it grew by > 2^8 in
-        // probability (exp2 units); p = exp2((s - m) c) then stays <= 2^8
-        const float m_new = fmaxf(m[rt], mx);
-        const bool grow = (m_new - m[rt]) * c > kRescaleLog2;  // m = -inf, m_new finite -> true
-        if (__any(grow)) {
-          const float alpha = grow ? __builtin_amdgcn_exp2f((m[rt] - m_new) * c) : 1.f;
-          if (grow) m[rt] = m_new;
-          l[rt] *= alpha;
+        for (int rt = 0; rt < RT; ++rt)
+          o[rt][dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va[u][dt], pb[rt][u], o[rt][dt], 0, 0, 0);
+  };
+  // p = exp2(s * c - mc) as bf16 MFMA operands and the row sum of those bf16 values
+  auto exps = [&](const f32x16_t &s, float mc, bf16x8_t (&pb)[2], float &rs)
+      __attribute__((always_inline)) {
+    float r2[2] = {0.f, 0.f};  // two chains: the sum is needed early by the check
 #pragma unroll
-          for (int dt = 0; dt < 2; ++dt)
+    for (int u = 0; u < 2; ++u) {
 #pragma unroll
-            for (int i = 0; i < 16; ++i) o[rt][dt][i] *= alpha;
-        }
-        const float mc = (m[rt] == -INFINITY) ? 0.f : m[rt] * c;  // no visible key yet
-        float rs = 0.f;  // row sum of the bf16 P the MFMA consumes
+      for (int j = 0; j < 8; ++j) pb[u][j] = (__bf16)__builtin_amdgcn_exp2f(fmaf(s[8 * u + j], c, -mc));
 #pragma unroll
-        for (int kt = 0; kt < 2; ++kt)
+      for (int j = 0; j < 4; ++j)
+        r2[u] = __builtin_amdgcn_fdot2_f32_bf16(bf16x2_t{pb[u][2 * j], pb[u][2 * j + 1]}, ones,
+                                                r2[u], false);
+    }
+    rs = r2[0] + r2[1];
+  };
+  // causal / tail mask of tile t (keys kb..kb+31) in place
+  auto mask = [&](int t, f32x16_t (&sc)[RT]) __attribute__((always_inline)) {
+    const int kb = 32 * t;
+    if (kb + 32 > p.seq_kv || (p.causal && kb + 31 > q_wave0 + p.seq_offset)) {
 #pragma unroll
-          for (int u = 0; u < 2; ++u) {
+      for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
-            for (int j = 0; j < 8; ++j)
-              pb[rt][kt][u][j] =
-                  (__bf16)__builtin_amdgcn_exp2f(fmaf(s[rt][kt][8 * u + j], c, -mc));
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-              rs = __builtin_amdgcn_fdot2_f32_bf16(
-                  bf16x2_t{pb[rt][kt][u][2 * j], pb[rt][kt][u][2 * j + 1]}, ones, rs, false);
-          }
-        l[rt] += rs;
-      }
-      // O^T += V^T P^T over keys 32kt + 16u + (j/4)*8 + 4hf + j%4 (slot j); each
-      // V^T fragment feeds the RT row tiles
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          const bf16_t *vsl = vs + (32 * kt + 16 * u) * VP16 + tr_off;
-#pragma unroll
-          for (int dt = 0; dt < 2; ++dt) {
-            const bf16x4_t lo = tr16(vsl + 32 * dt);
-            const bf16x4_t hi = tr16(vsl + 8 * VP16 + 32 * dt);
-            const bf16x8_t a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-#pragma unroll
-            for (int rt = 0; rt < RT; ++rt)
-              o[rt][dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb[rt][kt][u], o[rt][dt], 0, 0, 0);
-          }
+        for (int i = 0; i < 16; ++i) {
+          const int key = kb + (i >> 2) * 8 + hf * 4 + (i & 3);
+          if (key >= p.seq_kv || key > qlimit[rt]) sc[rt][i] = -INFINITY;
         }
     }
-    if (blk + 1 < nblk) lstore((blk + 1) & 1);  // that buffer was last read in block blk-1
-    gload(blk + 2);                             // clamped: same loads on every path
-    __syncthreads();
+  };
+  // exact path for row tile rt (rare): move the reference max to the true
+  // running max when it grew by more than 2^8 in probability (or was -inf),
+  // rescale O and l, recompute P.  s holds raw scores, masked = -inf.
+  auto fixup = [&](int rt, const f32x16_t &s, bf16x8_t (&pb)[2], float &rs)
+      __attribute__((always_inline)) {
+    float mx = s[0];
+#pragma unroll
+    for (int i = 1; i < 16; ++i) mx = fmaxf(mx, s[i]);
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float m_true = fmaxf(m[rt], mx);  // -inf while nothing is visible
+    const bool move = m[rt] == -INFINITY || (m_true - m[rt]) * c > kRescaleLog2;
+    const float m_new = move ? m_true : m[rt];
+    const float mn = m_new == -INFINITY ? 0.f : m_new;
+    const float alpha = __builtin_amdgcn_exp2f((m[rt] - mn) * c);  // m = -inf -> 0
+    l[rt] *= alpha;
+#pragma unroll
+    for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) o[rt][dt][i] *= alpha;
+    m[rt] = m_new;
+    exps(s, mn * c, pb, rs);
+  };
+  auto finish = [&](int ok, const f32x16_t (&sc)[RT], bf16x8_t (&pb)[RT][2], float (&rs)[RT])
+      __attribute__((always_inline)) {
+    if (!__all(ok)) {
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) fixup(rt, sc[rt], pb[rt], rs[rt]);
+    }
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) l[rt] += rs[rt];
+  };
+
+  // step t (1 <= t): O += V_{t-1}^T P_{t-1} (V rows vs), scores of tile t+1
+  // (K rows ks) into sn, softmax of tile t (sc) into pc, all in one basic
+  // block.  Tiles past the wave's causal range are all -inf: P = 0.
+  auto step = [&](auto masked_tag, int t, const bf16_t *vs, const bf16_t *ks, f32x16_t (&sc)[RT],
+                  f32x16_t (&sn)[RT], const bf16x8_t (&pp)[RT][2], bf16x8_t (&pc)[RT][2])
+      __attribute__((always_inline)) {
+    constexpr bool MASKED = decltype(masked_tag)::value;
+    if (!MASKED) {
+    } else if (t >= ntw) {
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) sc[rt][i] = -INFINITY;
+    } else {
+      mask(t, sc);
+    }
+    bf16x8_t va[2][2], ka[4];
+    vfrags(vs, va);
+    kfrags(ks, ka);
+    pv(va, pp);
+    scores(ka, sn);
+    float rs[RT];
+    int ok = 1;
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+      exps(sc[rt], m[rt] * c, pc[rt], rs[rt]);  // m = -inf: inf/NaN -> fixup
+      ok = ok && rs[rt] <= kSumLimit;
+    }
+#if BN_PIPE_SCHED
+    // LDS reads first, then one MFMA every few VALU instructions
+    __builtin_amdgcn_sched_group_barrier(0x100, 12, 0);
+    __builtin_amdgcn_sched_group_barrier(0x002, BN_PIPE_V0, 0);
+#pragma unroll
+    for (int i = 0; i < 8 * RT; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, BN_PIPE_V1, 0);
+    }
+#endif
+    finish(ok, sc, pc, rs);
+  };
+
+  f32x16_t sa[RT], sb[RT];
+  bf16x8_t pa[RT][2], pbb[RT][2];
+  if (nblk > 0) {
+    gload_k(0);
+    gload_v(0);
+    lstore_k(0);
+    lstore_v(0);
+    gload_k(1);
+    gload_v(1);
+    lstore_k(1);
+    gload_k(2);
   }
+  __syncthreads();
+  if (ntw > 0) {  // step 0: scores of tiles 0 and 1, softmax of tile 0
+    bf16x8_t ka[4];
+    kfrags(kring, ka);
+    scores(ka, sa);
+    kfrags(kring + 32 * KP16, ka);
+    scores(ka, sb);
+    mask(0, sa);
+    float rs[RT];
+    int ok = 1;
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+      exps(sa[rt], m[rt] * c, pa[rt], rs[rt]);  // m = -inf: inf/NaN -> fixup
+      ok = ok && rs[rt] <= kSumLimit;
+    }
+    finish(ok, sa, pa, rs);
+  }
+  // iteration j: steps 2j+1 (P of tile 2j, scores of 2j+2, softmax of 2j+1)
+  // and 2j+2 (P of 2j+1, scores of 2j+3, softmax of 2j+2).  The leading
+  // iterations whose tiles every wave sees whole (no causal or tail mask)
+  // run a step without any mask code.
+  const int wg_first = w.mt * WGROWS;
+  const int t_safe = max(0, p.causal ? min((wg_first + p.seq_offset + 1) / 32, p.seq_kv / 32)
+                                     : p.seq_kv / 32);
+  const int j_safe = min(nblk, max(0, (t_safe - 1) / 2));
+  auto iteration = [&](auto masked_tag, int j) __attribute__((always_inline)) {
+    const bf16_t *vc = vring + (j & 1) * VBUF;
+    const bf16_t *kn = kring + ((j + 1) & 1) * KBUF;
+    step(masked_tag, 2 * j + 1, vc, kn, sb, sa, pa, pbb);
+    step(masked_tag, 2 * j + 2, vc + 32 * VP16, kn + 32 * KP16, sa, sb, pbb, pa);
+    lstore_k(j & 1);        // K_{j+2} into K_j's buffer (K_j last read in iteration j-1)
+    lstore_v((j + 1) & 1);  // V_{j+1} into V_{j-1}'s buffer
+    gload_k(j + 3);         // rows past seq_kv read as 0
+    gload_v(j + 2);
+    __syncthreads();
+  };
+  int j = 0;
+  for (; j < j_safe; ++j) iteration(std::false_type{}, j);
+  for (; j < nblk; ++j) iteration(std::true_type{}, j);
 
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
@@ -513,10 +655,16 @@ extern "C" int bn_gqa_prefill(int dtype, const void *q, const void *k, const voi
       kv_batch_stride % vec || o_batch_stride % vec)
     return fail(BN_ERR_UNSUPPORTED,
                 std::string(op) + ": pointers must be 16-byte aligned and strides multiples of 16 bytes");
+  // bf16 K/V blocks are fetched through 32-bit buffer ranges of 64 rows
+  if (dtype == BN_BF16 && kv_row_stride >= ((int64_t)1 << 24))
+    return fail(BN_ERR_UNSUPPORTED, std::string(op) + ": bf16 K/V row stride must be below 2^24 elements");
   // bf16: two 32-row tiles per wave (every LDS fragment feeds two MFMAs) when
   // that still leaves >= 2048 workgroups (8 per CU); one tile otherwise, so
   // short sequences keep enough workgroups in flight
-  const int rt16 = ((int64_t)batch * n_heads * ((seq_q + 255) / 256) >= 2048) ? 2 : 1;
+#ifndef BN_RT2_MIN_WG
+#define BN_RT2_MIN_WG 2048
+#endif
+  const int rt16 = ((int64_t)batch * n_heads * ((seq_q + 255) / 256) >= BN_RT2_MIN_WG) ? 2 : 1;
   const int rows_per_wg = dtype == BN_BF16 ? 4 * 32 * rt16 : BM;
   const int n_mt = (seq_q + rows_per_wg - 1) / rows_per_wg;
   const int64_t n_wg = (int64_t)batch * n_heads * n_mt;
@@ -534,12 +682,12 @@ extern "C" int bn_gqa_prefill(int dtype, const void *q, const void *k, const voi
   p.causal = causal ? 1 : 0; p.seq_offset = seq_offset;
   p.c = scale * 1.4426950408889634f;
   hipStream_t s = as_stream(stream);
-  if (dtype == BN_BF16)
+  if (dtype == BN_BF16) {
     if (rt16 == 2)
-      hipLaunchKernelGGL(prefill_bf16_kernel<2>, dim3((unsigned)n_wg), dim3(256), 0, s, p);
+      hipLaunchKernelGGL((prefill_bf16_kernel<2, BN_PIPE_OCC2>), dim3((unsigned)n_wg), dim3(256), 0, s, p);
     else
-      hipLaunchKernelGGL(prefill_bf16_kernel<1>, dim3((unsigned)n_wg), dim3(256), 0, s, p);
-  else
+      hipLaunchKernelGGL((prefill_bf16_kernel<1, BN_PIPE_OCC1>), dim3((unsigned)n_wg), dim3(256), 0, s, p);
+  } else
     hipLaunchKernelGGL(prefill_f32_kernel, dim3((unsigned)n_wg), dim3(256), 0, s, p);
   BN_LAUNCH_CHECK();
   return BN_OK;

@@ -96,6 +96,7 @@ def prefill_args(**kw):
     (dict(q=0), B.BN_ERR_INVALID_ARG),
     (dict(scale=-1.0), B.BN_ERR_INVALID_ARG),
     (dict(scale=float("nan")), B.BN_ERR_INVALID_ARG),
+    (dict(seq_kv=8, kvrs=1 << 24, kvbs=8 << 24), B.BN_ERR_UNSUPPORTED),  # bf16 K/V stride >= 2^24
 ])
 def test_prefill_validation(kw, status):
     s, m = st("bn_gqa_prefill", *prefill_args(**kw))

@@ -112,6 +112,22 @@ def test_prefill_baseline_shape(dtype):
         assert_close(got[b:b + 1, :, h:h + 1], ref, TOL[dtype], f"b={b} h={h}")
 
 
+@pytest.mark.parametrize("growth", [1 / 8, -1 / 600])
+def test_prefill_score_jumps(growth):
+    """Scores that grow along the sequence (K row j scaled by 1 + growth*j) take
+    the kernel's exact rescale path many times (later keys exceed the first
+    tile's max by far more than 2^16 in probability); shrinking scores make the
+    first keys dominate and later ones underflow.  Both must match the oracle."""
+    Bn, S, H, Hkv = 1, 600, 8, 2
+    q = draw((Bn, S, H, 64), 11, "bf16")
+    k = draw((Bn, S, Hkv, 64), 12, "f32") * (1 + growth * np.arange(S))[None, :, None, None]
+    k = bf16_round(k.astype(np.float32))
+    v = draw((Bn, S, Hkv, 64), 13, "bf16")
+    o = B.gqa_prefill(dev(q, torch.bfloat16), dev(k, torch.bfloat16), dev(v, torch.bfloat16),
+                      scale=0.125)
+    assert_close(host(o), O.gqa_prefill(q, k, v, 0.125, True, 0), BF16_TOL, f"growth {growth}")
+
+
 def test_prefill_zero_query_prefix_means():
     # size-independent property at the full shape: Q = 0 -> row i is mean(V[0..i])
     Bn, S, H, Hkv = 4, 2048, 32, 4
