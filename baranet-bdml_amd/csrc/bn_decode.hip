@@ -30,18 +30,6 @@ constexpr int HD = 64;
 constexpr int NT = 4;  // keys per lane group between softmax rescales
 
 template <typename T> struct DecVec;
-template <> struct DecVec<bf16_t> {
-  static constexpr int VEC = 8;
-  __device__ static __forceinline__ void load(const bf16_t *p, float (&v)[8]) {
-    const uint4 t = *reinterpret_cast<const uint4 *>(p);
-    const uint32_t u[4] = {t.x, t.y, t.z, t.w};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      v[2 * i] = __uint_as_float(u[i] << 16);
-      v[2 * i + 1] = __uint_as_float(u[i] & 0xffff0000u);
-    }
-  }
-};
 template <> struct DecVec<float> {
   static constexpr int VEC = 4;
   __device__ static __forceinline__ void load(const float *p, float (&v)[4]) {
@@ -452,8 +440,9 @@ __device__ __forceinline__ dbf16x4_t lds_read_tr16(const bf16_t *p) {
 
 template <int G>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(BN_DECODE_ROWS_WAVES))) void decode_bf16_rows_kernel(DecodeParams p) {
-  __shared__ __attribute__((aligned(16))) bf16_t KL[TK * RKP];
-  __shared__ __attribute__((aligned(16))) bf16_t VL[TK * RVP];
+  // two tile buffers: one barrier per tile orders the LDS writes and reads
+  __shared__ __attribute__((aligned(16))) bf16_t KL[2][TK * RKP];
+  __shared__ __attribute__((aligned(16))) bf16_t VL[2][TK * RVP];
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int l16 = lane & 15, grp = lane >> 4;
@@ -504,25 +493,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(BN_DECODE_R
     r.k2 = *(const u32x4 *)(Kr + o2); r.v2 = *(const u32x4 *)(Vr + o2);
     r.k3 = *(const u32x4 *)(Kr + o3); r.v3 = *(const u32x4 *)(Vr + o3);
   };
-  auto lstore = [&](const RegTile &r) __attribute__((always_inline)) {
-    *(u32x4 *)(KL + crow * RKP + ccol) = r.k0;
-    *(u32x4 *)(KL + (crow + 8) * RKP + ccol) = r.k1;
-    *(u32x4 *)(KL + (crow + 16) * RKP + ccol) = r.k2;
-    *(u32x4 *)(KL + (crow + 24) * RKP + ccol) = r.k3;
-    *(u32x4 *)(VL + crow * RVP + ccol) = r.v0;
-    *(u32x4 *)(VL + (crow + 8) * RVP + ccol) = r.v1;
-    *(u32x4 *)(VL + (crow + 16) * RVP + ccol) = r.v2;
-    *(u32x4 *)(VL + (crow + 24) * RVP + ccol) = r.v3;
+  auto lstore = [&](const RegTile &r, int buf) __attribute__((always_inline)) {
+    bf16_t *kd = KL[buf], *vd = VL[buf];
+    *(u32x4 *)(kd + crow * RKP + ccol) = r.k0;
+    *(u32x4 *)(kd + (crow + 8) * RKP + ccol) = r.k1;
+    *(u32x4 *)(kd + (crow + 16) * RKP + ccol) = r.k2;
+    *(u32x4 *)(kd + (crow + 24) * RKP + ccol) = r.k3;
+    *(u32x4 *)(vd + crow * RVP + ccol) = r.v0;
+    *(u32x4 *)(vd + (crow + 8) * RVP + ccol) = r.v1;
+    *(u32x4 *)(vd + (crow + 16) * RVP + ccol) = r.v2;
+    *(u32x4 *)(vd + (crow + 24) * RVP + ccol) = r.v3;
   };
   RegTile ta, tb;
 
   float m = -INFINITY, l = 0.f;
   df32x4_t o[4] = {df32x4_t{}, df32x4_t{}, df32x4_t{}, df32x4_t{}};
   const float c = p.c;
-  const bf16_t *kl = KL + wave * HD + 8 * grp;  // this wave's head inside the tile
-  const bf16_t *vl = VL + wave * HD;
-
-  auto compute = [&](int kb) __attribute__((always_inline)) {
+  auto compute = [&](int kb, int buf) __attribute__((always_inline)) {
+    const bf16_t *kl = KL[buf] + wave * HD + 8 * grp;  // this wave's head inside the tile
+    const bf16_t *vl = VL[buf] + wave * HD;
     df32x4_t s[2];
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
@@ -572,21 +561,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(BN_DECODE_R
     }
   };
 
+  // tile ti lives in LDS buffer ti & 1 and in register tile ta (even) / tb
+  // (odd), loaded two tiles ahead.  Writing buffer x for tile t happens after
+  // the barrier that follows the reads of tile t-2 (same buffer).
   gload(ta, 0);
   gload(tb, 1);
+  lstore(ta, 0);
+  gload(ta, 2);
+  __syncthreads();
   for (int ti = 0; ti < ntiles; ti += 2) {
-    __syncthreads();  // every wave is done with the previous tile
-    lstore(ta);
-    __syncthreads();
-    gload(ta, ti + 2);
-    compute(k_begin + TK * ti);
+    compute(k_begin + TK * ti, 0);
     if (ti + 1 < ntiles) {  // workgroup-uniform
+      lstore(tb, 1);
+      gload(tb, ti + 3);
       __syncthreads();
-      lstore(tb);
+      compute(k_begin + TK * (ti + 1), 1);
+      lstore(ta, 0);
+      gload(ta, ti + 4);
       __syncthreads();
-      compute(k_begin + TK * (ti + 1));
     }
-    gload(tb, ti + 3);
   }
 
   // o[dt][i] = O^T[d = 16dt + 4grp + i][query head g*G + l16]; m is uniform over lane groups
@@ -609,50 +602,57 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(BN_DECODE_R
 // pass (running log-sum-exp), four chunks' loads in flight at a time.
 template <typename T>
 __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeParams p) {
+  // one thread per 4 consecutive d of one (sequence, head); the partial loads
+  // of 8 chunks are issued together with the length load (slots past the
+  // valid chunks read an in-range partial and get weight 0)
   const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (idx >= (int64_t)p.batch * p.n_heads * HD) return;
-  const int d = (int)(idx % HD);
-  const int64_t bh = idx / HD;
+  if (idx >= (int64_t)p.batch * p.n_heads * (HD / 4)) return;
+  const int d0 = (int)(idx % (HD / 4)) * 4;
+  const int64_t bh = idx / (HD / 4);
   const int b = (int)(bh / p.n_heads);
-  int len = p.lens[b];
-  len = len < 0 ? 0 : (len > p.max_len ? p.max_len : len);
-  const int nvalid = (len + p.chunk - 1) / p.chunk;
   const float *part = p.ws + bh * p.n_split * (HD + 2);
-  // every chunk below nvalid holds at least one key, so its max is finite
-  float M = -INFINITY, L = 0.f, A = 0.f;
-  int s = 0;
-  for (; s + 4 <= nvalid; s += 4) {
-    float ms[4], ls[4], as[4];
+  float ms[8], ls[8];
+  float4 as[8];
+  auto load8 = [&](int s0) __attribute__((always_inline)) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const float *ps = part + (s + j) * (HD + 2);
-      ms[j] = ps[0];
-      ls[j] = ps[1];
-      as[j] = ps[2 + d];
+    for (int j = 0; j < 8; ++j) {
+      const float *ps = part + min(s0 + j, p.n_split - 1) * (HD + 2);
+      const float2 ml = *reinterpret_cast<const float2 *>(ps);  // 264-byte records: 8-byte aligned
+      ms[j] = ml.x;
+      ls[j] = ml.y;
+      as[j] = make_float4(ps[2 + d0], ps[3 + d0], ps[4 + d0], ps[5 + d0]);
     }
-    const float Mn = fmaxf(fmaxf(M, fmaxf(ms[0], ms[1])), fmaxf(ms[2], ms[3]));
-    const float fo = __builtin_amdgcn_exp2f(M - Mn);  // M = -inf -> 0
+  };
+  int len = p.lens[b];
+  load8(0);
+  len = len < 0 ? 0 : (len > p.max_len ? p.max_len : len);
+  const int nvalid = (len + p.chunk - 1) / p.chunk;  // chunks holding keys (finite max)
+  float M = -INFINITY, L = 0.f, A[4] = {0.f, 0.f, 0.f, 0.f};
+  auto merge8 = [&](int s0) __attribute__((always_inline)) {
+    float mx = M;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) mx = s0 + j < nvalid ? fmaxf(mx, ms[j]) : mx;
+    const float mu = mx == -INFINITY ? 0.f : mx;       // nothing valid yet: weights stay 0
+    const float fo = __builtin_amdgcn_exp2f(M - mu);  // M = -inf -> 0
     L *= fo;
-    A *= fo;
+    A[0] *= fo; A[1] *= fo; A[2] *= fo; A[3] *= fo;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const float f = __builtin_amdgcn_exp2f(ms[j] - Mn);
+    for (int j = 0; j < 8; ++j) {
+      const float f = s0 + j < nvalid ? __builtin_amdgcn_exp2f(ms[j] - mu) : 0.f;
       L += ls[j] * f;
-      A += as[j] * f;
+      A[0] += as[j].x * f; A[1] += as[j].y * f; A[2] += as[j].z * f; A[3] += as[j].w * f;
     }
-    M = Mn;
+    M = mx;
+  };
+  merge8(0);  // the first 8 chunks need no branch on the length
+  for (int s0 = 8; s0 < nvalid; s0 += 8) {
+    load8(s0);
+    merge8(s0);
   }
-  for (; s < nvalid; ++s) {
-    const float *ps = part + s * (HD + 2);
-    const float ms = ps[0];
-    const float Mn = fmaxf(M, ms);
-    const float fo = __builtin_amdgcn_exp2f(M - Mn), f = __builtin_amdgcn_exp2f(ms - Mn);
-    L = L * fo + ps[1] * f;
-    A = A * fo + ps[2 + d] * f;
-    M = Mn;
-  }
-  const float out = L > 0.f ? A / L : 0.f;  // empty sequence -> zeros
-  Elem<T>::store((T *)p.o + idx, out);
+  const float inv = L > 0.f ? 1.0f / L : 0.f;  // empty sequence -> zeros
+  T *out = (T *)p.o + bh * HD + d0;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) Elem<T>::store(out + e, A[e] * inv);
 }
 
 #ifndef BN_DECODE_MIN_WG
@@ -696,7 +696,7 @@ int launch_decode(const DecodeParams &p, int G, hipStream_t s) {
     default: launch_split<T, 8>(p, grid, s); break;
   }
   BN_LAUNCH_CHECK();
-  const int64_t n = (int64_t)p.batch * p.n_heads * HD;
+  const int64_t n = (int64_t)p.batch * p.n_heads * (HD / 4);
   hipLaunchKernelGGL(decode_combine_kernel<T>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
                      s, p);
   BN_LAUNCH_CHECK();

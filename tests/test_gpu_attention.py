@@ -171,6 +171,29 @@ def test_decode_vs_oracle(case, dtype):
         assert_close(got[b:b + 1], ref, TOL[dtype], f"decode b={b} len={Lb}")
 
 
+@pytest.mark.parametrize("dtype,Hkv", [("bf16", 4), ("bf16", 2), ("f32", 4)])
+def test_decode_workspace_reuse(dtype, Hkv):
+    """One workspace across calls of different batches and lengths (the
+    whole-row, per-head and fp32 kernels): every result matches the oracle."""
+    H, L = 8 * Hkv, 1500
+    ws = B.decode_workspace(6, L, H)
+    for call, lens in enumerate([[1500, 700, 1, 129, 1024, 0], [33, 1500], [1499, 2, 900, 640]]):
+        Bn = len(lens)
+        q = draw((Bn, H, 64), 20 + call, dtype)
+        kc = draw((Bn, L, Hkv, 64), 30 + call, dtype)
+        vc = draw((Bn, L, Hkv, 64), 40 + call, dtype)
+        ld = torch.tensor(lens, dtype=torch.int32, device="cuda")
+        got = host(B.gqa_decode(dev(q, TD[dtype]), dev(kc, TD[dtype]), dev(vc, TD[dtype]), ld,
+                                scale=0.125, workspace=ws))
+        for b, Lb in enumerate(lens):
+            if Lb == 0:
+                assert np.all(got[b] == 0.0)
+                continue
+            ref = O.gqa_decode(q[b:b + 1], kc[b:b + 1, :Lb], vc[b:b + 1, :Lb],
+                               np.array([Lb], np.int32), 0.125)
+            assert_close(got[b:b + 1], ref, TOL[dtype], f"call {call} b={b} len={Lb}")
+
+
 @pytest.mark.parametrize("ragged", [False, True])
 def test_decode_baseline_shape(ragged):
     """B=64, bf16 cache of 4096, 32/4 heads; ragged lengths in [512, 4096]."""
