@@ -27,7 +27,7 @@ namespace bn {
 namespace {
 
 constexpr int HD = 64;
-constexpr int NT = 4;  // keys per lane group between softmax rescales
+constexpr int NT = 8;  // keys per lane group between softmax rescales
 
 template <typename T> struct DecVec;
 template <> struct DecVec<float> {
@@ -38,6 +38,24 @@ template <> struct DecVec<float> {
   }
 };
 
+// Sum over each group of N (8 or 16) consecutive lanes with DPP moves inside
+// a 16-lane row (no LDS round trip): quad xor 1, quad xor 2, half-row mirror
+// (lane i <-> 7 - i), row mirror (lane i <-> 15 - i); every lane gets the sum.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL,
+                                                               0xf, 0xf, false));
+}
+template <int N>
+__device__ __forceinline__ float row_sum(float x) {
+  static_assert(N == 8 || N == 16, "8 or 16 lanes");
+  x += dpp_mov<0xB1>(x);   // quad_perm 1,0,3,2
+  x += dpp_mov<0x4E>(x);   // quad_perm 2,3,0,1
+  x += dpp_mov<0x141>(x);  // row_half_mirror
+  if (N == 16) x += dpp_mov<0x140>(x);  // row_mirror
+  return x;
+}
+
 struct DecodeParams {
   const void *q, *k, *v;
   const int32_t *lens;
@@ -47,26 +65,47 @@ struct DecodeParams {
   float c;  // scale * log2(e)
 };
 
-template <typename T, int G>
-__global__ __launch_bounds__(256) void decode_split_kernel(DecodeParams p) {
+// WV waves per workgroup.  SINGLE (G = 1): one workgroup per (sequence,
+// query head) covers the whole cache of its KV head (each wave a contiguous
+// key range) and writes the output itself -- no partials, no combine launch;
+// for short caches and few sequences, where the split version is
+// latency-bound.  The workgroups of one KV head read the same cache rows
+// (from L2 after the first), each doing 1/G of the arithmetic.
+template <typename T, int G, int WV, bool SINGLE>
+__global__ __launch_bounds__(64 * WV) void decode_split_kernel(DecodeParams p) {
   constexpr int VEC = DecVec<T>::VEC;
   constexpr int LPK = HD / VEC;  // lanes per key
   constexpr int KPI = 64 / LPK;  // keys per wave per load instruction
-  __shared__ float red_m[4][G], red_l[4][G];
-  __shared__ float red_o[4][G][HD];
+  __shared__ float red_m[WV][G], red_l[WV][G];
+  __shared__ float red_o[WV][G][HD];
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int sub = lane % LPK;  // 16-byte slice of the key row
   const int grp = lane / LPK;  // key slot within the wave
-  const int split = blockIdx.x % p.n_split;
-  const int bg = blockIdx.x / p.n_split;
-  const int b = bg / p.n_kv_heads, g = bg % p.n_kv_heads;
+  static_assert(!SINGLE || G == 1, "single pass: one query head per workgroup");
+  const int split = SINGLE ? 0 : blockIdx.x % p.n_split;
+  const int bg = SINGLE ? blockIdx.x : blockIdx.x / p.n_split;
+  const int units = SINGLE ? p.n_heads : p.n_kv_heads;
+  const int b = bg / units;
+  // KV head g; query heads h0 .. h0 + G - 1
+  const int g = SINGLE ? (bg % units) / (p.n_heads / p.n_kv_heads) : bg % units;
+  const int h0 = SINGLE ? bg % units : g * G;
 
   int len = p.lens[b];
   len = len < 0 ? 0 : (len > p.max_len ? p.max_len : len);
-  const int k_begin = split * p.chunk;
+  if (SINGLE && len == 0) {  // no key: zeros
+    for (int idx = tid; idx < G * HD; idx += 64 * WV)
+      Elem<T>::store((T *)p.o + ((int64_t)b * p.n_heads + h0) * HD + idx, 0.f);
+    return;
+  }
+  const int k_begin = SINGLE ? 0 : split * p.chunk;
   if (k_begin >= len) return;  // the combine kernel ignores chunks past len
-  const int k_end = min(k_begin + p.chunk, len);
+  const int k_end = SINGLE ? len : min(k_begin + p.chunk, len);
+  // SINGLE: wave w takes keys [kw0, kw1), a contiguous range; else the waves
+  // interleave blocks of KPI*NT keys over the chunk
+  const int per = ((k_end - k_begin + WV - 1) / WV + KPI - 1) / KPI * KPI;
+  const int kw0 = SINGLE ? k_begin + wave * per : k_begin + wave * KPI * NT;
+  const int kw1 = SINGLE ? min(kw0 + per, k_end) : k_end;
 
   const int64_t kv_rs = (int64_t)p.n_kv_heads * HD;
   const T *Kb = (const T *)p.k + ((int64_t)b * p.max_len) * kv_rs + (int64_t)g * HD + sub * VEC;
@@ -76,7 +115,7 @@ __global__ __launch_bounds__(256) void decode_split_kernel(DecodeParams p) {
   float qv[G][VEC];
 #pragma unroll
   for (int h = 0; h < G; ++h) {
-    const T *qp = (const T *)p.q + ((int64_t)b * p.n_heads + g * G + h) * HD + sub * VEC;
+    const T *qp = (const T *)p.q + ((int64_t)b * p.n_heads + h0 + h) * HD + sub * VEC;
     DecVec<T>::load(qp, qv[h]);
 #pragma unroll
     for (int e = 0; e < VEC; ++e) qv[h][e] *= p.c;
@@ -91,20 +130,18 @@ __global__ __launch_bounds__(256) void decode_split_kernel(DecodeParams p) {
     for (int e = 0; e < VEC; ++e) acc[h][e] = 0.f;
   }
 
-  // keys of this wave: k_begin + wave*KPI*NT + it*4*KPI*NT ..., slot grp
-  const int step = 4 * KPI * NT;
-  for (int base = k_begin + wave * KPI * NT; base < k_end; base += step) {
+  const int step = SINGLE ? KPI * NT : WV * KPI * NT;
+  for (int base = kw0; base < kw1; base += step) {
+    // K and V of the NT keys of this lane group are requested together (one
+    // memory round trip per NT keys); keys past the chunk read the chunk's
+    // last row (initialised data, finite) and are masked to P = 0
     float s[G][NT];
-    float kvv[NT][VEC];
+    float kk[NT][VEC], vv[NT][VEC];
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
-      const int key = base + t * KPI + grp;
-      if (key < k_end) {
-        DecVec<T>::load(Kb + (int64_t)key * kv_rs, kvv[t]);
-      } else {
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) kvv[t][e] = 0.f;
-      }
+      const int key = min(base + t * KPI + grp, kw1 - 1);
+      DecVec<T>::load(Kb + (int64_t)key * kv_rs, kk[t]);
+      DecVec<T>::load(Vb + (int64_t)key * kv_rs, vv[t]);
     }
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
@@ -113,21 +150,9 @@ __global__ __launch_bounds__(256) void decode_split_kernel(DecodeParams p) {
       for (int h = 0; h < G; ++h) {
         float d = 0.f;
 #pragma unroll
-        for (int e = 0; e < VEC; ++e) d = fmaf(qv[h][e], kvv[t][e], d);
-#pragma unroll
-        for (int msk = 1; msk < LPK; msk <<= 1) d += __shfl_xor(d, msk, 64);
-        s[h][t] = key < k_end ? d : -INFINITY;
-      }
-    }
-    // values for the same keys (zeros past the end: 0 * garbage must not be NaN)
-#pragma unroll
-    for (int t = 0; t < NT; ++t) {
-      const int key = base + t * KPI + grp;
-      if (key < k_end) {
-        DecVec<T>::load(Vb + (int64_t)key * kv_rs, kvv[t]);
-      } else {
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) kvv[t][e] = 0.f;
+        for (int e = 0; e < VEC; ++e) d = fmaf(qv[h][e], kk[t][e], d);
+        d = row_sum<LPK>(d);
+        s[h][t] = key < kw1 ? d : -INFINITY;
       }
     }
 #pragma unroll
@@ -150,7 +175,7 @@ __global__ __launch_bounds__(256) void decode_split_kernel(DecodeParams p) {
       for (int e = 0; e < VEC; ++e) {
         float a = acc[h][e] * alpha;
 #pragma unroll
-        for (int t = 0; t < NT; ++t) a = fmaf(pt[t], kvv[t][e], a);
+        for (int t = 0; t < NT; ++t) a = fmaf(pt[t], vv[t][e], a);
         acc[h][e] = a;
       }
     }
@@ -185,21 +210,26 @@ __global__ __launch_bounds__(256) void decode_split_kernel(DecodeParams p) {
   }
   __syncthreads();
 
-  // merge the 4 waves and write this chunk's partial (m, l, acc[HD]) per head
-  for (int idx = tid; idx < G * HD; idx += 256) {
+  // merge the waves and write this chunk's partial (m, l, acc[HD]) per head,
+  // or (SINGLE) the output
+  for (int idx = tid; idx < G * HD; idx += 64 * WV) {
     const int h = idx / HD, d = idx % HD;
     float M = red_m[0][h];
 #pragma unroll
-    for (int w2 = 1; w2 < 4; ++w2) M = fmaxf(M, red_m[w2][h]);
+    for (int w2 = 1; w2 < WV; ++w2) M = fmaxf(M, red_m[w2][h]);
     const float Mu = M == -INFINITY ? 0.f : M;
     float L = 0.f, A = 0.f;
 #pragma unroll
-    for (int w2 = 0; w2 < 4; ++w2) {
+    for (int w2 = 0; w2 < WV; ++w2) {
       const float f = __builtin_amdgcn_exp2f(red_m[w2][h] - Mu);
       L += red_l[w2][h] * f;
       A += red_o[w2][h][d] * f;
     }
-    float *part = p.ws + (((int64_t)b * p.n_heads + g * G + h) * p.n_split + split) * (HD + 2);
+    if (SINGLE) {
+      Elem<T>::store((T *)p.o + ((int64_t)b * p.n_heads + h0 + h) * HD + d, A / L);
+      continue;
+    }
+    float *part = p.ws + (((int64_t)b * p.n_heads + h0 + h) * p.n_split + split) * (HD + 2);
     part[2 + d] = A;
     if (d == 0) {
       part[0] = M;
@@ -678,11 +708,27 @@ void launch_split(const DecodeParams &p, dim3 grid, hipStream_t s) {
     else
       hipLaunchKernelGGL((decode_bf16_mfma_kernel<G>), grid, dim3(256), 0, s, p);
   } else {
-    hipLaunchKernelGGL((decode_split_kernel<T, G>), grid, dim3(256), 0, s, p);
+    hipLaunchKernelGGL((decode_split_kernel<T, G, 4, false>), grid, dim3(256), 0, s, p);
   }
 }
 
 bool rows_path(const DecodeParams &p, bool bf16) { return bf16 && p.n_kv_heads % 4 == 0; }
+
+#ifndef BN_DECODE_SINGLE_WV
+#define BN_DECODE_SINGLE_WV 16
+#endif
+// fp32 caches of at most this many keys with at most this many (sequence,
+// query head) pairs take the single-pass kernel
+constexpr int kSingleMaxLen = 1024, kSingleMaxUnits = 256;
+bool single_path(int dtype, int batch, int max_len, int n_heads) {
+  return dtype == BN_F32 && max_len <= kSingleMaxLen && (int64_t)batch * n_heads <= kSingleMaxUnits;
+}
+
+void launch_single(const DecodeParams &p, hipStream_t s) {
+  constexpr int WV = BN_DECODE_SINGLE_WV;
+  hipLaunchKernelGGL((decode_split_kernel<float, 1, WV, true>), dim3((unsigned)(p.batch * p.n_heads)),
+                     dim3(64 * WV), 0, s, p);
+}
 
 template <typename T>
 int launch_decode(const DecodeParams &p, int G, hipStream_t s) {
@@ -744,6 +790,18 @@ int bn_gqa_decode(int dtype, const void *q, const void *k_cache, const void *v_c
   DecodeParams p;
   p.q = q; p.k = k_cache; p.v = v_cache; p.lens = seq_lens; p.o = o;
   p.batch = batch; p.max_len = max_len; p.n_heads = n_heads; p.n_kv_heads = n_kv_heads;
+  if (single_path(dtype, batch, max_len, n_heads)) {  // no partials: the workspace is unused
+    p.ws = nullptr;
+    p.n_split = 1;
+    p.chunk = max_len;
+    p.c = scale * 1.4426950408889634f;
+    int st = ensure_device();
+    if (st) return st;
+    hipStream_t s = as_stream(stream);
+    launch_single(p, s);
+    BN_LAUNCH_CHECK();
+    return BN_OK;
+  }
   // the whole-row kernel gives each workgroup 4 KV heads: 1/4 of the workgroups per chunk
   p.chunk = rows_path(p, dtype == BN_BF16)
                 ? choose_chunk(batch, max_len, n_kv_heads / 4, BN_DECODE_ROWS_MIN_WG)

@@ -12,7 +12,10 @@ SwiGLU MLP -> +x, final RMSNorm, lm_head.  The reference keeps no KV cache
 kernel.  Per-head GQA semantics (query head h reads KV head h // 8).
 
 RMSNorm, RoPE, prefill attention and decode attention run on the HIP kernels
-through the C ABI (bnhip).  The dense projections, SwiGLU and the embedding
+through the C ABI (bnhip).  The Q, K and V projections are one GEMM against
+the concatenated weight [hidden, (H + 2*Hkv)*64]; RoPE rotates the Q and K
+columns of its output in place in one launch (same positions for every head
+block), and attention reads Q, K and V as column slices of that row.  The dense projections, SwiGLU and the embedding
 gather are plain torch GPU operations (library GEMMs): they are not part of
 the attention path, and the config's metric times only the attention, RoPE
 and RMSNorm kernels.  ``path_ms`` accumulates hip-event time around those
@@ -62,8 +65,9 @@ class TinyLlama:
         self.embed = w(cfg.vocab_size, h)
         self.layers = []
         for _ in range(cfg.num_hidden_layers):
+            wq, wk, wv = w(h, h), w(h, kv), w(h, kv)
             self.layers.append(dict(
-                ln1=torch.ones((1, h), device="cuda"), wq=w(h, h), wk=w(h, kv), wv=w(h, kv),
+                ln1=torch.ones((1, h), device="cuda"), wqkv=torch.cat([wq, wk, wv], dim=1),
                 wo=w(h, h), ln2=torch.ones((1, h), device="cuda"), wg=w(h, inter), wu=w(h, inter),
                 wd=w(inter, h),
                 k_cache=torch.zeros((1, max_len, cfg.num_key_value_heads, cfg.head_dim), device="cuda"),
@@ -103,16 +107,17 @@ class TinyLlama:
         self._record("rmsnorm", [x, weight], y, eps=self.cfg.rms_norm_eps)
         return y
 
-    def rope(self, x, offset):
-        y = torch.empty_like(x)
+    def rope_(self, x, offset):
+        """RoPE in place on a (possibly strided) [rows, heads*64] view."""
+        before = x.clone() if self.trace is not None else None
 
         def run():
-            bnhip.call("bn_rope", C.byref(bnhip.view(x)), C.byref(bnhip.view(y)), offset,
+            bnhip.call("bn_rope", C.byref(bnhip.view(x)), C.byref(bnhip.view(x)), offset,
                        self.cfg.head_dim, self.cfg.rope_theta, bnhip.stream_of())
         self._timed(run)
-        self._record("rope", [x], y, offset=offset, head_dim=self.cfg.head_dim,
-                     theta=self.cfg.rope_theta)
-        return y
+        self._record("rope", [before] if before is not None else [], x, offset=offset,
+                     head_dim=self.cfg.head_dim, theta=self.cfg.rope_theta)
+        return x
 
     def prefill_attention(self, q, k, v):
         cfg = self.cfg
@@ -140,8 +145,10 @@ class TinyLlama:
         cfg = self.cfg
         n = hdn.shape[0]
         x = self.rmsnorm(hdn, L["ln1"])
-        q, k, v = x @ L["wq"], x @ L["wk"], x @ L["wv"]
-        q, k = self.rope(q, pos0), self.rope(k, pos0)
+        hq, hk = cfg.hidden_size, cfg.num_key_value_heads * cfg.head_dim
+        qkv = x @ L["wqkv"]                       # [n, hq + 2*hk]
+        self.rope_(qkv[:, :hq + hk], pos0)        # Q and K columns, one launch
+        q, k, v = qkv[:, :hq], qkv[:, hq:hq + hk], qkv[:, hq + hk:]
         L["k_cache"][0, pos0:pos0 + n] = k.view(n, cfg.num_key_value_heads, cfg.head_dim)
         L["v_cache"][0, pos0:pos0 + n] = v.view(n, cfg.num_key_value_heads, cfg.head_dim)
         if pos0 == 0:
