@@ -252,7 +252,9 @@ def cpu_baseline_tinyllama(m, ids):
     t0 = time.perf_counter()
     xn = O.rmsnorm(x, w, cfg.rms_norm_eps)
     t_norm = time.perf_counter() - t0
-    q, k, v = xn @ L0["wq"].cpu().numpy(), xn @ L0["wk"].cpu().numpy(), xn @ L0["wv"].cpu().numpy()
+    hq, hk = cfg.hidden_size, cfg.num_key_value_heads * cfg.head_dim
+    qkv = xn @ L0["wqkv"].cpu().numpy()  # the model's fused [hidden, hq + 2*hk] projection
+    q, k, v = qkv[:, :hq].copy(), qkv[:, hq:hq + hk].copy(), qkv[:, hq + hk:].copy()
     S = x.shape[0]
     t0 = time.perf_counter()
     qr, kr = O.rope(q, 0, 64, 1e4), O.rope(k, 0, 64, 1e4)
