@@ -80,50 +80,87 @@ __global__ __launch_bounds__(256) void softmax_backward_kernel(DView<const float
 }
 
 // -------------------------------------------------------------- matmul
-// fp32 c = a @ b on arbitrary strided views.  64x64 output tile per
-// 256-thread workgroup, 4x4 outputs per thread, k staged through LDS in
-// steps of 16.  Each output keeps one fp32 accumulator with k ascending, the
-// association of op_mm_tiled_kernel (op_mm_optimized.cuh:35-62).
-constexpr int MT = 64, KT = 16;
+// fp32 c = a @ b on arbitrary strided views (op_mm, op_mm.cuh:39-57) on the
+// fp32 matrix cores: v_mfma_f32_32x32x2f32 (lane l supplies A[l%32][l/32] and
+// B[l/32][l%32]; D[8(i/4) + 4(l/32) + i%4][l%32] lands in register i).
+// A 256-thread workgroup owns a 64x64 output tile, each wave a 32x32 block;
+// k steps of 32 are staged through k-major LDS tiles (conflict-free operand
+// reads), the next step's tile prefetched into registers, coalesced along
+// whichever dimension of each view has unit stride (so transposed views such
+// as key.T load as well as row-major ones).  Small outputs split k across
+// workgroups into partial slabs that a second kernel sums in a fixed order
+// (deterministic).  Products and sums are fp32; the association differs from
+// op_mm_tiled_kernel's single running sum (op_mm_optimized.cuh:35-62).
+typedef float mf32x16_t __attribute__((ext_vector_type(16)));
+constexpr int MT = 64, KT = 32, LP = MT + 4;
+
 __global__ __launch_bounds__(256) void matmul_kernel(DView<const float> a, DView<const float> b,
-                                                     DView<float> c) {
-  __shared__ float As[KT][MT + 4];
-  __shared__ float Bs[KT][MT + 4];
-  const int tid = threadIdx.x;
-  const int tr = tid / 16, tc = tid % 16;
+                                                     DView<float> c, float *part, int kchunk) {
+  __shared__ float As[KT][LP];  // As[k][m]
+  __shared__ float Bs[KT][LP];  // Bs[k][n]
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
   const int row0 = blockIdx.y * MT, col0 = blockIdx.x * MT;
-  float acc[4][4] = {};
-  for (int k0 = 0; k0 < a.w; k0 += KT) {
-    for (int e = tid; e < MT * KT; e += 256) {
-      int r = e / KT, k = e % KT;  // A tile: 64 rows x 16 k
-      int gr = row0 + r, gk = k0 + k;
-      As[k][r] = (gr < a.h && gk < a.w) ? a.at(gr, gk) : 0.f;
-      int kk = e / MT, cc = e % MT;  // B tile: 16 k x 64 cols
-      int bk = k0 + kk, bc = col0 + cc;
-      Bs[kk][cc] = (bk < b.h && bc < b.w) ? b.at(bk, bc) : 0.f;
+  const int kb = blockIdx.z * kchunk, ke = min(kb + kchunk, a.w);
+  // staging maps: 8 elements per thread per matrix, consecutive along the
+  // unit-stride dimension when there is one
+  const bool a_krow = a.sw == 1 || a.sh != 1;  // a's k dimension is the contiguous one (or neither)
+  const bool b_nrow = b.sw == 1 || b.sh != 1;
+  const int am = a_krow ? tid >> 2 : (tid & 7) * 8, ak = a_krow ? (tid & 3) * 8 : tid >> 3;
+  const int bk = b_nrow ? tid >> 3 : (tid & 3) * 8, bn = b_nrow ? (tid & 7) * 8 : tid >> 2;
+  float ra[8], rb[8];
+  auto gload = [&](int k0) __attribute__((always_inline)) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int m = row0 + am + (a_krow ? 0 : e), k = k0 + ak + (a_krow ? e : 0);
+      ra[e] = (m < a.h && k < ke) ? a.at(m, k) : 0.f;
+      const int kk = k0 + bk + (b_nrow ? 0 : e), n = col0 + bn + (b_nrow ? e : 0);
+      rb[e] = (kk < ke && n < b.w) ? b.at(kk, n) : 0.f;
     }
-    __syncthreads();
+  };
+  auto lstore = [&]() __attribute__((always_inline)) {
 #pragma unroll
-    for (int k = 0; k < KT; ++k) {
-      float av[4], bv[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) av[i] = As[k][tr + 16 * i];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) bv[j] = Bs[k][tc + 16 * j];
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] += av[i] * bv[j];
+    for (int e = 0; e < 8; ++e) {
+      As[ak + (a_krow ? e : 0)][am + (a_krow ? 0 : e)] = ra[e];
+      Bs[bk + (b_nrow ? 0 : e)][bn + (b_nrow ? e : 0)] = rb[e];
     }
+  };
+  mf32x16_t acc = {};
+  if (kb < ke) gload(kb);
+  for (int k0 = kb; k0 < ke; k0 += KT) {
+    __syncthreads();  // previous step's operand reads are done
+    lstore();
     __syncthreads();
+    if (k0 + KT < ke) gload(k0 + KT);
+#pragma unroll
+    for (int kk = 0; kk < KT; kk += 2) {
+      const float av = As[kk + (lane >> 5)][wm * 32 + (lane & 31)];
+      const float bv = Bs[kk + (lane >> 5)][wn * 32 + (lane & 31)];
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av, bv, acc, 0, 0, 0);
+    }
   }
+  const int n = col0 + wn * 32 + (lane & 31);
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      int r = row0 + tr + 16 * i, cidx = col0 + tc + 16 * j;
-      if (r < c.h && cidx < c.w) c.at(r, cidx) = acc[i][j];
+  for (int i = 0; i < 16; ++i) {
+    const int m = row0 + wm * 32 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
+    if (m < c.h && n < c.w) {
+      if (part)
+        part[((int64_t)blockIdx.z * c.h + m) * c.w + n] = acc[i];
+      else
+        c.at(m, n) = acc[i];
     }
+  }
+}
+
+// c = sum over the k slabs, slab 0 first
+__global__ __launch_bounds__(256) void matmul_reduce_kernel(const float *part, int nsplit,
+                                                            DView<float> c) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t mn = (int64_t)c.h * c.w;
+  if (idx >= mn) return;
+  float s = 0.f;
+  for (int z = 0; z < nsplit; ++z) s += part[z * mn + idx];
+  c.at((int)(idx / c.w), (int)(idx % c.w)) = s;
 }
 
 // ---------------------------------------------------------- elementwise
@@ -314,11 +351,36 @@ int bn_matmul(const bn_view *a, const bn_view *b, const bn_view *c, void *stream
   if ((st = require_device("Matrix multiply", {a, b, c}))) return st;
   if ((st = ensure_device())) return st;
   if (c->h == 0 || c->w == 0) return BN_OK;
-  dim3 grid((c->w + MT - 1) / MT, (c->h + MT - 1) / MT);
-  hipLaunchKernelGGL(matmul_kernel, grid, dim3(256), 0, as_stream(stream), dview<const float>(a),
-                     dview<const float>(b), dview<float>(c));
-  BN_LAUNCH_CHECK();
-  return BN_OK;
+  const int tiles = ((c->w + MT - 1) / MT) * ((c->h + MT - 1) / MT);
+  // split k while the grid is small and every slab keeps >= 128 of k
+  int nsplit = 1;
+  while (nsplit < 16 && tiles * nsplit < 256 && a->w / (2 * nsplit) >= 128) nsplit *= 2;
+  const int kchunk = ((a->w + nsplit - 1) / nsplit + KT - 1) / KT * KT;
+  nsplit = a->w == 0 ? 1 : (a->w + kchunk - 1) / kchunk;
+  hipStream_t s = as_stream(stream);
+  float *part = nullptr;
+  if (nsplit > 1) {
+    void *ws = nullptr;
+    if ((st = bn_alloc(&ws, (size_t)nsplit * c->h * c->w * sizeof(float), stream))) return st;
+    part = (float *)ws;
+  }
+  dim3 grid((c->w + MT - 1) / MT, (c->h + MT - 1) / MT, nsplit);
+  hipLaunchKernelGGL(matmul_kernel, grid, dim3(256), 0, s, dview<const float>(a),
+                     dview<const float>(b), dview<float>(c), part, kchunk > 0 ? kchunk : KT);
+  hipError_t e = hipGetLastError();
+  st = e == hipSuccess ? BN_OK : hip_fail(e, __FILE__, __LINE__);
+  if (st == BN_OK && part) {
+    const int64_t mn = (int64_t)c->h * c->w;
+    hipLaunchKernelGGL(matmul_reduce_kernel, dim3((unsigned)((mn + 255) / 256)), dim3(256), 0, s,
+                       part, nsplit, dview<float>(c));
+    e = hipGetLastError();
+    st = e == hipSuccess ? BN_OK : hip_fail(e, __FILE__, __LINE__);
+  }
+  if (part) {
+    const int st2 = bn_free(part, stream);
+    if (st == BN_OK) st = st2;
+  }
+  return st;
 }
 
 int bn_repeat_kv(const bn_view *kv, const bn_view *out, int head_dim, int n_rep, void *stream) {
