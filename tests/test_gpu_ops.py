@@ -34,7 +34,8 @@ S0 = None  # legacy default stream
 
 
 @pytest.mark.parametrize("rows,w,dtype", [(7, 2048, "f32"), (5, 300, "f32"), (64, 2048, "bf16"),
-                                          (3, 4096, "f32"), (2, 6000, "f32"), (1, 2048, "bf16")])
+                                          (3, 4096, "f32"), (2, 6000, "f32"), (1, 2048, "bf16"),
+                                          (8195, 256, "f32"), (8193, 2048, "bf16")])  # 4 rows/wave
 def test_rmsnorm(rows, w, dtype):
     r = rng(1)
     x = r.standard_normal((rows, w)).astype(np.float32)
@@ -90,7 +91,8 @@ def test_rope_transposed_view():
 
 @pytest.mark.parametrize("rows,w,off,dtype", [(32, 2048, 0, "f32"), (9, 2048, 77, "f32"),
                                               (64, 2048, 1000, "bf16"), (5, 512, 3, "bf16"),
-                                              (3, 320, 0, "f32")])
+                                              (3, 320, 0, "f32"), (8194, 512, 5, "bf16"),
+                                              (8198, 2048, 0, "f32")])
 def test_rmsnorm_rope(rows, w, off, dtype):
     r = rng(5)
     x = r.standard_normal((rows, w)).astype(np.float32)
