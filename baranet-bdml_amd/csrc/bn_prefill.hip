@@ -239,10 +239,18 @@ __global__ __launch_bounds__(256, OCC) void prefill_bf16_kernel(PrefillParams p)
   const int crow = tid >> 3, ccol = (tid & 7) * 8;
   const int voff0 = (crow * (int)p.kv_rs + ccol) * 2, voff1 = voff0 + 64 * (int)p.kv_rs;
   u32x4_t k0, k1, v0, v1;
+  // Every descriptor field goes through readfirstlane: the values are
+  // uniform, but one computed on the VALU (the clamp) would leave the
+  // descriptor in VGPRs and the compiler would wrap each load in a
+  // readfirstlane/exec loop.
   auto rsrc = [&](const bf16_t *base, int blk) __attribute__((always_inline)) {
     const int rows = min(max(p.seq_kv - BN * blk, 0), BN);
-    return __builtin_amdgcn_make_buffer_rsrc((void *)(base + (int64_t)BN * blk * p.kv_rs),
-                                             (short)0, rows * (int)p.kv_rs * 2, 0x00020000);
+    const uint64_t a = (uint64_t)(base + (int64_t)BN * blk * p.kv_rs);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
+    const int nrec = __builtin_amdgcn_readfirstlane(rows * (int)p.kv_rs * 2);
+    return __builtin_amdgcn_make_buffer_rsrc((void *)(((uint64_t)hi << 32) | lo), (short)0, nrec,
+                                             0x00020000);
   };
   auto gload_k = [&](int blk) __attribute__((always_inline)) {
     const __amdgpu_buffer_rsrc_t r = rsrc(K, blk);
