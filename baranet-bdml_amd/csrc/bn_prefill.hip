@@ -668,7 +668,9 @@ extern "C" int bn_gqa_prefill(int dtype, const void *q, const void *k, const voi
     return fail(BN_ERR_UNSUPPORTED, std::string(op) + ": bf16 K/V row stride must be below 2^24 elements");
   // bf16: two 32-row tiles per wave (every LDS fragment feeds two MFMAs) when
   // that still leaves >= 2048 workgroups (8 per CU); one tile otherwise, so
-  // short sequences keep enough workgroups in flight
+  // short sequences keep enough workgroups in flight and waste less of the
+  // causal diagonal (measured with settled clocks: RT = 2 gains 3-7% from
+  // S = 4096 on at >= 2048 workgroups, loses up to 30% below 1024)
 #ifndef BN_RT2_MIN_WG
 #define BN_RT2_MIN_WG 2048
 #endif

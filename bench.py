@@ -21,7 +21,9 @@ kernels, test infrastructure) on a bounded sample of the same workload.
 
 Timing: hip events recorded on the stream the kernels are launched on (the
 current torch stream, passed to the C ABI), around K back-to-back launches
-after W warm-up launches, with torch.cuda.synchronize() on both sides.
+after W warm-up launches followed by at least --warm-seconds (default 1 s)
+of untimed back-to-back launches of the same workload (GPU clock settled),
+with torch.cuda.synchronize() on both sides.
 """
 import argparse
 import json
@@ -48,12 +50,28 @@ def decode_bytes(lens, Hkv, D, B, H, elem):
     return int(sum(2 * int(L) * Hkv * D * elem for L in lens) + 2 * B * H * D * elem)
 
 
+WARM_SECONDS = 1.0  # --warm-seconds
+
+
 def time_launches(fn, steps, warmup):
-    """Average launch duration (ms) of fn() over `steps` back-to-back calls."""
+    """Average launch duration (ms) of fn() over `steps` back-to-back calls.
+
+    Untimed warm-up: `warmup` calls, then more calls until WARM_SECONDS of
+    back-to-back work have run, so the GPU clock has left its idle state
+    (a cold GPU runs the first ~100 ms of MFMA work ~20% slower)."""
     import torch
     for i in range(warmup):
         fn(i)
     torch.cuda.synchronize()
+    t0, i, burst = time.perf_counter(), warmup, 4
+    while time.perf_counter() - t0 < WARM_SECONDS:
+        tb = time.perf_counter()
+        for _ in range(burst):
+            fn(i)
+            i += 1
+        torch.cuda.synchronize()
+        if time.perf_counter() - tb < 0.05:
+            burst *= 2
     s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     s.record()
     for i in range(steps):
@@ -315,6 +333,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--warm-seconds", type=float, default=1.0,
+                    help="minimum untimed warm-up per workload, seconds of back-to-back launches")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--tl-warmup", type=int, default=2,
                     help="config 4: warm-up decode tokens before the timed generate (0: none, "
@@ -336,6 +356,7 @@ def main():
     only = set(filter(None, args.only.split(",")))
     want = lambda k: not only or k in only
     K, W = args.steps, args.warmup
+    globals()["WARM_SECONDS"] = args.warm_seconds
 
     head = bench_prefill(4, 2048, 32, 4, "bf16", K, W)
     out = {"metric": METRIC, "value": head["value"], "unit": "TFLOP/s", "n_gpus": 1,
