@@ -38,6 +38,9 @@ inline hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s);
 
 // Makes sure the library's device is current on the calling thread.
 int ensure_device();
+// Compute units of the library's device (0 if the query fails); call after
+// ensure_device().
+int device_cu_count();
 
 // ------------------------------------------------------------ validation
 inline size_t dtype_size(int dt) { return dt == BN_BF16 ? 2 : 4; }

@@ -628,6 +628,208 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(BN_DECODE_R
   }
 }
 
+// bf16 cache, one workgroup per (sequence, KV head) over the whole cache:
+// no partials in memory and no combine launch.  Chosen when there are at
+// least as many (sequence, KV head) pairs as compute units, so every CU has a
+// workgroup.  Wave w of the WWV takes the 32-key tiles w, w + WWV, ... and
+// streams them through a private LDS tile (no workgroup barrier in the loop):
+// 16-byte loads of the head's 128-byte cache rows, 8 rows per instruction,
+// the next tile register-staged; the scores and P V on
+// v_mfma_f32_16x16x32_bf16 as in the whole-row kernel.  The waves'
+// (m, l, acc) are merged through LDS at the end and the workgroup writes the
+// G output rows.
+#ifndef BN_DECODE_WHOLE_WAVES
+#define BN_DECODE_WHOLE_WAVES 4
+#endif
+constexpr int WWV = BN_DECODE_WHOLE_WAVES;
+constexpr int WKP = HD + 8;  // tile row pitch, 144 B: b128 K reads of 16 rows and tr16 V
+                             // reads of 4 rows x 32 B hit distinct banks
+
+template <int G>
+__global__ __launch_bounds__(64 * WWV) void decode_bf16_whole_kernel(DecodeParams p) {
+  __shared__ __attribute__((aligned(16))) bf16_t KT[WWV][TK * WKP];
+  __shared__ __attribute__((aligned(16))) bf16_t VT[WWV][TK * WKP];
+  __shared__ float red_m[WWV][G], red_l[WWV][G];
+  __shared__ float red_o[WWV][G][HD];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l16 = lane & 15, grp = lane >> 4;
+  const int b = blockIdx.x / p.n_kv_heads, g = blockIdx.x % p.n_kv_heads;
+
+  int len = p.lens[b];
+  len = len < 0 ? 0 : (len > p.max_len ? p.max_len : len);
+  bf16_t *out = (bf16_t *)p.o + ((int64_t)b * p.n_heads + (int64_t)g * G) * HD;
+  if (len == 0) {  // no key: zeros
+    for (int idx = tid; idx < G * HD; idx += 64 * WWV) out[idx] = f32_to_bf16(0.f);
+    return;
+  }
+  // wave w takes the 32-key tiles w, w + WWV, w + 2*WWV, ...: the waves of a
+  // workgroup stream adjacent tiles (a contiguous key range per wave, or the
+  // KV heads of one sequence placed on one XCD, measured 3-4% slower)
+  const int all_tiles = (len + TK - 1) / TK;
+  const int kw0 = TK * wave, kw1 = len;
+  const int tstride = TK * WWV;  // keys between a wave's tiles
+  const int ntiles = all_tiles > wave ? (all_tiles - wave + WWV - 1) / WWV : 0;
+
+  const int64_t kv_rs = (int64_t)p.n_kv_heads * HD;
+  const bf16_t *Kr = (const bf16_t *)p.k + (int64_t)b * p.max_len * kv_rs + (int64_t)g * HD;
+  const bf16_t *Vr = (const bf16_t *)p.v + (int64_t)b * p.max_len * kv_rs + (int64_t)g * HD;
+
+  dbf16x8_t qb[2];
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    if (l16 < G)
+      qb[t] = *(const dbf16x8_t *)((const bf16_t *)p.q +
+                                   ((int64_t)b * p.n_heads + g * G + l16) * HD + 8 * grp + 32 * t);
+    else
+      qb[t] = dbf16x8_t{};
+  }
+
+  // lane's 16-byte chunks of a tile: rows crow + 8i (i = 0..3), columns ccol..ccol+7
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  struct RegTile {
+    u32x4 k0, k1, k2, k3, v0, v1, v2, v3;
+  };
+  const int crow = lane >> 3, ccol = (lane & 7) * 8;
+  auto gload = [&](RegTile &r, int ti) __attribute__((always_inline)) {
+    const int kb = kw0 + tstride * min(ti, ntiles - 1);  // clamped: same load count on every path
+    const int last = min(kb + TK, kw1) - 1;  // past the end: a valid row, masked to P = 0
+    const int64_t o0 = (int64_t)min(kb + crow, last) * kv_rs + ccol;
+    const int64_t o1 = (int64_t)min(kb + crow + 8, last) * kv_rs + ccol;
+    const int64_t o2 = (int64_t)min(kb + crow + 16, last) * kv_rs + ccol;
+    const int64_t o3 = (int64_t)min(kb + crow + 24, last) * kv_rs + ccol;
+    r.k0 = *(const u32x4 *)(Kr + o0); r.v0 = *(const u32x4 *)(Vr + o0);
+    r.k1 = *(const u32x4 *)(Kr + o1); r.v1 = *(const u32x4 *)(Vr + o1);
+    r.k2 = *(const u32x4 *)(Kr + o2); r.v2 = *(const u32x4 *)(Vr + o2);
+    r.k3 = *(const u32x4 *)(Kr + o3); r.v3 = *(const u32x4 *)(Vr + o3);
+  };
+  bf16_t *const kt = KT[wave], *const vt = VT[wave];
+  auto lstore = [&](const RegTile &r) __attribute__((always_inline)) {
+    *(u32x4 *)(kt + crow * WKP + ccol) = r.k0;
+    *(u32x4 *)(kt + (crow + 8) * WKP + ccol) = r.k1;
+    *(u32x4 *)(kt + (crow + 16) * WKP + ccol) = r.k2;
+    *(u32x4 *)(kt + (crow + 24) * WKP + ccol) = r.k3;
+    *(u32x4 *)(vt + crow * WKP + ccol) = r.v0;
+    *(u32x4 *)(vt + (crow + 8) * WKP + ccol) = r.v1;
+    *(u32x4 *)(vt + (crow + 16) * WKP + ccol) = r.v2;
+    *(u32x4 *)(vt + (crow + 24) * WKP + ccol) = r.v3;
+  };
+
+  float m = -INFINITY, l = 0.f;
+  df32x4_t o[4] = {df32x4_t{}, df32x4_t{}, df32x4_t{}, df32x4_t{}};
+  const float c = p.c;
+  // one 32-key tile from this wave's LDS tile; keys kb .. kb + 31
+  auto compute = [&](int kb) __attribute__((always_inline)) {
+    const bf16_t *kl = kt + 8 * grp;
+    df32x4_t s[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const bf16_t *kp = kl + (16 * u + l16) * WKP;
+      s[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*(const dbf16x8_t *)(kp), qb[0], df32x4_t{},
+                                                     0, 0, 0);
+      s[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*(const dbf16x8_t *)(kp + 32), qb[1], s[u],
+                                                     0, 0, 0);
+    }
+    // s[u][i] = score of key kb + 16u + 4grp + i for query head g*G + l16
+    if (kb + TK > kw1) {
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (kb + 16 * u + 4 * grp + i >= kw1) s[u][i] = -INFINITY;
+    }
+    float mx = fmaxf(fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3])),
+                     fmaxf(fmaxf(s[1][0], s[1][1]), fmaxf(s[1][2], s[1][3])));
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float m_new = fmaxf(m, mx);  // finite: every tile holds at least one key
+    const float mc = m_new * c;
+    const float alpha = __builtin_amdgcn_exp2f(m * c - mc);  // m = -inf -> 0
+    float rs = 0.f;
+    dbf16x8_t pb;
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float e = __builtin_amdgcn_exp2f(fmaf(s[u][i], c, -mc));
+        rs += e;
+        pb[4 * u + i] = (__bf16)e;  // k-slot (grp, 4u+i) = key 16u + 4grp + i
+      }
+    l = l * alpha + rs;
+    m = m_new;
+    // V^T operand: slot j of lane (grp, l16) = V[key 16(j/4) + 4grp + j%4][16dt + l16];
+    // transpose read: local lane n supplies V[key 4grp + n/4 (+16)][16dt + 4(n%4) .. +3]
+    const bf16_t *vp = vt + (4 * grp + (l16 >> 2)) * WKP + 4 * (l16 & 3);
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+      o[dt] *= alpha;
+      const dbf16x4_t lo = lds_read_tr16(vp + 16 * dt);
+      const dbf16x4_t hi = lds_read_tr16(vp + 16 * WKP + 16 * dt);
+      const dbf16x8_t a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb, o[dt], 0, 0, 0);
+    }
+  };
+
+  // Tile ti is register tile ta (even) / tb (odd), loaded two tiles ahead,
+  // and goes through the wave's single LDS tile.  LDS instructions of one
+  // wave execute in order, so the tile's writes follow the previous tile's
+  // reads (already consumed) and precede its own reads without a barrier;
+  // wave_barrier keeps the compiler from moving LDS accesses across.
+  // The wave's tile ti goes through one register tile (loaded one tile ahead)
+  // and the wave's LDS tile.  LDS instructions of one wave execute in order,
+  // so a tile's writes follow the previous tile's reads (already consumed) and
+  // precede its own reads with no barrier; wave_barrier keeps the compiler
+  // from moving LDS accesses across.  One tile in flight per wave (4 KB of K
+  // and of V; 32 KB per CU at 4 waves) streams best: two tiles ahead measured
+  // 8% slower on config 3, more waves per workgroup slower still.
+  if (ntiles > 0) {  // wave-uniform
+    RegTile ta;
+    gload(ta, 0);
+    lstore(ta);
+    gload(ta, 1);
+    __builtin_amdgcn_wave_barrier();
+    for (int ti = 0; ti < ntiles; ++ti) {
+      compute(kw0 + tstride * ti);
+      if (ti + 1 < ntiles) {
+        __builtin_amdgcn_wave_barrier();
+        lstore(ta);
+        gload(ta, ti + 2);
+        __builtin_amdgcn_wave_barrier();
+      }
+    }
+  }
+
+  // merge the waves: o[dt][i] = O^T[d = 16dt + 4grp + i][head g*G + l16]
+  l += __shfl_xor(l, 16, 64);
+  l += __shfl_xor(l, 32, 64);
+  if (l16 < G) {
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) red_o[wave][l16][16 * dt + 4 * grp + i] = o[dt][i];
+    if (grp == 0) {
+      red_m[wave][l16] = m * c;  // -inf for a wave without keys
+      red_l[wave][l16] = l;
+    }
+  }
+  __syncthreads();
+  for (int idx = tid; idx < G * HD; idx += 64 * WWV) {
+    const int h = idx / HD, d = idx - h * HD;
+    float M = red_m[0][h];
+#pragma unroll
+    for (int w = 1; w < WWV; ++w) M = fmaxf(M, red_m[w][h]);  // finite: wave 0 has keys
+    float L = 0.f, A = 0.f;
+#pragma unroll
+    for (int w = 0; w < WWV; ++w) {
+      const float wt = __builtin_amdgcn_exp2f(red_m[w][h] - M);
+      L += red_l[w][h] * wt;
+      A += red_o[w][h][d] * wt;
+    }
+    out[idx] = f32_to_bf16(A / L);
+  }
+}
+
 // One thread per (b, head, d): merge the chunks [0, ceil(len/chunk)) in one
 // pass (running log-sum-exp), four chunks' loads in flight at a time.
 template <typename T>
@@ -801,6 +1003,30 @@ int bn_gqa_decode(int dtype, const void *q, const void *k_cache, const void *v_c
     launch_single(p, s);
     BN_LAUNCH_CHECK();
     return BN_OK;
+  }
+#ifndef BN_DECODE_WHOLE
+#define BN_DECODE_WHOLE 1
+#endif
+  if (BN_DECODE_WHOLE && dtype == BN_BF16) {  // one workgroup per (sequence, KV head) when that fills the CUs
+    int st = ensure_device();
+    if (st) return st;
+    const int cus = device_cu_count();
+    if (cus > 0 && (int64_t)batch * n_kv_heads >= cus) {
+      p.ws = nullptr;
+      p.n_split = 1;
+      p.chunk = max_len;
+      p.c = scale * 1.4426950408889634f;
+      hipStream_t s = as_stream(stream);
+      const dim3 grid((unsigned)((int64_t)batch * n_kv_heads)), block(64 * WWV);
+      switch (G) {
+        case 1: hipLaunchKernelGGL(decode_bf16_whole_kernel<1>, grid, block, 0, s, p); break;
+        case 2: hipLaunchKernelGGL(decode_bf16_whole_kernel<2>, grid, block, 0, s, p); break;
+        case 4: hipLaunchKernelGGL(decode_bf16_whole_kernel<4>, grid, block, 0, s, p); break;
+        default: hipLaunchKernelGGL(decode_bf16_whole_kernel<8>, grid, block, 0, s, p); break;
+      }
+      BN_LAUNCH_CHECK();
+      return BN_OK;
+    }
   }
   // the whole-row kernel gives each workgroup 4 KV heads: 1/4 of the workgroups per chunk
   p.chunk = rows_path(p, dtype == BN_BF16)

@@ -68,6 +68,19 @@ int ensure_device() {
   return BN_OK;
 }
 
+int device_cu_count() {
+  static int cached_device = -1, cached_count = 0;
+  std::lock_guard<std::mutex> lk(g_mu);
+  if (cached_device != g_device) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, g_device) != hipSuccess)
+      n = 0;
+    cached_device = g_device;
+    cached_count = n;
+  }
+  return cached_count;
+}
+
 // -------------------------------------------------------------- validation
 int check_view(const bn_view *v, const char *op, const char *name, unsigned dtype_mask,
                bool need_device) {

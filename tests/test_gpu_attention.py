@@ -171,6 +171,33 @@ def test_decode_vs_oracle(case, dtype):
         assert_close(got[b:b + 1], ref, TOL[dtype], f"decode b={b} len={Lb}")
 
 
+@pytest.mark.parametrize("L,H,Hkv", [(300, 32, 4), (130, 16, 4), (200, 8, 4), (96, 16, 2),
+                                     (70, 4, 4)])
+def test_decode_bf16_one_workgroup_per_kv_head(L, H, Hkv):
+    """bf16 with at least as many (sequence, KV head) pairs as CUs takes the
+    single-pass kernel (one workgroup per pair, per-wave key ranges merged in
+    LDS): G = 8, 4, 2, 1; empty, one-key, tile-edge, clamped and short
+    lengths that leave some waves without keys."""
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    Bn = -(-cus // Hkv)
+    r = np.random.default_rng(L + H)
+    lens = r.integers(1, L + 1, Bn).astype(np.int32)
+    lens[:8] = [0, 1, 31, 32, 33, L, L + 5, min(255, L)]
+    q = bf16_round(r.standard_normal((Bn, H, 64)).astype(np.float32))
+    kc = bf16_round(r.standard_normal((Bn, L, Hkv, 64)).astype(np.float32))
+    vc = bf16_round(r.standard_normal((Bn, L, Hkv, 64)).astype(np.float32))
+    got = host(B.gqa_decode(dev(q, torch.bfloat16), dev(kc, torch.bfloat16),
+                            dev(vc, torch.bfloat16), torch.from_numpy(lens).cuda(), scale=0.125))
+    for b in list(range(8)) + list(range(8, Bn, 7)):
+        Lb = int(min(max(lens[b], 0), L))
+        if Lb == 0:
+            assert np.all(got[b] == 0.0)
+            continue
+        ref = O.gqa_decode(q[b:b + 1], kc[b:b + 1, :Lb], vc[b:b + 1, :Lb],
+                           np.array([Lb], np.int32), 0.125)
+        assert_close(got[b:b + 1], ref, BF16_TOL, f"b={b} len={Lb}")
+
+
 @pytest.mark.parametrize("dtype,Hkv", [("bf16", 4), ("bf16", 2), ("f32", 4)])
 def test_decode_workspace_reuse(dtype, Hkv):
     """One workspace across calls of different batches and lengths (the
