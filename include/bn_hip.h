@@ -179,7 +179,10 @@ int bn_gqa_prefill(int dtype, const void *q, const void *k, const void *v,
  * [batch, max_len, n_kv_heads, head_dim] contiguous; seq_lens: device int32
  * [batch], each in [1, max_len] (checked on the device: out-of-range lengths
  * are clamped and reported as zeros).  workspace: device memory of
- * bn_gqa_decode_workspace_size() bytes (NULL: taken from the pool). */
+ * bn_gqa_decode_workspace_size() bytes (NULL: taken from the pool when the
+ * call needs it); single-pass calls use none: bf16 caches with
+ * batch*n_kv_heads >= the device's compute units, fp32 caches of at most 1024
+ * keys with batch*n_heads <= 256. */
 size_t bn_gqa_decode_workspace_size(int batch, int max_len, int n_heads,
                                     int head_dim);
 int bn_gqa_decode(int dtype, const void *q, const void *k_cache,
