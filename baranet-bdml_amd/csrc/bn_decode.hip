@@ -989,6 +989,15 @@ int bn_gqa_decode(int dtype, const void *q, const void *k_cache, const void *v_c
     return fail(BN_ERR_INVALID_ARG, std::string(op) + ": NULL pointer");
   if (((uintptr_t)q | (uintptr_t)k_cache | (uintptr_t)v_cache) & 15u)
     return fail(BN_ERR_UNSUPPORTED, std::string(op) + ": q and caches must be 16-byte aligned");
+  // a caller's workspace must hold what bn_gqa_decode_workspace_size() asks
+  // for, whichever kernel the call takes (checked before any device work)
+  if (workspace) {
+    const size_t want = bn_gqa_decode_workspace_size(batch, max_len, n_heads, head_dim);
+    if (workspace_bytes < want)
+      return fail(BN_ERR_INVALID_ARG, std::string(op) + ": workspace of " +
+                                          std::to_string(workspace_bytes) + " bytes, need " +
+                                          std::to_string(want));
+  }
   DecodeParams p;
   p.q = q; p.k = k_cache; p.v = v_cache; p.lens = seq_lens; p.o = o;
   p.batch = batch; p.max_len = max_len; p.n_heads = n_heads; p.n_kv_heads = n_kv_heads;
@@ -1035,10 +1044,6 @@ int bn_gqa_decode(int dtype, const void *q, const void *k_cache, const void *v_c
   p.n_split = (max_len + p.chunk - 1) / p.chunk;
   p.c = scale * 1.4426950408889634f;
   const size_t need = (size_t)batch * n_heads * p.n_split * (HD + 2) * sizeof(float);
-  if (workspace && workspace_bytes < need)
-    return fail(BN_ERR_INVALID_ARG, std::string(op) + ": workspace of " +
-                                        std::to_string(workspace_bytes) + " bytes, need " +
-                                        std::to_string(need));
   int st = ensure_device();
   if (st) return st;
   hipStream_t s = as_stream(stream);
