@@ -464,8 +464,13 @@ __global__ __launch_bounds__(256, OCC) void prefill_bf16_kernel(PrefillParams p)
   auto iteration = [&](auto masked_tag, int j) __attribute__((always_inline)) {
     const bf16_t *vc = vring + (j & 1) * VBUF;
     const bf16_t *kn = kring + ((j + 1) & 1) * KBUF;
-    step(masked_tag, 2 * j + 1, vc, kn, sb, sa, pa, pbb);
-    step(masked_tag, 2 * j + 2, vc + 32 * VP16, kn + 32 * KP16, sa, sb, pbb, pa);
+    // masked iterations: a wave skips the steps past its causal range (step
+    // ntw still adds P V of its last tile); the others' barriers and staging
+    // go on, and the SIMD's other waves get the issue slots
+    constexpr bool MASKED = decltype(masked_tag)::value;
+    if (!MASKED || 2 * j + 1 <= ntw) step(masked_tag, 2 * j + 1, vc, kn, sb, sa, pa, pbb);
+    if (!MASKED || 2 * j + 2 <= ntw)
+      step(masked_tag, 2 * j + 2, vc + 32 * VP16, kn + 32 * KP16, sa, sb, pbb, pa);
     lstore_k(j & 1);        // K_{j+2} into K_j's buffer (K_j last read in iteration j-1)
     lstore_v((j + 1) & 1);  // V_{j+1} into V_{j-1}'s buffer
     gload_k(j + 3);         // rows past seq_kv read as 0
@@ -667,12 +672,12 @@ extern "C" int bn_gqa_prefill(int dtype, const void *q, const void *k, const voi
   if (dtype == BN_BF16 && kv_row_stride >= ((int64_t)1 << 24))
     return fail(BN_ERR_UNSUPPORTED, std::string(op) + ": bf16 K/V row stride must be below 2^24 elements");
   // bf16: two 32-row tiles per wave (every LDS fragment feeds two MFMAs) when
-  // that still leaves >= 2048 workgroups (8 per CU); one tile otherwise, so
-  // short sequences keep enough workgroups in flight and waste less of the
-  // causal diagonal (measured with settled clocks: RT = 2 gains 3-7% from
-  // S = 4096 on at >= 2048 workgroups, loses up to 30% below 1024)
+  // that still leaves >= 1024 workgroups (4 per CU); one tile otherwise, so
+  // small problems keep enough workgroups in flight (measured with settled
+  // clocks: RT = 2 gains 3% on config 2 and 3-7% from S = 4096 on, and loses
+  // 10-30% at 512 workgroups or fewer)
 #ifndef BN_RT2_MIN_WG
-#define BN_RT2_MIN_WG 2048
+#define BN_RT2_MIN_WG 1024
 #endif
   const int rt16 = ((int64_t)batch * n_heads * ((seq_q + 255) / 256) >= BN_RT2_MIN_WG) ? 2 : 1;
   const int rows_per_wg = dtype == BN_BF16 ? 4 * 32 * rt16 : BM;
