@@ -198,6 +198,32 @@ def test_decode_bf16_one_workgroup_per_kv_head(L, H, Hkv):
         assert_close(got[b:b + 1], ref, BF16_TOL, f"b={b} len={Lb}")
 
 
+@pytest.mark.parametrize("dtype,Bn,L,H,Hkv", [("f32", 1, 640, 32, 4), ("f32", 3, 300, 8, 2),
+                                              ("bf16", 2, 300, 32, 4), ("bf16", 80, 200, 16, 4)])
+def test_decode_ignores_cache_rows_past_len(dtype, Bn, L, H, Hkv):
+    """Cache rows at or past a sequence's length hold NaN (memory the caller
+    never wrote): no kernel may let them reach the output (single-pass fp32,
+    split and per-KV-head bf16 paths)."""
+    r = np.random.default_rng(Bn + L)
+    lens = r.integers(1, L + 1, Bn).astype(np.int32)
+    lens[0] = L // 2
+    q = draw((Bn, H, 64), 50, dtype)
+    kc = draw((Bn, L, Hkv, 64), 51, dtype)
+    vc = draw((Bn, L, Hkv, 64), 52, dtype)
+    kn, vn = kc.copy(), vc.copy()
+    for b in range(Bn):
+        kn[b, lens[b]:] = np.nan
+        vn[b, lens[b]:] = np.nan
+    got = host(B.gqa_decode(dev(q, TD[dtype]), dev(kn, TD[dtype]), dev(vn, TD[dtype]),
+                            torch.from_numpy(lens).cuda(), scale=0.125))
+    assert np.all(np.isfinite(got))
+    for b in range(Bn):
+        Lb = int(lens[b])
+        ref = O.gqa_decode(q[b:b + 1], kc[b:b + 1, :Lb], vc[b:b + 1, :Lb],
+                           np.array([Lb], np.int32), 0.125)
+        assert_close(got[b:b + 1], ref, TOL[dtype], f"b={b} len={Lb}")
+
+
 @pytest.mark.parametrize("dtype,Hkv", [("bf16", 4), ("bf16", 2), ("f32", 4)])
 def test_decode_workspace_reuse(dtype, Hkv):
     """One workspace across calls of different batches and lengths (the
