@@ -10,6 +10,8 @@
 //   repeat_kv host loop (src/llama/llama_layers.hpp:131-175)
 //   functor kernels of src/ops/op_elemwise.cuh:169-283, op_silu.cuh:33-48,
 //     op_reduction.cuh:36-109
+#include <rocblas/rocblas.h>
+
 #include <cfloat>
 
 #include "bn_common.hpp"
@@ -292,6 +294,57 @@ __global__ void argmax_kernel(DView<const T> x, DView<uint32_t> y) {
 
 inline dim3 grid1d(int64_t n) { return dim3((unsigned)((n + 255) / 256)); }
 
+// Plain GEMMs (each operand row-major or a transposed view, output row-major)
+// go to rocBLAS's fp32 GEMM; other strided views take matmul_kernel.  One
+// rocBLAS handle per thread, bound to the library's device.
+bool unit_stride(const bn_view *v, bool &transposed, int64_t &ld) {
+  if (v->stride_w == 1 && v->stride_h >= v->w) {
+    transposed = false;
+    ld = v->stride_h;
+    return ld >= 1;
+  }
+  if (v->stride_h == 1 && v->stride_w >= v->h) {
+    transposed = true;
+    ld = v->stride_w;
+    return ld >= 1;
+  }
+  return false;
+}
+
+int blas_gemm(const bn_view *a, const bn_view *b, const bn_view *c, hipStream_t s, bool &done) {
+  done = false;
+  bool ta, tb, tc;
+  int64_t lda, ldb, ldc;
+  if (!unit_stride(a, ta, lda) || !unit_stride(b, tb, ldb) || !unit_stride(c, tc, ldc) || tc)
+    return BN_OK;
+  if (lda > INT32_MAX || ldb > INT32_MAX || ldc > INT32_MAX) return BN_OK;
+  thread_local rocblas_handle handle = nullptr;
+  if (!handle) {
+    if (rocblas_create_handle(&handle) != rocblas_status_success) {
+      handle = nullptr;
+      return fail(BN_ERR_HIP, "Matrix multiply: rocblas_create_handle failed");
+    }
+  }
+  if (rocblas_set_stream(handle, s) != rocblas_status_success)
+    return fail(BN_ERR_HIP, "Matrix multiply: rocblas_set_stream failed");
+  // row-major C = A B  <=>  column-major C^T = B^T A^T; a row-major view is
+  // its transpose in column-major, a transposed view needs op T
+  const float one = 1.f, zero = 0.f;
+  const float *ap = (const float *)a->data + a->offset;
+  const float *bp = (const float *)b->data + b->offset;
+  float *cp = (float *)c->data + c->offset;
+  const rocblas_status r =
+      rocblas_sgemm(handle, tb ? rocblas_operation_transpose : rocblas_operation_none,
+                    ta ? rocblas_operation_transpose : rocblas_operation_none, c->w, c->h, a->w,
+                    &one, bp, (rocblas_int)ldb, ap, (rocblas_int)lda, &zero, cp,
+                    (rocblas_int)ldc);
+  if (r != rocblas_status_success)
+    return fail(BN_ERR_HIP, std::string("Matrix multiply: rocblas_sgemm: ") +
+                                rocblas_status_to_string(r));
+  done = true;
+  return BN_OK;
+}
+
 }  // namespace
 }  // namespace bn
 
@@ -351,6 +404,11 @@ int bn_matmul(const bn_view *a, const bn_view *b, const bn_view *c, void *stream
   if ((st = require_device("Matrix multiply", {a, b, c}))) return st;
   if ((st = ensure_device())) return st;
   if (c->h == 0 || c->w == 0) return BN_OK;
+  if (a->w > 0) {
+    bool done = false;
+    if ((st = blas_gemm(a, b, c, as_stream(stream), done))) return st;
+    if (done) return BN_OK;
+  }
   const int tiles = ((c->w + MT - 1) / MT) * ((c->h + MT - 1) / MT);
   // split k while the grid is small and every slab keeps >= 128 of k
   int nsplit = 1;
