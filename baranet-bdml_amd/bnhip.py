@@ -78,6 +78,7 @@ def lib():
         "bn_rmsnorm_backward": ([V, V, V, V, V, f, vp], i),
         "bn_rope": ([V, V, i, i, f, vp], i), "bn_rope_backward": ([V, V, i, i, f, vp], i),
         "bn_rmsnorm_rope": ([V, V, V, f, i, i, f, vp], i),
+        "bn_add_rmsnorm": ([V, V, V, V, V, f, vp], i), "bn_silu_mul": ([V, V, V, vp], i),
         "bn_softmax": ([V, V, i, i, vp], i), "bn_softmax_backward": ([V, V, V, vp], i),
         "bn_matmul": ([V, V, V, vp], i), "bn_repeat_kv": ([V, V, i, i, vp], i),
         "bn_binary": ([i, V, V, V, vp], i), "bn_unary": ([i, V, f, V, vp], i),
@@ -149,6 +150,24 @@ def gqa_prefill(q, k, v, o=None, scale=None, causal=True, seq_offset=0, stream=N
          o.data_ptr(), B, Sq, Skv, H, Hkv, D, q.stride(0), q.stride(1), k.stride(0),
          k.stride(1), o.stride(0), o.stride(1), sc, int(causal), seq_offset, stream_of(stream))
     return o
+
+
+def add_rmsnorm(x, delta, weight, eps, h=None, y=None, stream=None):
+    """(h, y): h = x + delta, y = RMSNorm(h) * weight; h may be x (in place)."""
+    import torch
+    h = torch.empty_like(x) if h is None else h
+    y = torch.empty_like(x) if y is None else y
+    call("bn_add_rmsnorm", C.byref(view(x)), C.byref(view(delta)), C.byref(view(weight)),
+         C.byref(view(h)), C.byref(view(y)), eps, stream_of(stream))
+    return h, y
+
+
+def silu_mul(gate, up, out=None, stream=None):
+    """silu(gate) * up (SwiGLU activation)."""
+    import torch
+    out = torch.empty_like(gate) if out is None else out
+    call("bn_silu_mul", C.byref(view(gate)), C.byref(view(up)), C.byref(view(out)), stream_of(stream))
+    return out
 
 
 def gqa_decode(q, k_cache, v_cache, seq_lens, o=None, scale=None, workspace=None, stream=None):

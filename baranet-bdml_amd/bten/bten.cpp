@@ -10,7 +10,7 @@
 //   (:256-310), randgen_seed (bindings.cu:16-18), LLaMAConfig
 //   (llama_bindings.hpp:99-111).
 // Additions (new names only): TensorBF16, Tensor*.rmsnorm_rope, gqa_prefill,
-// gqa_decode, repeat_kv, pool_stats / pool_trim / pool_set_limit,
+// gqa_decode, repeat_kv, add_rmsnorm, silu_mul, pool_stats / pool_trim / pool_set_limit,
 // synchronize, set_stream / get_stream.
 //
 // Host tensors (is_cuda=False) support construction, copies, fill, views and
@@ -376,6 +376,23 @@ PyTensor<DT> rmsnorm_rope(const PyTensor<DT> &x, const PyTensor<DT> &wt, float e
 }
 
 template <int DT>
+py::tuple add_rmsnorm(const PyTensor<DT> &x, const PyTensor<DT> &delta, const PyTensor<DT> &wt,
+                      float eps) {
+  PyTensor<DT> h = x.like(), out = x.like();
+  bn_view xv = x.view(), dv = delta.view(), wv = wt.view(), hv = h.view(), ov = out.view();
+  check(bn_add_rmsnorm(&xv, &dv, &wv, &hv, &ov, eps, g_stream));
+  return py::make_tuple(h, out);
+}
+
+template <int DT>
+PyTensor<DT> silu_mul(const PyTensor<DT> &gate, const PyTensor<DT> &up) {
+  PyTensor<DT> out = gate.like();
+  bn_view gv = gate.view(), uv = up.view(), ov = out.view();
+  check(bn_silu_mul(&gv, &uv, &ov, g_stream));
+  return out;
+}
+
+template <int DT>
 PyTensor<DT> softmax(const PyTensor<DT> &x, bool causal, int off) {
   PyTensor<DT> out = x.like();
   bn_view xv = x.view(), ov = out.view();
@@ -593,6 +610,12 @@ PYBIND11_MODULE(bten, m) {
   m.def("gqa_decode", &gqa_decode<BN_BF16>, py::arg("q"), py::arg("k_cache"), py::arg("v_cache"),
         py::arg("seq_lens"), py::arg("n_heads") = 32, py::arg("n_kv_heads") = 4,
         py::arg("head_dim") = 64, py::arg("scale") = py::none());
+  m.def("add_rmsnorm", &add_rmsnorm<BN_F32>, py::arg("x"), py::arg("delta"), py::arg("weight"),
+        py::arg("eps") = 1e-6, "(x + delta, RMSNorm(x + delta) * weight) in one pass");
+  m.def("add_rmsnorm", &add_rmsnorm<BN_BF16>, py::arg("x"), py::arg("delta"), py::arg("weight"),
+        py::arg("eps") = 1e-6);
+  m.def("silu_mul", &silu_mul<BN_F32>, py::arg("gate"), py::arg("up"), "silu(gate) * up");
+  m.def("silu_mul", &silu_mul<BN_BF16>, py::arg("gate"), py::arg("up"));
   m.def("repeat_kv", &repeat_kv<BN_F32>, py::arg("kv"), py::arg("n_rep"), py::arg("head_dim") = 64);
   m.def("repeat_kv", &repeat_kv<BN_BF16>, py::arg("kv"), py::arg("n_rep"), py::arg("head_dim") = 64);
 

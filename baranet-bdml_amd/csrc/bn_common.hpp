@@ -109,10 +109,12 @@ template <typename T> struct Elem;
 template <> struct Elem<float> {
   __device__ static __forceinline__ float load(const float *p) { return *p; }
   __device__ static __forceinline__ void store(float *p, float v) { *p = v; }
+  __device__ static __forceinline__ float round(float v) { return v; }  // value as stored
 };
 template <> struct Elem<bf16_t> {
   __device__ static __forceinline__ float load(const bf16_t *p) { return bf16_to_f32(*p); }
   __device__ static __forceinline__ void store(bf16_t *p, float v) { *p = f32_to_bf16(v); }
+  __device__ static __forceinline__ float round(float v) { return bf16_to_f32(f32_to_bf16(v)); }
 };
 
 // --------------------------------------------------------- wave reductions

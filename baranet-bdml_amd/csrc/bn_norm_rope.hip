@@ -11,6 +11,8 @@
 // forms them (op_rope.cuh:82-83), sin/cos from the accurate device libm.
 // Any other view (transposes, column slices, odd widths) takes a strided
 // path with one workgroup per row.
+#include <algorithm>
+
 #include "bn_common.hpp"
 
 namespace bn {
@@ -133,6 +135,104 @@ __global__ __launch_bounds__(256) void rmsnorm_rows_kernel(
       }
       Chunk<T>::store(yr + c * VEC, o);
     }
+  }
+}
+
+// Residual add fused with the next RMSNorm (the decoder layer's
+// h = x + delta; y = RMSNorm(h) * w, llama_layers.hpp:241-272): one wave per
+// row, h written once and normalised from registers (bf16: the rounded h, as
+// a separate add would store it).  h may alias x (in-place residual update):
+// each lane reads its chunks before writing them.
+template <typename T, int NCH>
+__global__ __launch_bounds__(256) void add_rmsnorm_rows_kernel(
+    const T *x, int64_t x_rs, const T *__restrict__ dlt, int64_t d_rs, const T *__restrict__ w,
+    T *h, int64_t h_rs, T *__restrict__ y, int64_t y_rs, int rows, int cols, float eps) {
+  constexpr int VEC = Chunk<T>::VEC;
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int nchunks = cols / VEC;
+  raw16_t xraw[NCH], draw[NCH], wraw[NCH];
+#pragma unroll
+  for (int i = 0; i < NCH; ++i) {
+    const int cc = min(lane + 64 * i, nchunks - 1);
+    xraw[i] = load_raw(x + (int64_t)row * x_rs + cc * VEC);
+    draw[i] = load_raw(dlt + (int64_t)row * d_rs + cc * VEC);
+    wraw[i] = load_raw(w + cc * VEC);
+  }
+  float v[NCH][VEC];
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < NCH; ++i) {
+    float dv[VEC];
+    Chunk<T>::cvt(xraw[i], v[i]);
+    Chunk<T>::cvt(draw[i], dv);
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) v[i][j] = Elem<T>::round(v[i][j] + dv[j]);
+    if (lane + 64 * i < nchunks) {
+      Chunk<T>::store(h + (int64_t)row * h_rs + (lane + 64 * i) * VEC, v[i]);
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) ss += v[i][j] * v[i][j];
+    }
+  }
+  ss = wave_sum(ss);
+  const float rms = sqrtf(ss / (float)cols + eps);  // op_rmsnorm.cuh:44-45
+  const float inv_rms = 1.0f / rms;
+#pragma unroll
+  for (int i = 0; i < NCH; ++i) {
+    const int c = lane + 64 * i;
+    if (c < nchunks) {
+      float wv[VEC], o[VEC];
+      Chunk<T>::cvt(wraw[i], wv);
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) o[j] = (v[i][j] * inv_rms) * wv[j];
+      Chunk<T>::store(y + (int64_t)row * y_rs + c * VEC, o);
+    }
+  }
+}
+
+// SwiGLU activation: out = silu(gate) * up with silu(g) = g / (1 + exp(-g))
+// (op_silu.cuh:8-14 followed by op_multiply), one pass, 16-byte chunks.
+template <typename T>
+__global__ __launch_bounds__(256) void silu_mul_rows_kernel(const T *__restrict__ g, int64_t g_rs,
+                                                            const T *__restrict__ u, int64_t u_rs,
+                                                            T *__restrict__ o, int64_t o_rs,
+                                                            int rows, int cols) {
+  constexpr int VEC = Chunk<T>::VEC;
+  const int cpr = cols / VEC;  // chunks per row
+  const int64_t n = (int64_t)rows * cpr;
+  for (int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x; idx < n;
+       idx += (int64_t)gridDim.x * 256) {
+    const int r = (int)(idx / cpr), cc = (int)(idx - (int64_t)r * cpr);
+    float gv[VEC], uv[VEC], ov[VEC];
+    Chunk<T>::cvt(load_raw(g + (int64_t)r * g_rs + cc * VEC), gv);
+    Chunk<T>::cvt(load_raw(u + (int64_t)r * u_rs + cc * VEC), uv);
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) ov[j] = gv[j] / (1.0f + expf(-gv[j])) * uv[j];
+    Chunk<T>::store(o + (int64_t)r * o_rs + cc * VEC, ov);
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void silu_mul_strided_kernel(DView<const T> g, DView<const T> u,
+                                                               DView<T> o) {
+  const int64_t n = (int64_t)o.h * o.w;
+  for (int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x; idx < n;
+       idx += (int64_t)gridDim.x * 256) {
+    const int r = (int)(idx / o.w), c = (int)(idx - (int64_t)r * o.w);
+    const float gv = Elem<T>::load(&g.at(r, c));
+    Elem<T>::store(&o.at(r, c), gv / (1.0f + expf(-gv)) * Elem<T>::load(&u.at(r, c)));
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void add_strided_kernel(DView<const T> a, DView<const T> b,
+                                                          DView<T> c) {
+  const int64_t n = (int64_t)c.h * c.w;
+  for (int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x; idx < n;
+       idx += (int64_t)gridDim.x * 256) {
+    const int r = (int)(idx / c.w), col = (int)(idx - (int64_t)r * c.w);
+    Elem<T>::store(&c.at(r, col), Elem<T>::load(&a.at(r, col)) + Elem<T>::load(&b.at(r, col)));
   }
 }
 
@@ -332,6 +432,57 @@ int rope_common(const char *op, const bn_view *x, const bn_view *y, int pos_off,
   return BN_OK;
 }
 
+inline unsigned grid_for(int64_t n) { return (unsigned)std::min<int64_t>((n + 255) / 256, 8192); }
+
+template <typename T>
+int launch_add_rmsnorm(const bn_view *x, const bn_view *d, const bn_view *w, const bn_view *h,
+                       const bn_view *y, float eps, hipStream_t s) {
+  const int rows = x->h, cols = x->w;
+  constexpr int VEC = Chunk<T>::VEC;
+  const bool fast = rows_aligned(x, 16) && rows_aligned(d, 16) && rows_aligned(h, 16) &&
+                    rows_aligned(y, 16) && rows_aligned(w, 16) && cols % VEC == 0 &&
+                    cols <= 64 * kMaxChunks * VEC;
+  if (fast) {
+    const T *xp = (const T *)x->data + x->offset, *dp = (const T *)d->data + d->offset;
+    const T *wp = (const T *)w->data + w->offset;
+    T *hp = (T *)h->data + h->offset, *yp = (T *)y->data + y->offset;
+    dim3 grid((rows + kRowsPerBlock - 1) / kRowsPerBlock);
+    if (cols <= 64 * 4 * VEC)
+      hipLaunchKernelGGL((add_rmsnorm_rows_kernel<T, 4>), grid, dim3(256), 0, s, xp,
+                         (int64_t)x->stride_h, dp, (int64_t)d->stride_h, wp, hp,
+                         (int64_t)h->stride_h, yp, (int64_t)y->stride_h, rows, cols, eps);
+    else
+      hipLaunchKernelGGL((add_rmsnorm_rows_kernel<T, kMaxChunks>), grid, dim3(256), 0, s, xp,
+                         (int64_t)x->stride_h, dp, (int64_t)d->stride_h, wp, hp,
+                         (int64_t)h->stride_h, yp, (int64_t)y->stride_h, rows, cols, eps);
+    BN_LAUNCH_CHECK();
+    return BN_OK;
+  }
+  // any other views: the add, then RMSNorm of h (two launches)
+  hipLaunchKernelGGL((add_strided_kernel<T>), dim3(grid_for((int64_t)rows * cols)), dim3(256), 0, s,
+                     dview<const T>(x), dview<const T>(d), dview<T>(h));
+  BN_LAUNCH_CHECK();
+  RopeFreqs fr;
+  return launch_rmsnorm<T, false>(h, w, y, eps, 0, 2, fr, s);
+}
+
+template <typename T>
+int launch_silu_mul(const bn_view *g, const bn_view *u, const bn_view *o, hipStream_t s) {
+  const int rows = g->h, cols = g->w;
+  constexpr int VEC = Chunk<T>::VEC;
+  const int64_t n = (int64_t)rows * cols;
+  if (rows_aligned(g, 16) && rows_aligned(u, 16) && rows_aligned(o, 16) && cols % VEC == 0)
+    hipLaunchKernelGGL((silu_mul_rows_kernel<T>), dim3(grid_for(n / VEC)), dim3(256), 0, s,
+                       (const T *)g->data + g->offset, (int64_t)g->stride_h,
+                       (const T *)u->data + u->offset, (int64_t)u->stride_h,
+                       (T *)o->data + o->offset, (int64_t)o->stride_h, rows, cols);
+  else
+    hipLaunchKernelGGL((silu_mul_strided_kernel<T>), dim3(grid_for(n)), dim3(256), 0, s,
+                       dview<const T>(g), dview<const T>(u), dview<T>(o));
+  BN_LAUNCH_CHECK();
+  return BN_OK;
+}
+
 }  // namespace
 }  // namespace bn
 
@@ -348,6 +499,50 @@ int bn_rmsnorm_rope(const bn_view *x, const bn_view *weight, const bn_view *y, f
                     int position_offset, int head_dim, float theta, void *stream) {
   return rmsnorm_common("RMSNorm+RoPE", x, weight, y, eps, true, position_offset, head_dim,
                         theta, stream);
+}
+
+int bn_add_rmsnorm(const bn_view *x, const bn_view *delta, const bn_view *weight,
+                   const bn_view *h, const bn_view *y, float eps, void *stream) {
+  const char *op = "Add+RMSNorm";
+  const unsigned mask = (1u << BN_F32) | (1u << BN_BF16);
+  int st;
+  if ((st = check_view(x, op, "input", mask))) return st;
+  if ((st = check_view(delta, op, "residual", mask))) return st;
+  if ((st = check_view(weight, op, "weight", mask))) return st;
+  if ((st = check_view(h, op, "sum", mask))) return st;
+  if ((st = check_view(y, op, "output", mask))) return st;
+  if (!same_shape(x, delta) || !same_shape(x, h) || !same_shape(x, y))
+    return fail(BN_ERR_SHAPE, std::string(op) + ": input/residual/sum/output shape mismatch");
+  if (weight->h != 1 || weight->w != x->w)
+    return fail(BN_ERR_SHAPE, std::string(op) + ": weight shape must be (1, hidden_dim)");
+  if (delta->dtype != x->dtype || h->dtype != x->dtype || y->dtype != x->dtype ||
+      weight->dtype != x->dtype)
+    return fail(BN_ERR_UNSUPPORTED, std::string(op) + ": dtypes differ");
+  if ((st = require_device(op, {x, delta, weight, h, y}))) return st;
+  if ((st = ensure_device())) return st;
+  if (x->h == 0 || x->w == 0) return BN_OK;
+  hipStream_t s = as_stream(stream);
+  return x->dtype == BN_F32 ? launch_add_rmsnorm<float>(x, delta, weight, h, y, eps, s)
+                            : launch_add_rmsnorm<bf16_t>(x, delta, weight, h, y, eps, s);
+}
+
+int bn_silu_mul(const bn_view *gate, const bn_view *up, const bn_view *out, void *stream) {
+  const char *op = "SiLU*up";
+  const unsigned mask = (1u << BN_F32) | (1u << BN_BF16);
+  int st;
+  if ((st = check_view(gate, op, "gate", mask))) return st;
+  if ((st = check_view(up, op, "up", mask))) return st;
+  if ((st = check_view(out, op, "output", mask))) return st;
+  if (!same_shape(gate, up) || !same_shape(gate, out))
+    return fail(BN_ERR_SHAPE, std::string(op) + ": gate/up/output shape mismatch");
+  if (up->dtype != gate->dtype || out->dtype != gate->dtype)
+    return fail(BN_ERR_UNSUPPORTED, std::string(op) + ": dtypes differ");
+  if ((st = require_device(op, {gate, up, out}))) return st;
+  if ((st = ensure_device())) return st;
+  if (gate->h == 0 || gate->w == 0) return BN_OK;
+  hipStream_t s = as_stream(stream);
+  return gate->dtype == BN_F32 ? launch_silu_mul<float>(gate, up, out, s)
+                               : launch_silu_mul<bf16_t>(gate, up, out, s);
 }
 
 int bn_rope(const bn_view *x, const bn_view *y, int position_offset, int head_dim, float theta,

@@ -6,19 +6,22 @@ a prompt prefill followed by greedy decode steps.
 
 The decoder layer follows the reference (src/llama/llama_layers.hpp:241-272,
 src/llama/llama_model.hpp:52-80): x -> RMSNorm -> GQA -> +x -> RMSNorm ->
-SwiGLU MLP -> +x, final RMSNorm, lm_head.  The reference keeps no KV cache
+SwiGLU MLP -> +x, final RMSNorm, lm_head.  Each residual add runs fused with
+the RMSNorm that follows it (bn_add_rmsnorm), and the SwiGLU activation
+silu(gate) * up is one kernel (bn_silu_mul).  The reference keeps no KV cache
 (llama_model.py:135-141 reruns the prefix); this driver keeps one per layer
 ([1, max_len, Hkv, 64]) and decodes the new token with the split-K decode
 kernel.  Per-head GQA semantics (query head h reads KV head h // 8).
 
-RMSNorm, RoPE, prefill attention and decode attention run on the HIP kernels
-through the C ABI (bnhip).  The Q, K and V projections are one GEMM against
-the concatenated weight [hidden, (H + 2*Hkv)*64]; RoPE rotates the Q and K
-columns of its output in place in one launch (same positions for every head
-block), and attention reads Q, K and V as column slices of that row.  The dense projections, SwiGLU and the embedding
-gather are plain torch GPU operations (library GEMMs): they are not part of
-the attention path, and the config's metric times only the attention, RoPE
-and RMSNorm kernels.  ``path_ms`` accumulates hip-event time around those
+RMSNorm (plain and fused with the residual add), RoPE, prefill attention,
+decode attention and the SwiGLU activation run on the HIP kernels through the
+C ABI (bnhip).  The Q, K and V projections are one GEMM against the
+concatenated weight [hidden, (H + 2*Hkv)*64]; RoPE rotates the Q and K columns
+of its output in place in one launch (same positions for every head block),
+and attention reads Q, K and V as column slices of that row.  The dense
+projections and the embedding gather are plain torch GPU operations (library
+GEMMs): they are not part of the attention path, and the config's metric
+times only the attention, RoPE and RMSNorm kernels.  ``path_ms`` accumulates hip-event time around those
 kernel launches (an upper bound on their device time; the rocprofv3 kernel
 trace gives the exact per-kernel durations).
 """
@@ -107,6 +110,27 @@ class TinyLlama:
         self._record("rmsnorm", [x, weight], y, eps=self.cfg.rms_norm_eps)
         return y
 
+    def add_rmsnorm(self, hdn, delta, weight):
+        """hdn += delta in place; returns (hdn, RMSNorm(hdn) * weight)."""
+        before = hdn.clone() if self.trace is not None else None
+        y = torch.empty_like(hdn)
+
+        def run():
+            bnhip.call("bn_add_rmsnorm", C.byref(bnhip.view(hdn)), C.byref(bnhip.view(delta)),
+                       C.byref(bnhip.view(weight)), C.byref(bnhip.view(hdn)), C.byref(bnhip.view(y)),
+                       self.cfg.rms_norm_eps, bnhip.stream_of())
+        self._timed(run)
+        if self.trace is not None:
+            self._record("add_rmsnorm", [before, delta, weight], torch.stack([hdn, y]),
+                         eps=self.cfg.rms_norm_eps)
+        return hdn, y
+
+    def silu_mul(self, gate, up):
+        out = torch.empty_like(gate)
+        bnhip.call("bn_silu_mul", C.byref(bnhip.view(gate)), C.byref(bnhip.view(up)),
+                   C.byref(bnhip.view(out)), bnhip.stream_of())
+        return out
+
     def rope_(self, x, offset):
         """RoPE in place on a (possibly strided) [rows, heads*64] view."""
         before = x.clone() if self.trace is not None else None
@@ -141,10 +165,10 @@ class TinyLlama:
         return o.view(1, cfg.hidden_size)
 
     # ------------------------------------------------------------ model
-    def _layer(self, hdn, L, pos0):
+    def _attention(self, x, L, pos0):
+        """Attention of one layer on the normalised rows x; returns o @ W_o."""
         cfg = self.cfg
-        n = hdn.shape[0]
-        x = self.rmsnorm(hdn, L["ln1"])
+        n = x.shape[0]
         hq, hk = cfg.hidden_size, cfg.num_key_value_heads * cfg.head_dim
         qkv = x @ L["wqkv"]                       # [n, hq + 2*hk]
         self.rope_(qkv[:, :hq + hk], pos0)        # Q and K columns, one launch
@@ -155,30 +179,33 @@ class TinyLlama:
             o = self.prefill_attention(q, k, v)
         else:
             o = self.decode_attention(q, L, pos0 + 1)
-        hdn = hdn + o @ L["wo"]
-        x = self.rmsnorm(hdn, L["ln2"])
-        return hdn + (torch.nn.functional.silu(x @ L["wg"]) * (x @ L["wu"])) @ L["wd"]
+        return o @ L["wo"]
 
-    def _logits(self, hdn):
-        return self.rmsnorm(hdn[-1:], self.ln_f) @ self.lm_head
+    def _forward(self, hdn, pos0):
+        """Decoder layers over rows hdn (positions pos0..); returns the final
+        norm of every row.  Each residual add is fused with the RMSNorm that
+        follows it (the next layer's input norm, or the final norm)."""
+        x = self.rmsnorm(hdn, self.layers[0]["ln1"])
+        for i, L in enumerate(self.layers):
+            hdn, x = self.add_rmsnorm(hdn, self._attention(x, L, pos0), L["ln2"])
+            mlp = self.silu_mul(x @ L["wg"], x @ L["wu"]) @ L["wd"]
+            nxt = self.layers[i + 1]["ln1"] if i + 1 < len(self.layers) else self.ln_f
+            hdn, x = self.add_rmsnorm(hdn, mlp, nxt)
+        return x
 
     def prefill(self, ids: torch.Tensor) -> torch.Tensor:
         """Process the prompt (positions 0..S-1); returns last-row logits."""
         assert self.length == 0 and ids.numel() <= self.max_len
-        hdn = self.embed[ids]
-        for L in self.layers:
-            hdn = self._layer(hdn, L, 0)
+        xf = self._forward(self.embed[ids], 0)
         self.length = ids.numel()
-        return self._logits(hdn)
+        return xf[-1:] @ self.lm_head
 
     def step(self, token: torch.Tensor) -> torch.Tensor:
         """Append one token at position `length`; returns its logits."""
         assert self.length < self.max_len
-        hdn = self.embed[token.view(1)]
-        for L in self.layers:
-            hdn = self._layer(hdn, L, self.length)
+        xf = self._forward(self.embed[token.view(1)], self.length)
         self.length += 1
-        return self._logits(hdn)
+        return xf @ self.lm_head
 
     def generate(self, ids: torch.Tensor, new_tokens: int, time_path: bool = False):
         """Greedy decode; returns the generated ids and the path-kernel ms."""

@@ -251,7 +251,8 @@ def bench_tinyllama(prompt=512, new_tokens=128, cpu=True, warmup_tokens=2):
     wall = time.perf_counter() - t0
     res = {"prompt": prompt, "new_tokens": new_tokens, "wall_s": round(wall, 3),
            "path_ms": round(path_ms, 3),
-           "path_kernels": "RMSNorm, RoPE, GQA prefill, GQA decode (fp32)",
+           "path_kernels": "RMSNorm (plain and fused with the residual add), RoPE, GQA prefill, "
+                           "GQA decode (fp32)",
            "first_tokens": [int(t) for t in toks[:8].cpu()], "cache_length_end": m.length}
     if cpu:
         res["cpu_baseline"] = cpu_baseline_tinyllama(m, ids)

@@ -115,6 +115,17 @@ int bn_rope_backward(const bn_view *dy, const bn_view *dx, int position_offset,
 int bn_rmsnorm_rope(const bn_view *x, const bn_view *weight, const bn_view *y,
                     float eps, int position_offset, int head_dim, float theta,
                     void *stream);
+/* The decoder layer's residual add and the next RMSNorm in one pass
+ * (llama_layers.hpp:241-272: x -> RMSNorm -> attention -> +x -> RMSNorm ->
+ * MLP -> +x): h = x + delta, y = RMSNorm(h) * weight (op_rmsnorm
+ * arithmetic).  h may alias x.  The reference's own fused kernel,
+ * op_rmsnorm_residual (op_mm_optimized.cuh:93-162, unused there), adds the
+ * residual after the norm; this is the pre-norm order the layer needs. */
+int bn_add_rmsnorm(const bn_view *x, const bn_view *delta, const bn_view *weight,
+                   const bn_view *h, const bn_view *y, float eps, void *stream);
+/* SwiGLU activation: out = silu(gate) * up, silu(g) = g / (1 + exp(-g))
+ * (op_silu.cuh:8-14 then op_multiply, llama_layers.hpp:199-211), one pass. */
+int bn_silu_mul(const bn_view *gate, const bn_view *up, const bn_view *out, void *stream);
 /* op_softmax (src/ops/op_softmax.cuh:153-180): row softmax; with causal,
  * column i of row r is kept iff i <= r + seq_offset, masked outputs are 0. */
 int bn_softmax(const bn_view *x, const bn_view *y, int causal, int seq_offset,

@@ -107,6 +107,23 @@ def rmsnorm_backward(x, weight, dy, eps=1e-6):
     return dx, dw
 
 
+def add_rmsnorm(x, delta, weight, eps=1e-6):
+    """Decoder-layer residual add then RMSNorm (llama_layers.hpp:241-272):
+    h = x + delta elementwise in fp32 (op_add, op_elemwise.cuh:77-88 shape),
+    y = rmsnorm(h) as op_rmsnorm computes it.  Returns (h, y)."""
+    h = (_f32(x) + _f32(delta)).astype(np.float32)
+    return h, rmsnorm(h, weight, eps)
+
+
+def silu_mul(gate, up):
+    """SwiGLU activation: SiLUFunc g / (1 + exp(-g)) (op_silu.cuh:8-14) on the
+    gate, then the elementwise product with up (op_multiply), fp32."""
+    g = _f32(gate)
+    with np.errstate(over="ignore"):
+        s = g / (np.float32(1) + np.exp(-g))
+    return (s * _f32(up)).astype(np.float32)
+
+
 def rope_freq(pair, head_dim, theta):
     return lib().or_rope_freq(pair, head_dim, theta)
 

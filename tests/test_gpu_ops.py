@@ -61,6 +61,69 @@ def test_rmsnorm_strided_view():
     assert_close(host(yd), O.rmsnorm(big[2:9, 100:356], wt, 1e-6), FP32_TOL)
 
 
+@pytest.mark.parametrize("rows,w,dtype,inplace", [(7, 2048, "f32", False), (512, 2048, "f32", True),
+                                                  (1, 2048, "f32", True), (5, 300, "f32", False),
+                                                  (64, 2048, "bf16", False), (9, 300, "bf16", True),
+                                                  (3, 6000, "f32", False)])
+def test_add_rmsnorm(rows, w, dtype, inplace):
+    """h = x + delta, y = RMSNorm(h): fast path (rows in registers), the
+    composed fallback (bf16 width 300, width 6000), and h written over x."""
+    r = rng(21)
+    x = r.standard_normal((rows, w)).astype(np.float32)
+    d = r.standard_normal((rows, w)).astype(np.float32)
+    wt = r.standard_normal((1, w)).astype(np.float32)
+    td = torch.bfloat16 if dtype == "bf16" else torch.float32
+    if dtype == "bf16":
+        x, d, wt = bf16_round(x), bf16_round(d), bf16_round(wt)
+    xd, dd, wd = dev(x, td), dev(d, td), dev(wt, td)
+    hd = xd if inplace else torch.empty_like(xd)
+    yd = torch.empty_like(xd)
+    B.call("bn_add_rmsnorm", V(xd), V(dd), V(wd), V(hd), V(yd), 1e-5, S0)
+    h_ref, y_ref = O.add_rmsnorm(x, d, wt, 1e-5)
+    if dtype == "bf16":  # h is stored in bf16 and the norm reads the stored h
+        h_ref = bf16_round(h_ref)
+        y_ref = O.rmsnorm(h_ref, wt, 1e-5)
+    tol = BF16_TOL if dtype == "bf16" else FP32_TOL
+    assert_close(host(hd), h_ref, tol, "h")
+    assert_close(host(yd), y_ref, tol, "y")
+
+
+def test_add_rmsnorm_strided_views():
+    r = rng(22)
+    big = r.standard_normal((10, 600)).astype(np.float32)
+    dl = r.standard_normal((7, 256)).astype(np.float32)
+    wt = r.standard_normal((1, 256)).astype(np.float32)
+    bd, dd, wd = dev(big), dev(dl), dev(wt)
+    xv = bd[2:9, 100:356]
+    hd, yd = torch.empty((7, 256), device="cuda"), torch.empty((7, 256), device="cuda")
+    B.call("bn_add_rmsnorm", V(xv), V(dd), V(wd), V(hd), V(yd), 1e-6, S0)
+    h_ref, y_ref = O.add_rmsnorm(big[2:9, 100:356], dl, wt, 1e-6)
+    assert_close(host(hd), h_ref, FP32_TOL, "h")
+    assert_close(host(yd), y_ref, FP32_TOL, "y")
+
+
+@pytest.mark.parametrize("rows,w,dtype", [(512, 5632, "f32"), (1, 5632, "f32"), (7, 300, "f32"),
+                                          (64, 5632, "bf16"), (3, 36, "bf16")])
+def test_silu_mul(rows, w, dtype):
+    r = rng(23)
+    g = (r.standard_normal((rows, w)) * 3).astype(np.float32)
+    u = r.standard_normal((rows, w)).astype(np.float32)
+    g[0, :4] = [0.0, -200.0, 200.0, -1e30]  # exp overflow must give -0, not NaN
+    td = torch.bfloat16 if dtype == "bf16" else torch.float32
+    if dtype == "bf16":
+        g, u = bf16_round(g), bf16_round(u)
+    gd, ud = dev(g, td), dev(u, td)
+    od = torch.empty_like(gd)
+    B.call("bn_silu_mul", V(gd), V(ud), V(od), S0)
+    out = host(od)
+    assert np.all(np.isfinite(out))
+    assert_close(out, O.silu_mul(g, u), BF16_TOL if dtype == "bf16" else FP32_TOL, "silu_mul")
+    # strided operands (transposed views) take the element kernel
+    od2 = torch.empty((w, rows), device="cuda", dtype=td).t()
+    B.call("bn_silu_mul", V(gd), V(ud), V(od2), S0)
+    assert_close(host(od2), O.silu_mul(g, u), BF16_TOL if dtype == "bf16" else FP32_TOL, "silu_mul T")
+
+
 @pytest.mark.parametrize("rows,w,D,off,dtype", [(16, 2048, 64, 0, "f32"), (3, 256, 64, 511, "f32"),
                                                 (4, 64, 32, 7, "f32"), (8, 2048, 64, 16383, "f32"),
                                                 (32, 2048, 64, 100, "bf16")])
@@ -143,6 +206,21 @@ def test_matmul(m, k, n):
     bt = dev(np.ascontiguousarray(b.T))
     B.call("bn_matmul", V(ad), V(bt.t()), V(cd), S0)
     assert_close(host(cd), O.matmul(a, b), FP32_TOL, "matmul(T view)")
+
+
+@pytest.mark.parametrize("m,k,n", [(70, 130, 50), (128, 512, 256)])
+def test_matmul_strided_views(m, k, n):
+    """Operands with no unit stride (every other column) and a transposed
+    output take the hand-written MFMA kernel instead of the library GEMM."""
+    r = rng(18)
+    a2 = r.standard_normal((m, 2 * k)).astype(np.float32)
+    b2 = r.standard_normal((k, 2 * n)).astype(np.float32)
+    ad, bd = dev(a2)[:, ::2], dev(b2)[:, ::2]
+    ct = torch.zeros((n, m), device="cuda")
+    c = ct.t()  # stride (1, m): a transposed output view
+    B.call("bn_matmul", V(ad), V(bd), V(c), S0)
+    ref = a2[:, ::2].astype(np.float64) @ b2[:, ::2]
+    assert_close(host(c), ref, FP32_TOL, "matmul strided")
 
 
 def test_repeat_kv_exact():

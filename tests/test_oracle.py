@@ -60,6 +60,39 @@ def test_rmsnorm_matches_torch():
     assert relerr(O.rmsnorm(x, wt, 1e-6), ref.numpy()) < 2e-6
 
 
+def test_add_rmsnorm_closed_form_and_reduction():
+    r = rng(31)
+    x = r.standard_normal((6, 2048)).astype(np.float32)
+    d = r.standard_normal((6, 2048)).astype(np.float32)
+    wt = r.standard_normal((1, 2048)).astype(np.float32)
+    h, y = O.add_rmsnorm(x, d, wt, 1e-5)
+    h64 = x.astype(np.float64) + d
+    np.testing.assert_array_equal(h, (x + d).astype(np.float32))   # fp32 add, exact
+    ref = h64 / np.sqrt((h64 ** 2).mean(1, keepdims=True) + 1e-5) * wt
+    assert relerr(y, ref) < 2e-6
+    # delta = 0 reduces to the plain RMSNorm
+    h0, y0 = O.add_rmsnorm(x, np.zeros_like(x), wt, 1e-5)
+    np.testing.assert_array_equal(h0, x)
+    np.testing.assert_array_equal(y0, O.rmsnorm(x, wt, 1e-5))
+
+
+def test_silu_mul_closed_form_and_limits():
+    r = rng(32)
+    g = (r.standard_normal((5, 300)) * 4).astype(np.float32)
+    u = r.standard_normal((5, 300)).astype(np.float32)
+    g64 = g.astype(np.float64)
+    ref = g64 / (1.0 + np.exp(-g64)) * u
+    assert relerr(O.silu_mul(g, u), ref) < 1e-6
+    # silu(0) = 0, silu(g) -> g for large g, -> -0 for very negative g (no NaN)
+    edge = np.array([[0.0, 30.0, -30.0, -1000.0, 1000.0]], np.float32)
+    out = O.silu_mul(edge, np.ones_like(edge))
+    assert out[0, 0] == 0.0 and abs(out[0, 1] - 30.0) < 1e-5 and abs(out[0, 2]) < 1e-10
+    assert out[0, 3] == 0.0 and out[0, 4] == 1000.0 and np.all(np.isfinite(out))
+    # torch's SiLU on the same values (an independent implementation)
+    t = torch.nn.functional.silu(torch.from_numpy(g64)) * torch.from_numpy(u.astype(np.float64))
+    assert relerr(O.silu_mul(g, u), t.numpy()) < 1e-6
+
+
 # ---------------------------------------------------------------- RoPE
 def rope_complex_fp64(x, pos_off, D, theta):
     """Independent restatement: interleaved pairs as complex numbers rotated by
