@@ -192,7 +192,9 @@ __global__ __launch_bounds__(256) void add_rmsnorm_rows_kernel(
 }
 
 // SwiGLU activation: out = silu(gate) * up with silu(g) = g / (1 + exp(-g))
-// (op_silu.cuh:8-14 followed by op_multiply), one pass, 16-byte chunks.
+// (op_silu.cuh:8-14 followed by op_multiply), one pass over 16-byte chunks:
+// each thread requests its SCPT chunks of gate and up before the first use.
+constexpr int SCPT = 4;
 template <typename T>
 __global__ __launch_bounds__(256) void silu_mul_rows_kernel(const T *__restrict__ g, int64_t g_rs,
                                                             const T *__restrict__ u, int64_t u_rs,
@@ -201,15 +203,28 @@ __global__ __launch_bounds__(256) void silu_mul_rows_kernel(const T *__restrict_
   constexpr int VEC = Chunk<T>::VEC;
   const int cpr = cols / VEC;  // chunks per row
   const int64_t n = (int64_t)rows * cpr;
-  for (int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x; idx < n;
-       idx += (int64_t)gridDim.x * 256) {
+  const int64_t first = (int64_t)blockIdx.x * 256 * SCPT + threadIdx.x;
+  raw16_t graw[SCPT], uraw[SCPT];
+  int64_t goff[SCPT], uoff[SCPT], ooff[SCPT];
+#pragma unroll
+  for (int k = 0; k < SCPT; ++k) {
+    const int64_t idx = min(first + 256 * k, n - 1);  // clamped: in range, stored only if valid
     const int r = (int)(idx / cpr), cc = (int)(idx - (int64_t)r * cpr);
+    goff[k] = (int64_t)r * g_rs + cc * VEC;
+    uoff[k] = (int64_t)r * u_rs + cc * VEC;
+    ooff[k] = (int64_t)r * o_rs + cc * VEC;
+    graw[k] = load_raw(g + goff[k]);
+    uraw[k] = load_raw(u + uoff[k]);
+  }
+#pragma unroll
+  for (int k = 0; k < SCPT; ++k) {
+    if (first + 256 * k >= n) break;
     float gv[VEC], uv[VEC], ov[VEC];
-    Chunk<T>::cvt(load_raw(g + (int64_t)r * g_rs + cc * VEC), gv);
-    Chunk<T>::cvt(load_raw(u + (int64_t)r * u_rs + cc * VEC), uv);
+    Chunk<T>::cvt(graw[k], gv);
+    Chunk<T>::cvt(uraw[k], uv);
 #pragma unroll
     for (int j = 0; j < VEC; ++j) ov[j] = gv[j] / (1.0f + expf(-gv[j])) * uv[j];
-    Chunk<T>::store(o + (int64_t)r * o_rs + cc * VEC, ov);
+    Chunk<T>::store(o + ooff[k], ov);
   }
 }
 
@@ -472,7 +487,8 @@ int launch_silu_mul(const bn_view *g, const bn_view *u, const bn_view *o, hipStr
   constexpr int VEC = Chunk<T>::VEC;
   const int64_t n = (int64_t)rows * cols;
   if (rows_aligned(g, 16) && rows_aligned(u, 16) && rows_aligned(o, 16) && cols % VEC == 0)
-    hipLaunchKernelGGL((silu_mul_rows_kernel<T>), dim3(grid_for(n / VEC)), dim3(256), 0, s,
+    hipLaunchKernelGGL((silu_mul_rows_kernel<T>), dim3((unsigned)((n / VEC + 256 * SCPT - 1) / (256 * SCPT))),
+                       dim3(256), 0, s,
                        (const T *)g->data + g->offset, (int64_t)g->stride_h,
                        (const T *)u->data + u->offset, (int64_t)u->stride_h,
                        (T *)o->data + o->offset, (int64_t)o->stride_h, rows, cols);

@@ -14,6 +14,8 @@ Also measured in the same run and reported as sub-objects:
   prefill_fp32  config 2 in fp32
   rmsnorm_rope  config 5's fused RMSNorm+RoPE on [16384, 2048] bf16, GB/s
   prefill_long  config 5's prefill, B=1, S=16384, bf16
+  add_rmsnorm   fused residual add + RMSNorm, bf16 [16384, 2048], GB/s
+  silu_mul      SwiGLU activation, bf16 [16384, 5632], GB/s
 Each carries a ``roofline`` object priced against MI355X peaks (bf16 MFMA
 2.5 PFLOP/s dense, fp32 MFMA 157.3 TFLOP/s, HBM 8 TB/s).  ``cpu_baseline``
 times the CPU oracle (a single-threaded C restatement of the reference
@@ -172,6 +174,58 @@ def bench_rmsnorm_rope(steps, warmup):
     return {"value": round(gbs, 2), "unit": "GB/s", "ms_per_launch": round(ms, 5),
             "bytes_per_launch": nb,
             "roofline": roofline("hbm", gbs, PEAK_HBM_GBS, "GB/s", measured_traffic("rmsnorm_rope"))}
+
+
+def bench_add_rmsnorm(steps, warmup):
+    """Fused residual add + RMSNorm on a config-5-sized bf16 row block
+    [16384, 2048]: read x, delta (and the weight), write h and y."""
+    import ctypes as C
+    import torch
+    import bnhip
+    rows, w = 16384, 2048
+    g = torch.Generator(device="cuda").manual_seed(6)
+    sets = [[torch.randn((rows, w), generator=g, device="cuda").bfloat16() for _ in range(4)]
+            for _ in range(2)]  # 2 x 268 MB > 256 MB MALL
+    wt = torch.ones((1, w), device="cuda", dtype=torch.bfloat16)
+    wv = bnhip.view(wt)
+    views = [[bnhip.view(t) for t in st] for st in sets]
+    st_ = bnhip.stream_of()
+
+    def run(i):
+        xv, dv, hv, yv = views[i % 2]
+        bnhip.call("bn_add_rmsnorm", C.byref(xv), C.byref(dv), C.byref(wv), C.byref(hv), C.byref(yv),
+                   1e-5, st_)
+
+    ms = time_launches(run, steps, warmup)
+    nb = 4 * rows * w * 2 + w * 2
+    gbs = nb / (ms * 1e-3) / 1e9
+    return {"value": round(gbs, 2), "unit": "GB/s", "ms_per_launch": round(ms, 5),
+            "bytes_per_launch": nb, "shape": [rows, w], "dtype": "bf16",
+            "roofline": roofline("hbm", gbs, PEAK_HBM_GBS, "GB/s", measured_traffic("add_rmsnorm"))}
+
+
+def bench_silu_mul(steps, warmup):
+    """SwiGLU activation silu(gate) * up on a [16384, 5632] bf16 block (the
+    TinyLLaMA MLP width at config 5's row count): read gate and up, write out."""
+    import ctypes as C
+    import torch
+    import bnhip
+    rows, w = 16384, 5632
+    g = torch.Generator(device="cuda").manual_seed(7)
+    gt, ut = (torch.randn((rows, w), generator=g, device="cuda").bfloat16() for _ in range(2))
+    ot = torch.empty_like(gt)
+    gv, uv, ov = bnhip.view(gt), bnhip.view(ut), bnhip.view(ot)
+    st_ = bnhip.stream_of()
+
+    def run(i):
+        bnhip.call("bn_silu_mul", C.byref(gv), C.byref(uv), C.byref(ov), st_)
+
+    ms = time_launches(run, steps, warmup)
+    nb = 3 * rows * w * 2  # 554 MB per launch: larger than the MALL
+    gbs = nb / (ms * 1e-3) / 1e9
+    return {"value": round(gbs, 2), "unit": "GB/s", "ms_per_launch": round(ms, 5),
+            "bytes_per_launch": nb, "shape": [rows, w], "dtype": "bf16",
+            "roofline": roofline("hbm", gbs, PEAK_HBM_GBS, "GB/s", measured_traffic("silu_mul"))}
 
 
 def bench_copy(steps, warmup):
@@ -342,7 +396,7 @@ def main():
                          "so a kernel trace holds exactly one prefill + 128 steps)")
     ap.add_argument("--only", default="",
                     help="comma list of extra workloads (default: all but copy): "
-                         "decode,ragged,fp32,norm,long,block,tinyllama,copy; "
+                         "decode,ragged,fp32,norm,long,addnorm,swiglu,block,tinyllama,copy; "
                          "'head' = headline prefill only")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -386,6 +440,12 @@ def main():
         out["prefill_long"] = bench_prefill(1, 16384, 32, 4, "bf16", max(K // 4, 3), 1)
         print(f"prefill S=16384: {out['prefill_long']['value']} TFLOP/s", file=sys.stderr,
               flush=True)
+    if want("addnorm"):
+        out["add_rmsnorm"] = bench_add_rmsnorm(K, W)
+        print(f"add_rmsnorm: {out['add_rmsnorm']['value']} GB/s", file=sys.stderr, flush=True)
+    if want("swiglu"):
+        out["silu_mul"] = bench_silu_mul(K, W)
+        print(f"silu_mul: {out['silu_mul']['value']} GB/s", file=sys.stderr, flush=True)
     if want("block"):
         out["attention_block"], blk_inputs = bench_block(K, W)
         if not args.no_cpu:
