@@ -215,6 +215,69 @@ def gqa_decode(q, k_cache, v_cache, seq_lens, scale):
     return o
 
 
+def _visible(Sq, Skv, causal, seq_offset):
+    """Mask of visible keys: key j for query row i iff j <= i + seq_offset
+    (op_softmax.cuh:89-99) and j < Skv."""
+    i = np.arange(Sq)[:, None]
+    j = np.arange(Skv)[None, :]
+    return (j <= i + seq_offset) if causal else np.ones((Sq, Skv), bool)
+
+
+def gqa_prefill_lse(q, k, scale, causal=True, seq_offset=0):
+    """Row log-sum-exp (natural log) of the scaled, masked scores per query head:
+    lse[b, h, i] = log sum_{visible j} exp(scale * q_i . k_j), fp64; -inf for a
+    row with no visible key.  Returns float64 [B, H, Sq]."""
+    q, k = np.asarray(q, np.float64), np.asarray(k, np.float64)
+    B, Sq, H, D = q.shape
+    _, Skv, Hkv, _ = k.shape
+    G = H // Hkv
+    vis = _visible(Sq, Skv, causal, seq_offset)
+    out = np.empty((B, H, Sq))
+    for b in range(B):
+        for h in range(H):
+            s = scale * q[b, :, h] @ k[b, :, h // G].T
+            s = np.where(vis, s, -np.inf)
+            m = s.max(1, keepdims=True)
+            mf = np.where(np.isfinite(m), m, 0.0)
+            with np.errstate(divide="ignore"):
+                out[b, h] = (mf + np.log(np.exp(s - mf).sum(1, keepdims=True)))[:, 0]
+    return out
+
+
+def gqa_prefill_backward(q, k, v, do, scale, causal=True, seq_offset=0):
+    """Gradients of o = gqa_prefill(q, k, v) for the upstream gradient do,
+    composed per query head h (KV head g = h // (H/Hkv)) from the backward of
+    the reference chain's primitives: S = Q_h K_g^T, P = softmax(scale*S,
+    causal, seq_offset); dP = dO_h V_g^T and dV_g += P^T dO_h (op_mm's
+    backward); dS = P * (dP - rowsum(P * dP)) (op_softmax_backward,
+    op_softmax.cuh:182-246); dQ_h = scale dS K_g, dK_g += scale dS^T Q_h (the
+    scale, op_elemwise.cuh:436-451); repeat_kv's backward sums the G query
+    heads of a KV head (llama_layers.hpp:159-163).  fp64; returns float32
+    (dq, dk, dv) shaped like (q, k, v).  Rows with no visible key have P = 0."""
+    q, k, v, do = (np.asarray(a, np.float64) for a in (q, k, v, do))
+    B, Sq, H, D = q.shape
+    _, Skv, Hkv, _ = k.shape
+    G = H // Hkv
+    vis = _visible(Sq, Skv, causal, seq_offset)
+    dq, dk, dv = np.zeros_like(q), np.zeros_like(k), np.zeros_like(v)
+    for b in range(B):
+        for h in range(H):
+            g = h // G
+            s = scale * q[b, :, h] @ k[b, :, g].T
+            s = np.where(vis, s, -np.inf)
+            m = s.max(1, keepdims=True)
+            m = np.where(np.isfinite(m), m, 0.0)
+            e = np.where(vis, np.exp(s - m), 0.0)
+            tot = e.sum(1, keepdims=True)
+            p = np.divide(e, tot, out=np.zeros_like(e), where=tot > 0)
+            dp = do[b, :, h] @ v[b, :, g].T
+            ds = p * (dp - (p * dp).sum(1, keepdims=True))
+            dq[b, :, h] = scale * ds @ k[b, :, g]
+            dk[b, :, g] += scale * ds.T @ q[b, :, h]
+            dv[b, :, g] += p.T @ do[b, :, h]
+    return dq.astype(np.float32), dk.astype(np.float32), dv.astype(np.float32)
+
+
 def gqa_layer(x, wq, wk, wv, wo, n_heads, n_kv_heads, theta=10000.0,
               position_offset=0, per_head=False):
     x = _f32(x)

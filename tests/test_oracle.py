@@ -407,3 +407,61 @@ def test_checks_catch_planted_pair_slip():
     perm = np.arange(64).reshape(2, 32).T.reshape(-1)   # interleave halves
     wrong = O.rope(x[:, perm], 2, 64, 1e4)[:, np.argsort(perm)]
     assert relerr(wrong, rope_complex_fp64(x, 2, 64, 1e4)) > 1e-2
+
+
+# ---------------------------------------------------- attention backward
+@pytest.mark.parametrize("B,Sq,Skv,H,Hkv,causal,off", [(1, 40, 40, 8, 2, True, 0), (2, 17, 30, 4, 4, True, 13),
+                                                       (1, 24, 24, 8, 1, False, 0), (1, 9, 12, 2, 1, True, -3)])
+def test_gqa_prefill_backward_vs_torch_autograd(B, Sq, Skv, H, Hkv, causal, off):
+    """The composed backward equals torch fp64 autograd through an explicit
+    GQA attention (repeat_interleave of K/V, masked softmax)."""
+    r = rng(41)
+    q = r.standard_normal((B, Sq, H, 64))
+    k = r.standard_normal((B, Skv, Hkv, 64))
+    v = r.standard_normal((B, Skv, Hkv, 64))
+    do = r.standard_normal((B, Sq, H, 64))
+    dq, dk, dv = O.gqa_prefill_backward(q, k, v, do, 0.125, causal, off)
+    tq, tk, tv = (torch.tensor(a, requires_grad=True) for a in (q, k, v))
+    G = H // Hkv
+    kr = tk.repeat_interleave(G, dim=2)
+    vr = tv.repeat_interleave(G, dim=2)
+    s = torch.einsum("bqhd,bkhd->bhqk", tq, kr) * 0.125
+    i = torch.arange(Sq)[:, None]
+    j = torch.arange(Skv)[None, :]
+    vis = (j <= i + off) if causal else torch.ones(Sq, Skv, dtype=torch.bool)
+    s = s.masked_fill(~vis, float("-inf"))
+    p = torch.softmax(s, -1).nan_to_num(0.0)   # rows with no visible key -> 0
+    o = torch.einsum("bhqk,bkhd->bqhd", p, vr)
+    o.backward(torch.tensor(do))
+    assert relerr(dq, tq.grad.numpy()) < 1e-6
+    assert relerr(dk, tk.grad.numpy()) < 1e-6
+    assert relerr(dv, tv.grad.numpy()) < 1e-6
+
+
+def test_gqa_prefill_lse_closed_form():
+    """lse is the log of the softmax denominator: exp(scale*s - lse) sums to 1
+    over the visible keys, and matches a brute-force log-sum-exp."""
+    r = rng(42)
+    q = r.standard_normal((1, 20, 4, 64))
+    k = r.standard_normal((1, 26, 2, 64))
+    lse = O.gqa_prefill_lse(q, k, 0.125, True, 6)
+    for h in range(4):
+        for i in range(20):
+            s = [0.125 * q[0, i, h] @ k[0, j, h // 2] for j in range(min(26, i + 7))]
+            assert abs(lse[0, h, i] - math.log(sum(math.exp(x) for x in s))) < 1e-9
+
+
+def test_backward_check_catches_planted_slip():
+    """Dropping the rowsum term of the softmax backward (a plausible slip)
+    moves dq far outside the tolerance the GPU is held to."""
+    r = rng(43)
+    q, k, v, do = (r.standard_normal(sh) for sh in ((1, 16, 2, 64), (1, 16, 1, 64), (1, 16, 1, 64), (1, 16, 2, 64)))
+    dq, _, _ = O.gqa_prefill_backward(q, k, v, do, 0.125)
+    vis = O._visible(16, 16, True, 0)
+    wrong = np.zeros_like(dq)
+    for h in range(2):
+        s = np.where(vis, 0.125 * q[0, :, h] @ k[0, :, 0].T, -np.inf)
+        p = np.exp(s - s.max(1, keepdims=True))
+        p /= p.sum(1, keepdims=True)
+        wrong[0, :, h] = 0.125 * (p * (do[0, :, h] @ v[0, :, 0].T)) @ k[0, :, 0]
+    assert relerr(wrong, dq) > 0.05
