@@ -85,6 +85,9 @@ def lib():
         "bn_unary_backward": ([i, V, V, V, vp], i), "bn_fill": ([V, C.c_double, vp], i),
         "bn_sum": ([V, V, i, vp], i), "bn_argmax": ([V, V, vp], i), "bn_copy": ([V, V, vp], i),
         "bn_gqa_prefill": ([i, vp, vp, vp, vp] + [i] * 6 + [i64] * 6 + [f, i, i, vp], i),
+        "bn_gqa_prefill_lse": ([i, vp, vp, vp, vp, vp] + [i] * 6 + [i64] * 6 + [f, i, i, vp], i),
+        "bn_gqa_prefill_backward_workspace_size": ([i, i, i], sz),
+        "bn_gqa_prefill_backward": ([i] + [vp] * 9 + [i] * 6 + [i64] * 6 + [f, i, i, vp, sz, vp], i),
         "bn_gqa_decode_workspace_size": ([i, i, i, i], sz),
         "bn_gqa_decode": ([i, vp, vp, vp, vp, vp] + [i] * 5 + [f, vp, sz, vp], i),
     }
@@ -168,6 +171,45 @@ def silu_mul(gate, up, out=None, stream=None):
     out = torch.empty_like(gate) if out is None else out
     call("bn_silu_mul", C.byref(view(gate)), C.byref(view(up)), C.byref(view(out)), stream_of(stream))
     return out
+
+
+def gqa_prefill_lse(q, k, v, o=None, lse=None, scale=None, causal=True, seq_offset=0, stream=None):
+    """gqa_prefill that also returns lse [B, H, Sq] fp32 (natural-log row
+    log-sum-exp of scale * q.k over the visible keys)."""
+    import torch
+    B, Sq, H, D = q.shape
+    _, Skv, Hkv, _ = k.shape
+    o = torch.empty_like(q) if o is None else o
+    lse = torch.empty((B, H, Sq), device=q.device, dtype=torch.float32) if lse is None else lse
+    sc = 1.0 / math.sqrt(D) if scale is None else scale
+    assert k.stride(1) == v.stride(1) and k.stride(0) == v.stride(0) and lse.is_contiguous()
+    call("bn_gqa_prefill_lse", _torch_dtype_code(q), q.data_ptr(), k.data_ptr(), v.data_ptr(),
+         o.data_ptr(), lse.data_ptr(), B, Sq, Skv, H, Hkv, D, q.stride(0), q.stride(1),
+         k.stride(0), k.stride(1), o.stride(0), o.stride(1), sc, int(causal), seq_offset,
+         stream_of(stream))
+    return o, lse
+
+
+def gqa_prefill_backward(q, k, v, o, dout, lse, scale=None, causal=True, seq_offset=0,
+                         dq=None, dk=None, dv=None, workspace=None, stream=None):
+    """(dq, dk, dv) of gqa_prefill (bf16): o and lse from gqa_prefill_lse,
+    dout the gradient of o.  dq shares q's strides, dk/dv share k's."""
+    import torch
+    B, Sq, H, D = q.shape
+    _, Skv, Hkv, _ = k.shape
+    dq = torch.empty_like(q) if dq is None else dq
+    dk = torch.empty_like(k) if dk is None else dk
+    dv = torch.empty_like(k) if dv is None else dv
+    sc = 1.0 / math.sqrt(D) if scale is None else scale
+    assert k.stride()[:2] == v.stride()[:2] == dk.stride()[:2] == dv.stride()[:2]
+    assert q.stride()[:2] == dq.stride()[:2] and o.stride()[:2] == dout.stride()[:2]
+    assert lse.is_contiguous() and lse.dtype == torch.float32
+    ws, wsb = (None, 0) if workspace is None else (workspace.data_ptr(), workspace.numel() * workspace.element_size())
+    call("bn_gqa_prefill_backward", _torch_dtype_code(q), q.data_ptr(), k.data_ptr(), v.data_ptr(),
+         o.data_ptr(), dout.data_ptr(), lse.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
+         B, Sq, Skv, H, Hkv, D, q.stride(0), q.stride(1), k.stride(0), k.stride(1), o.stride(0),
+         o.stride(1), sc, int(causal), seq_offset, ws, wsb, stream_of(stream))
+    return dq, dk, dv
 
 
 def gqa_decode(q, k_cache, v_cache, seq_lens, o=None, scale=None, workspace=None, stream=None):

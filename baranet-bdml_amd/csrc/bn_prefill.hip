@@ -49,7 +49,15 @@ struct PrefillParams {
   int batch, seq_q, seq_kv, n_heads, group, n_mt;
   int causal, seq_offset;
   float c;  // scale * log2(e): softmax evaluated as exp2(s*c - m*c)
+  float *lse;  // optional [batch, n_heads, seq_q]: natural-log row log-sum-exp of scale*s
 };
+
+// natural-log log-sum-exp of the row from its reference max (raw score
+// units) and the sum of exp2(s*c - m*c): log(sum exp(scale*s)) = (m*c +
+// log2(l)) * ln 2; -inf when no key is visible
+__device__ __forceinline__ float row_lse(float m, float l, float c) {
+  return l > 0.f ? (m * c + __log2f(l)) * 0.6931471805599453f : -INFINITY;
+}
 
 struct Work {
   int b, h, g, mt;
@@ -486,6 +494,8 @@ __global__ __launch_bounds__(256, OCC) void prefill_bf16_kernel(PrefillParams p)
     const int qrow = q_wave0 + 32 * rt + r32;
     const float lt = l[rt] + __shfl_xor(l[rt], 32, 64);
     const float inv = lt > 0.f ? 1.0f / lt : 0.f;  // no visible key -> zeros
+    if (p.lse && hf == 0 && qrow < p.seq_q)
+      p.lse[((int64_t)w.b * p.n_heads + w.h) * p.seq_q + qrow] = row_lse(m[rt], lt, c);
     if (qrow < p.seq_q) {
       bf16_t *orow = O + (int64_t)qrow * p.o_rs;
 #pragma unroll
@@ -615,6 +625,8 @@ __global__ __launch_bounds__(256, 2) void prefill_f32_kernel(PrefillParams p) {
 
   const float lt = l + __shfl_xor(l, 32, 64);
   const float inv = lt > 0.f ? 1.0f / lt : 0.f;
+  if (p.lse && hf == 0 && row_ok)
+    p.lse[((int64_t)w.b * p.n_heads + w.h) * p.seq_q + qrow] = row_lse(m, lt, p.c);
   if (row_ok) {
     float *orow = O + (int64_t)qrow * p.o_rs;
 #pragma unroll
@@ -635,12 +647,12 @@ bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 
 using namespace bn;
 
-extern "C" int bn_gqa_prefill(int dtype, const void *q, const void *k, const void *v, void *o,
-                              int batch, int seq_q, int seq_kv, int n_heads, int n_kv_heads,
-                              int head_dim, int64_t q_batch_stride, int64_t q_row_stride,
-                              int64_t kv_batch_stride, int64_t kv_row_stride,
-                              int64_t o_batch_stride, int64_t o_row_stride, float scale,
-                              int causal, int seq_offset, void *stream) {
+static int prefill_impl(int dtype, const void *q, const void *k, const void *v, void *o,
+                        int batch, int seq_q, int seq_kv, int n_heads, int n_kv_heads,
+                        int head_dim, int64_t q_batch_stride, int64_t q_row_stride,
+                        int64_t kv_batch_stride, int64_t kv_row_stride, int64_t o_batch_stride,
+                        int64_t o_row_stride, float scale, int causal, int seq_offset,
+                        float *lse, void *stream) {
   const char *op = "GQA prefill";
   if (dtype != BN_F32 && dtype != BN_BF16)
     return fail(BN_ERR_UNSUPPORTED, std::string(op) + ": dtype must be F32 or BF16");
@@ -696,6 +708,7 @@ extern "C" int bn_gqa_prefill(int dtype, const void *q, const void *k, const voi
   p.group = n_heads / n_kv_heads; p.n_mt = n_mt;
   p.causal = causal ? 1 : 0; p.seq_offset = seq_offset;
   p.c = scale * 1.4426950408889634f;
+  p.lse = lse;
   hipStream_t s = as_stream(stream);
   if (dtype == BN_BF16) {
     if (rt16 == 2)
@@ -706,4 +719,31 @@ extern "C" int bn_gqa_prefill(int dtype, const void *q, const void *k, const voi
     hipLaunchKernelGGL(prefill_f32_kernel, dim3((unsigned)n_wg), dim3(256), 0, s, p);
   BN_LAUNCH_CHECK();
   return BN_OK;
+}
+
+extern "C" int bn_gqa_prefill(int dtype, const void *q, const void *k, const void *v, void *o,
+                              int batch, int seq_q, int seq_kv, int n_heads, int n_kv_heads,
+                              int head_dim, int64_t q_batch_stride, int64_t q_row_stride,
+                              int64_t kv_batch_stride, int64_t kv_row_stride,
+                              int64_t o_batch_stride, int64_t o_row_stride, float scale,
+                              int causal, int seq_offset, void *stream) {
+  return prefill_impl(dtype, q, k, v, o, batch, seq_q, seq_kv, n_heads, n_kv_heads, head_dim,
+                      q_batch_stride, q_row_stride, kv_batch_stride, kv_row_stride,
+                      o_batch_stride, o_row_stride, scale, causal, seq_offset, nullptr, stream);
+}
+
+extern "C" int bn_gqa_prefill_lse(int dtype, const void *q, const void *k, const void *v, void *o,
+                                  float *lse, int batch, int seq_q, int seq_kv, int n_heads,
+                                  int n_kv_heads, int head_dim, int64_t q_batch_stride,
+                                  int64_t q_row_stride, int64_t kv_batch_stride,
+                                  int64_t kv_row_stride, int64_t o_batch_stride,
+                                  int64_t o_row_stride, float scale, int causal, int seq_offset,
+                                  void *stream) {
+  if (!lse && batch > 0 && seq_q > 0)
+    return fail(BN_ERR_INVALID_ARG, "GQA prefill: NULL log-sum-exp pointer");
+  if (reinterpret_cast<uintptr_t>(lse) & 3u)
+    return fail(BN_ERR_UNSUPPORTED, "GQA prefill: log-sum-exp pointer must be 4-byte aligned");
+  return prefill_impl(dtype, q, k, v, o, batch, seq_q, seq_kv, n_heads, n_kv_heads, head_dim,
+                      q_batch_stride, q_row_stride, kv_batch_stride, kv_row_stride,
+                      o_batch_stride, o_row_stride, scale, causal, seq_offset, lse, stream);
 }

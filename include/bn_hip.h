@@ -182,6 +182,47 @@ int bn_gqa_prefill(int dtype, const void *q, const void *k, const void *v,
                    int64_t kv_row_stride, int64_t o_batch_stride,
                    int64_t o_row_stride, float scale, int causal,
                    int seq_offset, void *stream);
+/* bn_gqa_prefill that also writes, per (batch, query head, row), the natural
+ * log of the row's softmax denominator, lse = log sum_{visible j}
+ * exp(scale * q_i . k_j) (-inf for a row with no visible key), into lse
+ * [batch, n_heads, seq_q] fp32 contiguous: the residual the backward needs.
+ * No reference counterpart as one call (the reference's autograd keeps the
+ * probability matrix instead). */
+int bn_gqa_prefill_lse(int dtype, const void *q, const void *k, const void *v,
+                       void *o, float *lse, int batch, int seq_q, int seq_kv,
+                       int n_heads, int n_kv_heads, int head_dim,
+                       int64_t q_batch_stride, int64_t q_row_stride,
+                       int64_t kv_batch_stride, int64_t kv_row_stride,
+                       int64_t o_batch_stride, int64_t o_row_stride, float scale,
+                       int causal, int seq_offset, void *stream);
+
+/* Backward of bn_gqa_prefill (bf16, head_dim 64), flash-style: with
+ * P = exp(scale * Q_h K_g^T - lse) over the visible keys (g = h / (n_heads /
+ * n_kv_heads)), dP = dO_h V_g^T and D = rowsum(dO_h * O_h),
+ *   dq_h = scale * (P * (dP - D)) K_g
+ *   dk_g = scale * sum over the heads h of group g of (P * (dP - D))^T Q_h
+ *   dv_g = sum over the heads h of group g of P^T dO_h
+ * q/dq share (q_batch_stride, q_row_stride), o/dout share the o strides,
+ * k/v/dk/dv share the kv strides ("bshd" layout as bn_gqa_prefill); lse is
+ * bn_gqa_prefill_lse's output [batch, n_heads, seq_q].  causal / seq_offset
+ * as in the forward.  dq, dk and dv are written, not accumulated.  It
+ * replaces the reference autograd chain through op_mm (op_mm.cuh),
+ * op_softmax_backward (op_softmax.cuh:182-246), the scale op and repeat_kv's
+ * gradient sum (llama_layers.hpp:156-167).  workspace (fp32 D,
+ * bn_gqa_prefill_backward_workspace_size bytes) may be NULL: the pool then
+ * supplies it. */
+size_t bn_gqa_prefill_backward_workspace_size(int batch, int seq_q, int n_heads);
+int bn_gqa_prefill_backward(int dtype, const void *q, const void *k,
+                            const void *v, const void *o, const void *dout,
+                            const float *lse, void *dq, void *dk, void *dv,
+                            int batch, int seq_q, int seq_kv, int n_heads,
+                            int n_kv_heads, int head_dim,
+                            int64_t q_batch_stride, int64_t q_row_stride,
+                            int64_t kv_batch_stride, int64_t kv_row_stride,
+                            int64_t o_batch_stride, int64_t o_row_stride,
+                            float scale, int causal, int seq_offset,
+                            void *workspace, size_t workspace_bytes,
+                            void *stream);
 
 /* KV-cache decode: one new query token per sequence.  The reference has no
  * KV cache (llama_model.py:135-141 recomputes the prefix); this is the last

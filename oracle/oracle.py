@@ -278,6 +278,45 @@ def gqa_prefill_backward(q, k, v, do, scale, causal=True, seq_offset=0):
     return dq.astype(np.float32), dk.astype(np.float32), dv.astype(np.float32)
 
 
+def gqa_prefill_backward_from_residuals(q, k, v, o, lse, do, scale, causal=True, seq_offset=0,
+                                        with_condition=False):
+    """The same gradients as gqa_prefill_backward, computed from the forward's
+    residuals (o and the natural-log row log-sum-exp lse [B,H,Sq]) as a
+    flash-style backward does: P = exp(scale*Q_h K_g^T - lse) on the visible
+    keys, and D = rowsum(dO_h * O_h) in place of rowsum(P * dP) -- equal
+    because O_h = P V_g.  No reference counterpart (the reference keeps P);
+    with exact o and lse it equals the chain form, which pins it.  fp64 on
+    the given o and lse (which may carry bf16 rounding); float32 results.
+    with_condition also returns the sums of absolute products behind each
+    output element (scale |dS| |K|, scale |dS|^T |Q|, P^T |dO|): the factor
+    that a rounding of the dot products' operands is multiplied by."""
+    q, k, v, o, do = (np.asarray(a, np.float64) for a in (q, k, v, o, do))
+    lse = np.asarray(lse, np.float64)
+    B, Sq, H, D = q.shape
+    _, Skv, Hkv, _ = k.shape
+    G = H // Hkv
+    vis = _visible(Sq, Skv, causal, seq_offset)
+    dq, dk, dv = np.zeros_like(q), np.zeros_like(k), np.zeros_like(v)
+    mq, mk, mv = np.zeros_like(q), np.zeros_like(k), np.zeros_like(v)
+    for b in range(B):
+        for h in range(H):
+            g = h // G
+            ok = vis & np.isfinite(lse[b, h])[:, None]
+            with np.errstate(invalid="ignore", over="ignore"):
+                p = np.where(ok, np.exp(scale * q[b, :, h] @ k[b, :, g].T - lse[b, h][:, None]), 0.0)
+            dp = do[b, :, h] @ v[b, :, g].T
+            ds = p * (dp - (do[b, :, h] * o[b, :, h]).sum(1, keepdims=True))
+            dq[b, :, h] = scale * ds @ k[b, :, g]
+            dk[b, :, g] += scale * ds.T @ q[b, :, h]
+            dv[b, :, g] += p.T @ do[b, :, h]
+            if with_condition:
+                mq[b, :, h] = scale * np.abs(ds) @ np.abs(k[b, :, g])
+                mk[b, :, g] += scale * np.abs(ds).T @ np.abs(q[b, :, h])
+                mv[b, :, g] += p.T @ np.abs(do[b, :, h])
+    grads = dq.astype(np.float32), dk.astype(np.float32), dv.astype(np.float32)
+    return (grads, (mq, mk, mv)) if with_condition else grads
+
+
 def gqa_layer(x, wq, wk, wv, wo, n_heads, n_kv_heads, theta=10000.0,
               position_offset=0, per_head=False):
     x = _f32(x)

@@ -32,8 +32,9 @@ def relerr(a, b) -> float:
     return float(np.max(np.abs(a - b)) / max(float(np.max(np.abs(b))), 1e-30))
 
 
-def assert_close(got, ref, tol, what=""):
-    """max|a-b|/max|b| <= tol and, element-wise, |a-b| <= tol*max(|b|, rms(b))."""
+def assert_close(got, ref, tol, what="", floor=None):
+    """max|a-b|/max|b| <= tol and, element-wise, |a-b| <= tol*max(|b|, rms(b)),
+    or <= floor where an element-wise error model (an array like ref) allows more."""
     got = np.asarray(got, np.float64)
     ref = np.asarray(ref, np.float64)
     assert got.shape == ref.shape, (got.shape, ref.shape)
@@ -42,6 +43,8 @@ def assert_close(got, ref, tol, what=""):
     assert r <= tol, f"{what}: max relative error {r:.3e} > {tol:.0e}"
     rms = float(np.sqrt(np.mean(ref ** 2))) if ref.size else 0.0
     bound = tol * np.maximum(np.abs(ref), rms)
+    if floor is not None:
+        bound = np.maximum(bound, floor)
     bad = np.abs(got - ref) > bound
     assert not bad.any(), f"{what}: {int(bad.sum())} elements outside the element-wise bound"
     return r

@@ -145,3 +145,51 @@ def test_pool_bookkeeping_without_device():
     assert st("bn_free", None, None)[0] == B.BN_OK
     assert st("bn_memcpy", None, C.c_void_p(8), 8, 0, None)[0] == B.BN_ERR_INVALID_ARG
     assert st("bn_memcpy", C.c_void_p(8), C.c_void_p(8), 8, 7, None)[0] == B.BN_ERR_INVALID_ARG
+
+
+def backward_args(**kw):
+    a = dict(dtype=B.BN_BF16, q=0x1000, k=0x2000, v=0x3000, o=0x4000, do=0x5000, lse=0x6000,
+             dq=0x7000, dk=0x8000, dv=0x9000, batch=4, seq_q=2048, seq_kv=2048, H=32, Hkv=4,
+             D=64, qbs=2048 * 2048, qrs=2048, kvbs=2048 * 256, kvrs=256, obs=2048 * 2048,
+             ors=2048, scale=0.125, causal=1, off=0, ws=None, wsb=0)
+    a.update(kw)
+    return tuple(a[n] for n in ("dtype", "q", "k", "v", "o", "do", "lse", "dq", "dk", "dv",
+                                "batch", "seq_q", "seq_kv", "H", "Hkv", "D", "qbs", "qrs",
+                                "kvbs", "kvrs", "obs", "ors", "scale", "causal", "off", "ws",
+                                "wsb")) + (None,)
+
+
+@pytest.mark.parametrize("kw,status", [
+    (dict(dtype=B.BN_F32), B.BN_ERR_UNSUPPORTED),
+    (dict(H=30), B.BN_ERR_SHAPE),
+    (dict(D=128), B.BN_ERR_UNSUPPORTED),
+    (dict(seq_kv=-1), B.BN_ERR_SHAPE),
+    (dict(ors=1024), B.BN_ERR_SHAPE),
+    (dict(kvbs=100), B.BN_ERR_SHAPE),
+    (dict(dk=0x8008), B.BN_ERR_UNSUPPORTED),
+    (dict(lse=0x6002), B.BN_ERR_UNSUPPORTED),
+    (dict(lse=0), B.BN_ERR_INVALID_ARG),
+    (dict(do=0), B.BN_ERR_INVALID_ARG),
+    (dict(scale=0.0), B.BN_ERR_INVALID_ARG),
+    (dict(ws=0xA000, wsb=4 * 32 * 2048 * 4 - 4), B.BN_ERR_INVALID_ARG),  # workspace too small
+])
+def test_prefill_backward_validation(kw, status):
+    s, m = st("bn_gqa_prefill_backward", *backward_args(**kw))
+    assert s == status, m
+    assert m.startswith("GQA prefill backward:")
+
+
+def test_prefill_backward_workspace_size_and_empty():
+    L = B.lib()
+    assert L.bn_gqa_prefill_backward_workspace_size(4, 2048, 32) == 4 * 32 * 2048 * 4
+    assert L.bn_gqa_prefill_backward_workspace_size(0, 2048, 32) == 0
+    assert st("bn_gqa_prefill_backward", *backward_args(batch=0))[0] == B.BN_OK
+    assert st("bn_gqa_prefill_backward", *backward_args(seq_q=0, seq_kv=0))[0] == B.BN_OK
+
+
+def test_prefill_lse_validation():
+    args = list(prefill_args())
+    s, m = st("bn_gqa_prefill_lse", *args[:5], None, *args[5:])
+    assert s == B.BN_ERR_INVALID_ARG and m.startswith("GQA prefill:")
+    s, m = st("bn_gqa_prefill_lse", *args[:5], 0x6002, *args[5:])
+    assert s == B.BN_ERR_UNSUPPORTED

@@ -15,7 +15,7 @@ import torch
 
 import bnhip as B
 from oracle import oracle as O
-from gpu_util import BF16_TOL, FP32_TOL, assert_close, bf16_round, dev, host, require_gpu
+from gpu_util import BF16_TOL, FP32_TOL, assert_close, bf16_round, dev, host, relerr, require_gpu
 
 pytestmark = pytest.mark.gpu
 TD = {"f32": torch.float32, "bf16": torch.bfloat16}
@@ -271,3 +271,161 @@ def test_decode_baseline_shape(ragged):
         last = B.gqa_prefill(qd[b:b + 1, None], kd[b:b + 1, :Lb], vd[b:b + 1, :Lb],
                              scale=0.125, causal=True, seq_offset=Lb - 1)
         assert_close(got[b], host(last)[0, 0], BF16_TOL, f"decode vs prefill b={b}")
+
+
+# ---------------------------------------------------------------- forward lse
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("case", PREFILL_CASES)
+def test_prefill_lse_vs_oracle(case, dtype):
+    # lse is compared in absolute terms: an absolute lse error is the relative
+    # error of the row's softmax denominator, bounded by the dtype tolerance
+    Bn, Sq, Skv, H, Hkv, causal, off = case
+    q = draw((Bn, Sq, H, 64), 1, dtype)
+    k = draw((Bn, Skv, Hkv, 64), 2, dtype)
+    v = draw((Bn, Skv, Hkv, 64), 3, dtype)
+    o, lse = B.gqa_prefill_lse(dev(q, TD[dtype]), dev(k, TD[dtype]), dev(v, TD[dtype]),
+                               scale=0.125, causal=bool(causal), seq_offset=off)
+    assert_close(host(o), O.gqa_prefill(q, k, v, 0.125, bool(causal), off), TOL[dtype],
+                 f"prefill_lse o {case} {dtype}")
+    ref = O.gqa_prefill_lse(q, k, 0.125, bool(causal), off)
+    got = host(lse)
+    fin = np.isfinite(ref)
+    assert np.array_equal(np.isfinite(got), fin), "rows with / without visible keys differ"
+    assert np.all(got[~fin] == -np.inf)
+    if fin.any():
+        err = float(np.max(np.abs(got[fin] - ref[fin])))
+        assert err <= TOL[dtype], f"lse {case} {dtype}: max abs error {err:.3e}"
+
+
+# ------------------------------------------------------------------- backward
+BWD_CASES = PREFILL_CASES + [
+    (1, 300, 40, 4, 2, 1, 0),       # causal, fewer keys than query rows
+    (1, 96, 500, 8, 4, 0, 0),       # non-causal, many key blocks per query block
+]
+
+
+def bwd_inputs(case, seed=10):
+    Bn, Sq, Skv, H, Hkv, _, _ = case
+    return (draw((Bn, Sq, H, 64), seed, "bf16"), draw((Bn, Skv, Hkv, 64), seed + 1, "bf16"),
+            draw((Bn, Skv, Hkv, 64), seed + 2, "bf16"), draw((Bn, Sq, H, 64), seed + 3, "bf16"))
+
+
+def nan_like(t):
+    return torch.full_like(t, float("nan"))
+
+
+BF16_U = 2.0 ** -8   # bf16 unit roundoff
+
+
+def check_backward(got, q, k, v, do, o, lse, causal, off, what):
+    """got = (dq, dk, dv) on the host.  Against the exact chain form: the
+    north-star bound, max relative error <= 2e-2.  Element-wise (assert_close)
+    against the residual form evaluated in fp64 on the forward's own bf16 o
+    and fp32 lse, since the backward inherits the rounding of those residuals
+    (D = rowsum(dO*O) from a bf16 O moves a row's dq coherently), which the
+    exact chain form does not carry.  The element-wise bound is the larger of
+    2e-2 * max(|ref|, rms(ref)) and the bf16 error model of the products
+    dq = dS K, dk = dS^T Q, dv = P^T dO: dS and P enter the MFMA rounded to
+    bf16 (u = 2^-8) and the result is rounded to bf16 (u), so |error| <=
+    2u * sum|a||b|; 2.5u leaves room for the fp32 accumulation and the
+    recomputed exponential.  Without it, rows with one or two visible keys
+    (large dS of opposite signs whose products with K cancel) exceed 2% of
+    the rms in a few elements."""
+    chain = O.gqa_prefill_backward(q, k, v, do, 0.125, bool(causal), off)
+    res, cond = O.gqa_prefill_backward_from_residuals(q, k, v, o, lse, do, 0.125, bool(causal),
+                                                      off, with_condition=True)
+    for name, g, c, r, m in zip(("dq", "dk", "dv"), got, chain, res, cond):
+        e = relerr(g, c)
+        assert e <= BF16_TOL, f"{name} {what}: max relative error {e:.3e} vs the chain form"
+        assert_close(g, r, BF16_TOL, f"{name} {what} vs the residual form", floor=2.5 * BF16_U * m)
+
+
+@pytest.mark.parametrize("case", BWD_CASES)
+def test_prefill_backward_vs_oracle(case):
+    Bn, Sq, Skv, H, Hkv, causal, off = case
+    q, k, v, do = bwd_inputs(case)
+    qd, kd, vd, dod = (dev(a, torch.bfloat16) for a in (q, k, v, do))
+    o, lse = B.gqa_prefill_lse(qd, kd, vd, scale=0.125, causal=bool(causal), seq_offset=off)
+    # outputs start as NaN: every element is written, nothing accumulates
+    dq, dk, dv = B.gqa_prefill_backward(qd, kd, vd, o, dod, lse, scale=0.125,
+                                        causal=bool(causal), seq_offset=off, dq=nan_like(qd),
+                                        dk=nan_like(kd), dv=nan_like(vd))
+    gq, gk, gv = host(dq), host(dk), host(dv)
+    check_backward((gq, gk, gv), q, k, v, do, host(o), host(lse), causal, off, str(case))
+    if causal:
+        # query rows that see no key and keys that no query row sees: exactly 0
+        vis = np.arange(Skv)[None, :] <= np.arange(Sq)[:, None] + off
+        assert np.all(gq[:, ~vis.any(1)] == 0.0)
+        assert np.all(gk[:, ~vis.any(0)] == 0.0) and np.all(gv[:, ~vis.any(0)] == 0.0)
+
+
+def test_prefill_backward_strided_rows():
+    # q/k/v as column slices of a fused QKV row, the gradients as slices of a
+    # fused dQKV row with the same strides
+    Bn, S, H, Hkv = 2, 160, 8, 2
+    W = (H + 2 * Hkv) * 64
+    qkv = draw((Bn, S, W), 21, "bf16")
+    do = draw((Bn, S, H, 64), 22, "bf16")
+    t = dev(qkv, torch.bfloat16)
+    g = torch.full_like(t, float("nan"))
+
+    def split(x):
+        return (x[:, :, :H * 64].unflatten(2, (H, 64)),
+                x[:, :, H * 64:(H + Hkv) * 64].unflatten(2, (Hkv, 64)),
+                x[:, :, (H + Hkv) * 64:].unflatten(2, (Hkv, 64)))
+
+    q, k, v = split(t)
+    dq, dk, dv = split(g)
+    o, lse = B.gqa_prefill_lse(q, k, v, scale=0.125)
+    B.gqa_prefill_backward(q, k, v, o, dev(do, torch.bfloat16), lse, scale=0.125, dq=dq, dk=dk,
+                           dv=dv)
+    qn = qkv[:, :, :H * 64].reshape(Bn, S, H, 64)
+    kn = qkv[:, :, H * 64:(H + Hkv) * 64].reshape(Bn, S, Hkv, 64)
+    vn = qkv[:, :, (H + Hkv) * 64:].reshape(Bn, S, Hkv, 64)
+    check_backward((host(dq), host(dk), host(dv)), qn, kn, vn, do, host(o), host(lse), 1, 0,
+                   "strided")
+
+
+def test_prefill_backward_workspace_and_repeat():
+    # a caller workspace gives the same bits as the pool, and a second call
+    # over the same buffers reproduces the first
+    case = (2, 200, 200, 8, 2, 1, 0)
+    q, k, v, do = (dev(a, torch.bfloat16) for a in bwd_inputs(case, 30))
+    o, lse = B.gqa_prefill_lse(q, k, v, scale=0.125)
+    a = B.gqa_prefill_backward(q, k, v, o, do, lse, scale=0.125)
+    ws = torch.empty(B.lib().bn_gqa_prefill_backward_workspace_size(2, 200, 8) // 4,
+                     dtype=torch.float32, device="cuda")
+    b = B.gqa_prefill_backward(q, k, v, o, do, lse, scale=0.125, workspace=ws)
+    c = B.gqa_prefill_backward(q, k, v, o, do, lse, scale=0.125, workspace=ws)
+    for x, y, z in zip(a, b, c):
+        assert torch.equal(x, y) and torch.equal(y, z)
+
+
+def test_prefill_backward_baseline_shape():
+    # config-2 shape (B=4, S=2048, 32 heads over 4 KV heads): two (batch, KV
+    # head) groups against the oracle, and every group on two properties that
+    # hold at any size: each probability row sums to 1, so sum_key dv equals
+    # sum over the group's heads and rows of dout; each dS row sums to 0, so
+    # sum_key dk vanishes
+    Bn, S, H, Hkv = 4, 2048, 32, 4
+    G = H // Hkv
+    rng = np.random.default_rng(40)
+    q, k, v, do = (bf16_round(rng.standard_normal(s).astype(np.float32))
+                   for s in ((Bn, S, H, 64), (Bn, S, Hkv, 64), (Bn, S, Hkv, 64), (Bn, S, H, 64)))
+    qd, kd, vd, dod = (dev(a, torch.bfloat16) for a in (q, k, v, do))
+    o, lse = B.gqa_prefill_lse(qd, kd, vd, scale=0.125)
+    dq, dk, dv = B.gqa_prefill_backward(qd, kd, vd, o, dod, lse, scale=0.125)
+    gq, gk, gv = host(dq), host(dk), host(dv)
+    on, ln = host(o), host(lse)
+    assert np.all(np.isfinite(gq)) and np.all(np.isfinite(gk)) and np.all(np.isfinite(gv))
+    for b, g in ((3, 1), (0, 3)):
+        hs, gs, bs = slice(g * G, (g + 1) * G), slice(g, g + 1), slice(b, b + 1)
+        check_backward((gq[bs, :, hs], gk[bs, :, gs], gv[bs, :, gs]), q[bs, :, hs], k[bs, :, gs],
+                       v[bs, :, gs], do[bs, :, hs], on[bs, :, hs], ln[bs, hs], 1, 0, f"b{b} g{g}")
+    for b in range(Bn):
+        for g in range(Hkv):
+            want = do[b, :, g * G:(g + 1) * G].astype(np.float64).sum((0, 1))
+            got = gv[b, :, g].astype(np.float64).sum(0)
+            assert np.max(np.abs(got - want)) <= BF16_TOL * np.max(np.abs(want)), (b, g)
+            zs = np.abs(gk[b, :, g].astype(np.float64).sum(0))
+            assert np.all(zs <= BF16_TOL * np.abs(gk[b, :, g]).sum(0)), (b, g)

@@ -465,3 +465,31 @@ def test_backward_check_catches_planted_slip():
         p /= p.sum(1, keepdims=True)
         wrong[0, :, h] = 0.125 * (p * (do[0, :, h] @ v[0, :, 0].T)) @ k[0, :, 0]
     assert relerr(wrong, dq) > 0.05
+
+
+@pytest.mark.parametrize("B,Sq,Skv,H,Hkv,causal,off", [(1, 40, 40, 8, 2, True, 0), (2, 17, 30, 4, 4, True, 13),
+                                                       (1, 24, 24, 8, 1, False, 0), (1, 9, 12, 2, 1, True, -3)])
+def test_backward_from_residuals_equals_chain_form(B, Sq, Skv, H, Hkv, causal, off):
+    """Given the exact forward output and lse, the residual form (P from lse,
+    D = rowsum(dO*O)) reproduces the chain form; a natural-vs-base-2 lse slip
+    does not."""
+    r = rng(44)
+    q, k, v, do = (r.standard_normal(sh) for sh in ((B, Sq, H, 64), (B, Skv, Hkv, 64),
+                                                     (B, Skv, Hkv, 64), (B, Sq, H, 64)))
+    G = H // Hkv
+    vis = O._visible(Sq, Skv, causal, off)
+    o = np.zeros_like(q)
+    for b in range(B):
+        for h in range(H):
+            s = np.where(vis, 0.125 * q[b, :, h] @ k[b, :, h // G].T, -np.inf)
+            m = s.max(1, keepdims=True)
+            e = np.where(vis, np.exp(s - np.where(np.isfinite(m), m, 0.0)), 0.0)
+            t = e.sum(1, keepdims=True)
+            o[b, :, h] = np.divide(e, t, out=np.zeros_like(e), where=t > 0) @ v[b, :, h // G]
+    lse = O.gqa_prefill_lse(q, k, 0.125, causal, off)
+    chain = O.gqa_prefill_backward(q, k, v, do, 0.125, causal, off)
+    res = O.gqa_prefill_backward_from_residuals(q, k, v, o, lse, do, 0.125, causal, off)
+    for a, b_ in zip(res, chain):
+        assert relerr(a, b_) < 1e-6
+    wrong = O.gqa_prefill_backward_from_residuals(q, k, v, o, lse / math.log(2), do, 0.125, causal, off)
+    assert relerr(wrong[0], chain[0]) > 0.05
