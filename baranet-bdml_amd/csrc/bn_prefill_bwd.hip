@@ -41,10 +41,12 @@ struct BwdParams {
   const bf16_t *q, *k, *v, *o, *dout;
   const float *lse;  // [batch, n_heads, seq_q], natural log
   float *dvec;       // [batch, n_heads, seq_q]: D = rowsum(dO * O)
+  float *part;       // fp32 dK/dV partial sums per head chunk, or null
   bf16_t *dq, *dk, *dv;
   int64_t q_bs, q_rs, kv_bs, kv_rs, o_bs, o_rs;
   int batch, seq_q, seq_kv, n_heads, group, causal, seq_offset;
-  float c, scale;  // c = scale * log2(e)
+  int n_kv, hpw, nchunk;  // KV heads; query heads per dK/dV workgroup; group / hpw
+  float c, scale;         // c = scale * log2(e)
 };
 
 __device__ __forceinline__ bf16x4_t tr16(const bf16_t *lds) {
@@ -200,19 +202,29 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dq_kernel(BwdParams p) {
 }
 
 // ----------------------------------------------------------------- dK, dV
+constexpr int TPI = 2;  // 32-row query tiles staged per barrier
+
+// One workgroup per (key block of 128, batch, KV head, head chunk): the
+// chunk's hpw query heads are walked in turn.  With one chunk (hpw = group)
+// dK/dV are final and stored as bf16; otherwise each chunk writes its fp32
+// partial sums to part [batch][n_kv][nchunk][2][seq_kv][64] and
+// prefill_bwd_reduce_kernel adds them up.
 __global__ __launch_bounds__(256, 2) void prefill_bwd_dkv_kernel(BwdParams p) {
-  __shared__ __attribute__((aligned(16))) bf16_t Qs[2][32 * P16];
-  __shared__ __attribute__((aligned(16))) bf16_t Ds[2][32 * P16];
-  __shared__ __attribute__((aligned(16))) float lse_s[2][32];
-  __shared__ __attribute__((aligned(16))) float dv_s[2][32];
+  __shared__ __attribute__((aligned(16))) bf16_t Qs[2][TPI][32 * P16];
+  __shared__ __attribute__((aligned(16))) bf16_t Ds[2][TPI][32 * P16];
+  __shared__ __attribute__((aligned(16))) float lse_s[2][TPI][32];
+  __shared__ __attribute__((aligned(16))) float dv_s[2][TPI][32];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r32 = lane & 31, hf = lane >> 5;
-  const int n_kt = (p.seq_kv + 127) / 128;
-  const int n_kv = p.n_heads / p.group;
-  const int kt_blk = (int)(blockIdx.x % n_kt);
-  const int bg = (int)(blockIdx.x / n_kt);
-  const int b = bg / n_kv, g = bg % n_kv;
+  // key block outermost: low block ids (the most query rows under a causal
+  // mask) are dispatched first, and the workgroups of one (batch, KV head,
+  // chunk) share an XCD when batch*n_kv*nchunk is a multiple of 8
+  const int per_blk = p.batch * p.n_kv * p.nchunk;
+  const int kt_blk = (int)(blockIdx.x / per_blk);
+  const int rest = (int)(blockIdx.x % per_blk);
+  const int c = rest % p.nchunk, bg = rest / p.nchunk;
+  const int b = bg / p.n_kv, g = bg % p.n_kv;
   const int k0 = kt_blk * 128 + wave * 32, key = k0 + r32;
   const bool key_ok = key < p.seq_kv;
   const int kr_ = min(key, p.seq_kv - 1);
@@ -227,94 +239,165 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dkv_kernel(BwdParams p) {
     vreg[t] = key_ok ? *(const bf16x8_t *)(Vr + 16 * t) : bf16x8_t{};
   }
 
-  // query rows that see any key of the workgroup's block: q + off >= first key
-  const int wg_k0 = kt_blk * 128;
-  int q_first = p.causal ? wg_k0 - p.seq_offset : 0;
+  // query rows that see any key of the block: q + off >= first key
+  int q_first = p.causal ? kt_blk * 128 - p.seq_offset : 0;
   q_first = q_first < 0 ? 0 : q_first;
   const int qt0 = q_first / 32, nqt = (p.seq_q + 31) / 32;
   const int per_head = nqt > qt0 ? nqt - qt0 : 0;
-  const int ntile = per_head * p.group;
+  const int ntile = per_head * p.hpw;
+  const int h_first = p.group * g + c * p.hpw;
 
-  // staging: one 16-byte chunk of Q and of dO per thread per 32-row tile
+  // staging: per tile, one 16-byte chunk of Q and of dO per thread
   const int crow = tid >> 3, ccol = (tid & 7) * 8;
-  u32x4_t qv, dvv;
-  float lse_r = 0.f, dv_r = 0.f;
-  auto gload = [&](int n) __attribute__((always_inline)) {
-    const int hh = p.group * g + n / per_head, qt = qt0 + n % per_head;
-    const int qrow = qt * 32 + crow;
-    if (qrow < p.seq_q) {
-      qv = *(const u32x4_t *)(p.q + b * p.q_bs + (int64_t)qrow * p.q_rs + (int64_t)hh * HD + ccol);
-      dvv = *(const u32x4_t *)(p.dout + b * p.o_bs + (int64_t)qrow * p.o_rs + (int64_t)hh * HD + ccol);
-    } else {
-      qv = u32x4_t{0u, 0u, 0u, 0u};
-      dvv = u32x4_t{0u, 0u, 0u, 0u};
-    }
-    if (tid < 32) {
-      const int qq = qt * 32 + tid;
-      const bool ok = qq < p.seq_q;
-      const int64_t rix = ((int64_t)b * p.n_heads + hh) * p.seq_q + (ok ? qq : 0);
-      lse_r = lse2_of(ok ? p.lse[rix] : 0.f, ok);
-      dv_r = ok ? p.dvec[rix] : 0.f;
+  u32x4_t qv[TPI], dvv[TPI];
+  float lse_r[TPI], dv_r[TPI];
+  auto gload = [&](int it) __attribute__((always_inline)) {
+#pragma unroll
+    for (int t = 0; t < TPI; ++t) {
+      const int n = it * TPI + t;
+      const bool tile_ok = n < ntile;
+      const int hh = h_first + (tile_ok ? n / per_head : 0);
+      const int qt = qt0 + (tile_ok ? n % per_head : 0);
+      const int qrow = qt * 32 + crow;
+      if (tile_ok && qrow < p.seq_q) {
+        qv[t] = *(const u32x4_t *)(p.q + b * p.q_bs + (int64_t)qrow * p.q_rs + (int64_t)hh * HD + ccol);
+        dvv[t] = *(const u32x4_t *)(p.dout + b * p.o_bs + (int64_t)qrow * p.o_rs + (int64_t)hh * HD + ccol);
+      } else {
+        qv[t] = u32x4_t{0u, 0u, 0u, 0u};
+        dvv[t] = u32x4_t{0u, 0u, 0u, 0u};
+      }
+      if (tid < 32) {
+        const int qq = qt * 32 + tid;
+        const bool ok = tile_ok && qq < p.seq_q;
+        const int64_t rix = ((int64_t)b * p.n_heads + hh) * p.seq_q + (ok ? qq : 0);
+        lse_r[t] = lse2_of(ok ? p.lse[rix] : 0.f, ok);
+        dv_r[t] = ok ? p.dvec[rix] : 0.f;
+      }
     }
   };
   const int tr_off = (4 * hf + ((lane & 15) >> 2)) * P16 + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
   f32x16_t dk[2] = {f32x16_t{}, f32x16_t{}}, dv[2] = {f32x16_t{}, f32x16_t{}};
 
-  if (ntile > 0) gload(0);
-  for (int n = 0; n < ntile; ++n) {
-    const int buf = n & 1;
-    *(u32x4_t *)(Qs[buf] + crow * P16 + ccol) = qv;
-    *(u32x4_t *)(Ds[buf] + crow * P16 + ccol) = dvv;
-    if (tid < 32) {
-      lse_s[buf][tid] = lse_r;
-      dv_s[buf][tid] = dv_r;
-    }
-    __syncthreads();  // also: every wave finished tile n-2, the last user of buf
-    if (n + 1 < ntile) gload(n + 1);
-    const int qt = qt0 + n % per_head;
-    const int qb = qt * 32;
-    // wave-uniform skip: no query of the tile sees this wave's first key
-    if (p.causal && (long)qb + 31 + p.seq_offset < (long)k0) continue;
-    const bf16_t *qs = Qs[buf], *ds = Ds[buf];
-    f32x16_t s = f32x16_t{}, dp = f32x16_t{};
+  const int niter = (ntile + TPI - 1) / TPI;
+  if (niter > 0) gload(0);
+  for (int it = 0; it < niter; ++it) {
+    const int buf = it & 1;
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const bf16x8_t qa = *(const bf16x8_t *)(qs + r32 * P16 + 16 * t + 8 * hf);
-      const bf16x8_t da = *(const bf16x8_t *)(ds + r32 * P16 + 16 * t + 8 * hf);
-      s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(qa, kreg[t], s, 0, 0, 0);
-      dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(da, vreg[t], dp, 0, 0, 0);
-    }
-    // s[i] = S[query qb + 8(i/4) + 4hf + i%4][key]
-    bf16x8_t pb[2], sb[2];
-#pragma unroll
-    for (int gi = 0; gi < 4; ++gi) {
-      const float4 l4 = *(const float4 *)(&lse_s[buf][8 * gi + 4 * hf]);
-      const float4 d4 = *(const float4 *)(&dv_s[buf][8 * gi + 4 * hf]);
-      const float lv[4] = {l4.x, l4.y, l4.z, l4.w}, dvl[4] = {d4.x, d4.y, d4.z, d4.w};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int i = 4 * gi + e;
-        const int qrow = qb + 8 * gi + 4 * hf + e;
-        float pr = __builtin_amdgcn_exp2f(fmaf(s[i], p.c, -lv[e]));
-        if (!key_ok || (p.causal && (long)key > (long)qrow + p.seq_offset)) pr = 0.f;
-        pb[i >> 3][i & 7] = (__bf16)pr;
-        sb[i >> 3][i & 7] = (__bf16)(pr * (dp[i] - dvl[e]));
+    for (int t = 0; t < TPI; ++t) {
+      *(u32x4_t *)(Qs[buf][t] + crow * P16 + ccol) = qv[t];
+      *(u32x4_t *)(Ds[buf][t] + crow * P16 + ccol) = dvv[t];
+      if (tid < 32) {
+        lse_s[buf][t][tid] = lse_r[t];
+        dv_s[buf][t][tid] = dv_r[t];
       }
     }
+    __syncthreads();  // also: every wave finished iteration it-2, the last user of buf
+    if (it + 1 < niter) gload(it + 1);
 #pragma unroll
-    for (int u = 0; u < 2; ++u)
+    for (int t = 0; t < TPI; ++t) {
+      const int n = it * TPI + t;
+      if (n >= ntile) break;
+      const int qb = (qt0 + n % per_head) * 32;
+      // wave-uniform skip: no query of the tile sees this wave's first key
+      if (p.causal && (long)qb + 31 + p.seq_offset < (long)k0) continue;
+      const bf16_t *qs = Qs[buf][t], *ds = Ds[buf][t];
+      f32x16_t s = f32x16_t{}, dp = f32x16_t{};
 #pragma unroll
-      for (int dt = 0; dt < 2; ++dt) {
-        dv[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tfrag(ds, u, dt, tr_off), pb[u], dv[dt], 0, 0, 0);
-        dk[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tfrag(qs, u, dt, tr_off), sb[u], dk[dt], 0, 0, 0);
+      for (int u = 0; u < 4; ++u) {
+        const bf16x8_t qa = *(const bf16x8_t *)(qs + r32 * P16 + 16 * u + 8 * hf);
+        const bf16x8_t da = *(const bf16x8_t *)(ds + r32 * P16 + 16 * u + 8 * hf);
+        s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(qa, kreg[u], s, 0, 0, 0);
+        dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(da, vreg[u], dp, 0, 0, 0);
       }
+      // s[i] = S[query qb + 8(i/4) + 4hf + i%4][key]
+      bf16x8_t pb[2], sb[2];
+#pragma unroll
+      for (int gi = 0; gi < 4; ++gi) {
+        const float4 l4 = *(const float4 *)(&lse_s[buf][t][8 * gi + 4 * hf]);
+        const float4 d4 = *(const float4 *)(&dv_s[buf][t][8 * gi + 4 * hf]);
+        const float lv[4] = {l4.x, l4.y, l4.z, l4.w}, dvl[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int i = 4 * gi + e;
+          const int qrow = qb + 8 * gi + 4 * hf + e;
+          float pr = __builtin_amdgcn_exp2f(fmaf(s[i], p.c, -lv[e]));
+          if (!key_ok || (p.causal && (long)key > (long)qrow + p.seq_offset)) pr = 0.f;
+          pb[i >> 3][i & 7] = (__bf16)pr;
+          sb[i >> 3][i & 7] = (__bf16)(pr * (dp[i] - dvl[e]));
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int dt = 0; dt < 2; ++dt) {
+          dv[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tfrag(ds, u, dt, tr_off), pb[u], dv[dt], 0, 0, 0);
+          dk[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tfrag(qs, u, dt, tr_off), sb[u], dk[dt], 0, 0, 0);
+        }
+    }
   }
-  if (key_ok) {
+  if (!key_ok) return;
+  if (p.part) {
+    float *pk = p.part + ((((int64_t)b * p.n_kv + g) * p.nchunk + c) * 2 * p.seq_kv + key) * HD;
+    float *pv = pk + (int64_t)p.seq_kv * HD;
+#pragma unroll
+    for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+      for (int gi = 0; gi < 4; ++gi) {
+        const int d0 = dt * 32 + gi * 8 + hf * 4;
+        *(float4 *)(pk + d0) = make_float4(dk[dt][4 * gi], dk[dt][4 * gi + 1], dk[dt][4 * gi + 2], dk[dt][4 * gi + 3]);
+        *(float4 *)(pv + d0) = make_float4(dv[dt][4 * gi], dv[dt][4 * gi + 1], dv[dt][4 * gi + 2], dv[dt][4 * gi + 3]);
+      }
+  } else {
     const int64_t off = b * p.kv_bs + (int64_t)key * p.kv_rs + (int64_t)g * HD;
     store_rowT(p.dk + off, dk, hf, p.scale);
     store_rowT(p.dv + off, dv, hf, 1.f);
   }
 }
+
+// dK/dV from the chunks' fp32 partial sums: one thread per 8 consecutive d of
+// one (batch, KV head, K-or-V, key) row; reads are contiguous along d and keys
+__global__ __launch_bounds__(256) void prefill_bwd_reduce_kernel(BwdParams p, int64_t total) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= total) return;
+  const int dc = (int)(i & 7);
+  int64_t r = i >> 3;
+  const int key = (int)(r % p.seq_kv);
+  r /= p.seq_kv;
+  const int which = (int)(r & 1);
+  r >>= 1;
+  const int g = (int)(r % p.n_kv), b = (int)(r / p.n_kv);
+  const int64_t cstride = (int64_t)2 * p.seq_kv * HD;
+  const float *src = p.part + ((((int64_t)b * p.n_kv + g) * p.nchunk * 2 + which) * p.seq_kv + key) * HD + 8 * dc;
+  float a[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int c = 0; c < p.nchunk; ++c) {
+    const float4 x = *(const float4 *)(src + c * cstride);
+    const float4 y = *(const float4 *)(src + c * cstride + 4);
+    a[0] += x.x; a[1] += x.y; a[2] += x.z; a[3] += x.w;
+    a[4] += y.x; a[5] += y.y; a[6] += y.z; a[7] += y.w;
+  }
+  const float sc = which ? 1.f : p.scale;
+  uint32_t w[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    w[j] = (uint32_t)f32_to_bf16(a[2 * j] * sc) | ((uint32_t)f32_to_bf16(a[2 * j + 1] * sc) << 16);
+  bf16_t *dst = (which ? p.dv : p.dk) + b * p.kv_bs + (int64_t)key * p.kv_rs + (int64_t)g * HD + 8 * dc;
+  *(uint4 *)dst = make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+// query heads per dK/dV workgroup: the largest divisor of the group size that
+// still gives at least BN_BWD_MIN_WG workgroups (the whole group when G = 1)
+#ifndef BN_BWD_MIN_WG
+#define BN_BWD_MIN_WG 2048
+#endif
+int heads_per_wg(int batch, int seq_kv, int n_heads, int n_kv_heads) {
+  const int group = n_heads / n_kv_heads;
+  const int64_t base = (int64_t)batch * n_kv_heads * ((seq_kv + 127) / 128);
+  for (int hpw = group; hpw > 1; --hpw)
+    if (group % hpw == 0 && base * (group / hpw) >= BN_BWD_MIN_WG) return hpw;
+  return 1;
+}
+
+size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
 
 bool aligned16(const void *ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
 
@@ -323,9 +406,28 @@ bool aligned16(const void *ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u
 
 using namespace bn;
 
-extern "C" size_t bn_gqa_prefill_backward_workspace_size(int batch, int seq_q, int n_heads) {
-  if (batch <= 0 || seq_q <= 0 || n_heads <= 0) return 0;
-  return (size_t)batch * n_heads * seq_q * sizeof(float);
+// D (fp32 [batch, n_heads, seq_q]) and, when the KV heads' query heads are
+// split over workgroups, the fp32 dK/dV partial sums
+static void workspace_parts(int batch, int seq_q, int seq_kv, int n_heads, int n_kv_heads,
+                            size_t *d_bytes, size_t *part_bytes, int *hpw) {
+  *d_bytes = seq_q > 0 ? align256((size_t)batch * n_heads * seq_q * sizeof(float)) : 0;
+  *hpw = heads_per_wg(batch, seq_kv, n_heads, n_kv_heads);
+  const int nchunk = (n_heads / n_kv_heads) / *hpw;
+  *part_bytes = (nchunk > 1 && seq_kv > 0)
+                    ? (size_t)batch * n_kv_heads * nchunk * 2 * seq_kv * HD * sizeof(float)
+                    : 0;
+}
+
+extern "C" size_t bn_gqa_prefill_backward_workspace_size(int batch, int seq_q, int seq_kv,
+                                                          int n_heads, int n_kv_heads,
+                                                          int head_dim) {
+  if (batch <= 0 || seq_q < 0 || seq_kv < 0 || n_heads <= 0 || n_kv_heads <= 0 ||
+      n_heads % n_kv_heads != 0 || head_dim != HD)
+    return 0;
+  size_t d, part;
+  int hpw;
+  workspace_parts(batch, seq_q, seq_kv, n_heads, n_kv_heads, &d, &part, &hpw);
+  return d + part;
 }
 
 extern "C" int bn_gqa_prefill_backward(
@@ -360,14 +462,21 @@ extern "C" int bn_gqa_prefill_backward(
       o_row_stride % 8 || q_batch_stride % 8 || kv_batch_stride % 8 || o_batch_stride % 8)
     return fail(BN_ERR_UNSUPPORTED,
                 std::string(op) + ": pointers must be 16-byte aligned and strides multiples of 16 bytes");
-  const size_t need = seq_q > 0 ? bn_gqa_prefill_backward_workspace_size(batch, seq_q, n_heads) : 0;
+  size_t d_bytes, part_bytes;
+  int hpw;
+  workspace_parts(batch, seq_q, seq_kv, n_heads, n_kv_heads, &d_bytes, &part_bytes, &hpw);
+  const size_t need = d_bytes + part_bytes;
   if (workspace && workspace_bytes < need)
     return fail(BN_ERR_INVALID_ARG, std::string(op) + ": workspace of " +
                                         std::to_string(workspace_bytes) + " bytes, need " +
                                         std::to_string(need));
+  if (workspace && !aligned16(workspace))
+    return fail(BN_ERR_UNSUPPORTED, std::string(op) + ": workspace must be 16-byte aligned");
+  const int nchunk = (n_heads / n_kv_heads) / hpw;
   const int64_t n_dq = (int64_t)batch * n_heads * ((seq_q + 127) / 128);
-  const int64_t n_dkv = (int64_t)batch * n_kv_heads * ((seq_kv + 127) / 128);
-  if (n_dq > 0x7fffffff || n_dkv > 0x7fffffff)
+  const int64_t n_dkv = (int64_t)batch * n_kv_heads * nchunk * ((seq_kv + 127) / 128);
+  const int64_t n_red = part_bytes ? (int64_t)batch * n_kv_heads * 2 * seq_kv * 8 : 0;
+  if (n_dq > 0x7fffffff || n_dkv > 0x7fffffff || (n_red + 255) / 256 > 0x7fffffff)
     return fail(BN_ERR_UNSUPPORTED, std::string(op) + ": problem too large");
   int st = ensure_device();
   if (st) return st;
@@ -382,11 +491,13 @@ extern "C" int bn_gqa_prefill_backward(
   p.q = (const bf16_t *)q; p.k = (const bf16_t *)k; p.v = (const bf16_t *)v;
   p.o = (const bf16_t *)o; p.dout = (const bf16_t *)dout; p.lse = lse;
   p.dvec = (float *)ws;
+  p.part = part_bytes ? (float *)((char *)ws + d_bytes) : nullptr;
   p.dq = (bf16_t *)dq; p.dk = (bf16_t *)dk; p.dv = (bf16_t *)dv;
   p.q_bs = q_batch_stride; p.q_rs = q_row_stride; p.kv_bs = kv_batch_stride;
   p.kv_rs = kv_row_stride; p.o_bs = o_batch_stride; p.o_rs = o_row_stride;
   p.batch = batch; p.seq_q = seq_q; p.seq_kv = seq_kv; p.n_heads = n_heads;
   p.group = n_heads / n_kv_heads; p.causal = causal ? 1 : 0; p.seq_offset = seq_offset;
+  p.n_kv = n_kv_heads; p.hpw = hpw; p.nchunk = nchunk;
   p.scale = scale; p.c = scale * kLog2e;
   hipError_t e = hipSuccess;
   if (n_dq > 0) {
@@ -395,6 +506,11 @@ extern "C" int bn_gqa_prefill_backward(
   }
   if (e == hipSuccess && n_dkv > 0) {
     hipLaunchKernelGGL(prefill_bwd_dkv_kernel, dim3((unsigned)n_dkv), dim3(256), 0, s, p);
+    e = hipGetLastError();
+  }
+  if (e == hipSuccess && n_red > 0) {
+    hipLaunchKernelGGL(prefill_bwd_reduce_kernel, dim3((unsigned)((n_red + 255) / 256)), dim3(256),
+                       0, s, p, n_red);
     e = hipGetLastError();
   }
   st = e == hipSuccess ? BN_OK : hip_fail(e, __FILE__, __LINE__);

@@ -16,6 +16,8 @@ Also measured in the same run and reported as sub-objects:
   prefill_long  config 5's prefill, B=1, S=16384, bf16
   add_rmsnorm   fused residual add + RMSNorm, bf16 [16384, 2048], GB/s
   silu_mul      SwiGLU activation, bf16 [16384, 5632], GB/s
+  prefill_backward  config 2's flash-style backward (dQ, dK, dV), bf16,
+                TFLOP/s of 2.5x the forward's algorithmic flops
 Each carries a ``roofline`` object priced against MI355X peaks (bf16 MFMA
 2.5 PFLOP/s dense, fp32 MFMA 157.3 TFLOP/s, HBM 8 TB/s).  ``cpu_baseline``
 times the CPU oracle (a single-threaded C restatement of the reference
@@ -117,6 +119,33 @@ def bench_prefill(B_, S, H, Hkv, dtype, steps, warmup, seed=0):
             "roofline": roofline("mfma", tflops, peak, "TFLOP/s",
                                  measured_traffic("prefill_bf16") if (dtype == "bf16" and S == 2048)
                                  else None)}
+
+
+def bench_backward(steps, warmup, seed=5):
+    """Config 2's backward: one step = bn_gqa_prefill_backward (the dQ kernel,
+    then the dK/dV kernel) from the forward's o and lse.  Algorithmic work:
+    five products over the causal half, 2.5x the forward's flops (S = QK^T
+    recomputed, dP = dO V^T, dQ = dS K, dK = dS^T Q, dV = P^T dO)."""
+    import torch
+    import bnhip
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    B_, S, H, Hkv = 4, 2048, 32, 4
+    q = torch.randn((B_, S, H, 64), generator=g, device="cuda").to(torch.bfloat16)
+    k = torch.randn((B_, S, Hkv, 64), generator=g, device="cuda").to(torch.bfloat16)
+    v = torch.randn((B_, S, Hkv, 64), generator=g, device="cuda").to(torch.bfloat16)
+    do = torch.randn((B_, S, H, 64), generator=g, device="cuda").to(torch.bfloat16)
+    o, lse = bnhip.gqa_prefill_lse(q, k, v, scale=0.125)
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    ws = torch.empty(bnhip.lib().bn_gqa_prefill_backward_workspace_size(B_, S, S, H, Hkv, 64) // 4,
+                     dtype=torch.float32, device="cuda")
+    ms = time_launches(lambda i: bnhip.gqa_prefill_backward(q, k, v, o, do, lse, scale=0.125,
+                                                            dq=dq, dk=dk, dv=dv, workspace=ws),
+                       steps, warmup)
+    fl = 5 * prefill_flops(B_, S, H, 64) // 2
+    tflops = fl / (ms * 1e-3) / 1e12
+    return {"value": round(tflops, 3), "unit": "TFLOP/s", "ms_per_launch": round(ms, 5),
+            "flops_per_launch": fl, "config": "config 2 backward, bf16",
+            "roofline": roofline("mfma", tflops, PEAK_BF16_TFLOPS, "TFLOP/s")}
 
 
 def bench_decode(ragged, steps, warmup, seed=2):
@@ -396,7 +425,7 @@ def main():
                          "so a kernel trace holds exactly one prefill + 128 steps)")
     ap.add_argument("--only", default="",
                     help="comma list of extra workloads (default: all but copy): "
-                         "decode,ragged,fp32,norm,long,addnorm,swiglu,block,tinyllama,copy; "
+                         "decode,ragged,fp32,norm,long,addnorm,swiglu,bwd,block,tinyllama,copy; "
                          "'head' = headline prefill only")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -446,6 +475,10 @@ def main():
     if want("swiglu"):
         out["silu_mul"] = bench_silu_mul(K, W)
         print(f"silu_mul: {out['silu_mul']['value']} GB/s", file=sys.stderr, flush=True)
+    if want("bwd"):
+        out["prefill_backward"] = bench_backward(K, W)
+        print(f"prefill backward: {out['prefill_backward']['value']} TFLOP/s "
+              f"({out['prefill_backward']['ms_per_launch']} ms)", file=sys.stderr, flush=True)
     if want("block"):
         out["attention_block"], blk_inputs = bench_block(K, W)
         if not args.no_cpu:

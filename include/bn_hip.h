@@ -208,10 +208,13 @@ int bn_gqa_prefill_lse(int dtype, const void *q, const void *k, const void *v,
  * as in the forward.  dq, dk and dv are written, not accumulated.  It
  * replaces the reference autograd chain through op_mm (op_mm.cuh),
  * op_softmax_backward (op_softmax.cuh:182-246), the scale op and repeat_kv's
- * gradient sum (llama_layers.hpp:156-167).  workspace (fp32 D,
- * bn_gqa_prefill_backward_workspace_size bytes) may be NULL: the pool then
- * supplies it. */
-size_t bn_gqa_prefill_backward_workspace_size(int batch, int seq_q, int n_heads);
+ * gradient sum (llama_layers.hpp:156-167).  workspace (16-byte aligned,
+ * bn_gqa_prefill_backward_workspace_size bytes: fp32 D and, when a KV head's
+ * query heads are split over workgroups, fp32 dK/dV partial sums) may be
+ * NULL: the pool then supplies it.  Results are deterministic: no atomics. */
+size_t bn_gqa_prefill_backward_workspace_size(int batch, int seq_q, int seq_kv,
+                                              int n_heads, int n_kv_heads,
+                                              int head_dim);
 int bn_gqa_prefill_backward(int dtype, const void *q, const void *k,
                             const void *v, const void *o, const void *dout,
                             const float *lse, void *dq, void *dk, void *dv,

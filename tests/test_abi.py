@@ -181,8 +181,13 @@ def test_prefill_backward_validation(kw, status):
 
 def test_prefill_backward_workspace_size_and_empty():
     L = B.lib()
-    assert L.bn_gqa_prefill_backward_workspace_size(4, 2048, 32) == 4 * 32 * 2048 * 4
-    assert L.bn_gqa_prefill_backward_workspace_size(0, 2048, 32) == 0
+    # config 2: D (fp32 per query row) + fp32 dK/dV partials of 8 one-head chunks
+    assert L.bn_gqa_prefill_backward_workspace_size(4, 2048, 2048, 32, 4, 64) == \
+        4 * 32 * 2048 * 4 + 4 * 4 * 8 * 2 * 2048 * 64 * 4
+    # one query head per KV head: no partials; D rounded up to 256 bytes
+    assert L.bn_gqa_prefill_backward_workspace_size(1, 100, 100, 8, 8, 64) == 3328
+    assert L.bn_gqa_prefill_backward_workspace_size(0, 2048, 2048, 32, 4, 64) == 0
+    assert L.bn_gqa_prefill_backward_workspace_size(4, 2048, 2048, 32, 4, 128) == 0
     assert st("bn_gqa_prefill_backward", *backward_args(batch=0))[0] == B.BN_OK
     assert st("bn_gqa_prefill_backward", *backward_args(seq_q=0, seq_kv=0))[0] == B.BN_OK
 
