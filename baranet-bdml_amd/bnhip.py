@@ -86,7 +86,7 @@ def lib():
         "bn_sum": ([V, V, i, vp], i), "bn_argmax": ([V, V, vp], i), "bn_copy": ([V, V, vp], i),
         "bn_gqa_prefill": ([i, vp, vp, vp, vp] + [i] * 6 + [i64] * 6 + [f, i, i, vp], i),
         "bn_gqa_prefill_lse": ([i, vp, vp, vp, vp, vp] + [i] * 6 + [i64] * 6 + [f, i, i, vp], i),
-        "bn_gqa_prefill_backward_workspace_size": ([i] * 6, sz),
+        "bn_gqa_prefill_backward_workspace_size": ([i] * 7, sz),
         "bn_gqa_prefill_backward": ([i] + [vp] * 9 + [i] * 6 + [i64] * 6 + [f, i, i, vp, sz, vp], i),
         "bn_gqa_decode_workspace_size": ([i, i, i, i], sz),
         "bn_gqa_decode": ([i, vp, vp, vp, vp, vp] + [i] * 5 + [f, vp, sz, vp], i),

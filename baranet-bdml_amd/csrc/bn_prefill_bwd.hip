@@ -22,6 +22,8 @@
 //     Q/dO tiles of 32 rows are staged in LDS.  Per tile:
 //       S = Q K^T, dP = dO V^T        (lane = key)
 //       dV^T += dO^T P, dK^T += Q^T dS
+#include <type_traits>
+
 #include "bn_common.hpp"
 
 namespace bn {
@@ -36,6 +38,9 @@ typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 constexpr int HD = 64;
 constexpr int P16 = HD + 8;  // LDS row pitch (elements), 144 B: b128 row reads and tr16 reads
 constexpr float kLog2e = 1.4426950408889634f;
+#ifndef BN_BWD_MASK_SKIP
+#define BN_BWD_MASK_SKIP 1  // tiles clear of the causal diagonal and the sequence end skip the mask
+#endif
 
 struct BwdParams {
   const bf16_t *q, *k, *v, *o, *dout;
@@ -182,13 +187,23 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dq_kernel(BwdParams p) {
       }
       // s[i] = S^T[key kb + 8(i/4) + 4hf + i%4][query qrow]
       bf16x8_t dsb[2];
+      auto make_ds = [&](auto masked_tag) __attribute__((always_inline)) {
+        constexpr bool MASKED = decltype(masked_tag)::value;
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int key = kb + (i >> 2) * 8 + hf * 4 + (i & 3);
-        float pr = __builtin_amdgcn_exp2f(fmaf(s[i], p.c, -lse2));
-        if (key >= p.seq_kv || (long)key > qlimit) pr = 0.f;
-        dsb[i >> 3][i & 7] = (__bf16)(pr * (dp[i] - dsum));
-      }
+        for (int i = 0; i < 16; ++i) {
+          const int key = kb + (i >> 2) * 8 + hf * 4 + (i & 3);
+          float pr = __builtin_amdgcn_exp2f(fmaf(s[i], p.c, -lse2));
+          if (MASKED && (key >= p.seq_kv || (long)key > qlimit)) pr = 0.f;
+          dsb[i >> 3][i & 7] = (__bf16)(pr * (dp[i] - dsum));
+        }
+      };
+      // wave-uniform: every key of the sub-tile exists and every row of the
+      // wave sees it (padding rows have P = 0 through lse2 = +inf)
+      const bool full = kb + 31 < p.seq_kv && (!p.causal || (long)kb + 31 <= (long)q0 + p.seq_offset);
+      if (BN_BWD_MASK_SKIP && full)
+        make_ds(std::false_type{});
+      else
+        make_ds(std::true_type{});
 #pragma unroll
       for (int u = 0; u < 2; ++u)
 #pragma unroll
@@ -202,7 +217,10 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dq_kernel(BwdParams p) {
 }
 
 // ----------------------------------------------------------------- dK, dV
-constexpr int TPI = 2;  // 32-row query tiles staged per barrier
+#ifndef BN_BWD_TPI
+#define BN_BWD_TPI 1
+#endif
+constexpr int TPI = BN_BWD_TPI;  // 32-row query tiles staged per barrier
 
 // One workgroup per (key block of 128, batch, KV head, head chunk): the
 // chunk's hpw query heads are walked in turn.  With one chunk (hpw = group)
@@ -311,21 +329,31 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dkv_kernel(BwdParams p) {
       }
       // s[i] = S[query qb + 8(i/4) + 4hf + i%4][key]
       bf16x8_t pb[2], sb[2];
+      auto make_p = [&](auto masked_tag) __attribute__((always_inline)) {
+        constexpr bool MASKED = decltype(masked_tag)::value;
 #pragma unroll
-      for (int gi = 0; gi < 4; ++gi) {
-        const float4 l4 = *(const float4 *)(&lse_s[buf][t][8 * gi + 4 * hf]);
-        const float4 d4 = *(const float4 *)(&dv_s[buf][t][8 * gi + 4 * hf]);
-        const float lv[4] = {l4.x, l4.y, l4.z, l4.w}, dvl[4] = {d4.x, d4.y, d4.z, d4.w};
+        for (int gi = 0; gi < 4; ++gi) {
+          const float4 l4 = *(const float4 *)(&lse_s[buf][t][8 * gi + 4 * hf]);
+          const float4 d4 = *(const float4 *)(&dv_s[buf][t][8 * gi + 4 * hf]);
+          const float lv[4] = {l4.x, l4.y, l4.z, l4.w}, dvl[4] = {d4.x, d4.y, d4.z, d4.w};
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int i = 4 * gi + e;
-          const int qrow = qb + 8 * gi + 4 * hf + e;
-          float pr = __builtin_amdgcn_exp2f(fmaf(s[i], p.c, -lv[e]));
-          if (!key_ok || (p.causal && (long)key > (long)qrow + p.seq_offset)) pr = 0.f;
-          pb[i >> 3][i & 7] = (__bf16)pr;
-          sb[i >> 3][i & 7] = (__bf16)(pr * (dp[i] - dvl[e]));
+          for (int e = 0; e < 4; ++e) {
+            const int i = 4 * gi + e;
+            const int qrow = qb + 8 * gi + 4 * hf + e;
+            float pr = __builtin_amdgcn_exp2f(fmaf(s[i], p.c, -lv[e]));
+            if (MASKED && (!key_ok || (p.causal && (long)key > (long)qrow + p.seq_offset))) pr = 0.f;
+            pb[i >> 3][i & 7] = (__bf16)pr;
+            sb[i >> 3][i & 7] = (__bf16)(pr * (dp[i] - dvl[e]));
+          }
         }
-      }
+      };
+      // wave-uniform: the wave's 32 keys exist and the tile's first row sees
+      // all of them (padding rows have P = 0 through lse2 = +inf)
+      const bool full = k0 + 31 < p.seq_kv && (!p.causal || (long)qb + p.seq_offset >= (long)k0 + 31);
+      if (BN_BWD_MASK_SKIP && full)
+        make_p(std::false_type{});
+      else
+        make_p(std::true_type{});
 #pragma unroll
       for (int u = 0; u < 2; ++u)
 #pragma unroll
@@ -384,17 +412,29 @@ __global__ __launch_bounds__(256) void prefill_bwd_reduce_kernel(BwdParams p, in
   *(uint4 *)dst = make_uint4(w[0], w[1], w[2], w[3]);
 }
 
-// query heads per dK/dV workgroup: the largest divisor of the group size that
-// still gives at least BN_BWD_MIN_WG workgroups (the whole group when G = 1)
-#ifndef BN_BWD_MIN_WG
-#define BN_BWD_MIN_WG 2048
-#endif
-int heads_per_wg(int batch, int seq_kv, int n_heads, int n_kv_heads) {
+// Query heads per dK/dV workgroup: walking the divisors of the group size
+// downward, the first that gives enough workgroups (2048 under a causal mask,
+// whose key blocks differ in work, else 512), stopping early where the fp32
+// partial sums would pass 0.5 byte per 1000 flops of the backward (their
+// write and the reduction's read then cost more than the parallelism gains).
+// Measured on config 2 (B=4, S=2048, 32/4 heads), TFLOP/s: causal hpw 8/4/2/1
+// -> -/392/509/470, non-causal hpw 4/2/1 -> 564/548/523; B=1, S=16384
+// causal hpw 4/2/1 -> 551/591/604.
+int heads_per_wg(int batch, int seq_q, int seq_kv, int n_heads, int n_kv_heads, int causal) {
   const int group = n_heads / n_kv_heads;
   const int64_t base = (int64_t)batch * n_kv_heads * ((seq_kv + 127) / 128);
-  for (int hpw = group; hpw > 1; --hpw)
-    if (group % hpw == 0 && base * (group / hpw) >= BN_BWD_MIN_WG) return hpw;
-  return 1;
+  const int64_t min_wg = causal ? 2048 : 512;
+  // backward flops / 1000: 5 products of B*H*Sq*Skv*64 MACs (half under a causal mask)
+  const double kflops = 10.0 * batch * n_heads * (double)seq_q * seq_kv * HD / (causal ? 2 : 1) / 1000;
+  int best = group;
+  for (int hpw = group; hpw >= 1; --hpw) {
+    if (group % hpw) continue;
+    const double part = (hpw < group) ? 2.0 * batch * n_heads / hpw * (double)seq_kv * HD * 4 : 0;
+    if (part > 0.5 * kflops) break;
+    best = hpw;
+    if (base * (group / hpw) >= min_wg) break;
+  }
+  return best;
 }
 
 size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
@@ -409,9 +449,9 @@ using namespace bn;
 // D (fp32 [batch, n_heads, seq_q]) and, when the KV heads' query heads are
 // split over workgroups, the fp32 dK/dV partial sums
 static void workspace_parts(int batch, int seq_q, int seq_kv, int n_heads, int n_kv_heads,
-                            size_t *d_bytes, size_t *part_bytes, int *hpw) {
+                            int causal, size_t *d_bytes, size_t *part_bytes, int *hpw) {
   *d_bytes = seq_q > 0 ? align256((size_t)batch * n_heads * seq_q * sizeof(float)) : 0;
-  *hpw = heads_per_wg(batch, seq_kv, n_heads, n_kv_heads);
+  *hpw = heads_per_wg(batch, seq_q, seq_kv, n_heads, n_kv_heads, causal);
   const int nchunk = (n_heads / n_kv_heads) / *hpw;
   *part_bytes = (nchunk > 1 && seq_kv > 0)
                     ? (size_t)batch * n_kv_heads * nchunk * 2 * seq_kv * HD * sizeof(float)
@@ -420,13 +460,13 @@ static void workspace_parts(int batch, int seq_q, int seq_kv, int n_heads, int n
 
 extern "C" size_t bn_gqa_prefill_backward_workspace_size(int batch, int seq_q, int seq_kv,
                                                           int n_heads, int n_kv_heads,
-                                                          int head_dim) {
+                                                          int head_dim, int causal) {
   if (batch <= 0 || seq_q < 0 || seq_kv < 0 || n_heads <= 0 || n_kv_heads <= 0 ||
       n_heads % n_kv_heads != 0 || head_dim != HD)
     return 0;
   size_t d, part;
   int hpw;
-  workspace_parts(batch, seq_q, seq_kv, n_heads, n_kv_heads, &d, &part, &hpw);
+  workspace_parts(batch, seq_q, seq_kv, n_heads, n_kv_heads, causal ? 1 : 0, &d, &part, &hpw);
   return d + part;
 }
 
@@ -464,7 +504,8 @@ extern "C" int bn_gqa_prefill_backward(
                 std::string(op) + ": pointers must be 16-byte aligned and strides multiples of 16 bytes");
   size_t d_bytes, part_bytes;
   int hpw;
-  workspace_parts(batch, seq_q, seq_kv, n_heads, n_kv_heads, &d_bytes, &part_bytes, &hpw);
+  workspace_parts(batch, seq_q, seq_kv, n_heads, n_kv_heads, causal ? 1 : 0, &d_bytes, &part_bytes,
+                  &hpw);
   const size_t need = d_bytes + part_bytes;
   if (workspace && workspace_bytes < need)
     return fail(BN_ERR_INVALID_ARG, std::string(op) + ": workspace of " +

@@ -136,7 +136,7 @@ def bench_backward(steps, warmup, seed=5):
     do = torch.randn((B_, S, H, 64), generator=g, device="cuda").to(torch.bfloat16)
     o, lse = bnhip.gqa_prefill_lse(q, k, v, scale=0.125)
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
-    ws = torch.empty(bnhip.lib().bn_gqa_prefill_backward_workspace_size(B_, S, S, H, Hkv, 64) // 4,
+    ws = torch.empty(bnhip.lib().bn_gqa_prefill_backward_workspace_size(B_, S, S, H, Hkv, 64, 1) // 4,
                      dtype=torch.float32, device="cuda")
     ms = time_launches(lambda i: bnhip.gqa_prefill_backward(q, k, v, o, do, lse, scale=0.125,
                                                             dq=dq, dk=dk, dv=dv, workspace=ws),

@@ -214,7 +214,7 @@ int bn_gqa_prefill_lse(int dtype, const void *q, const void *k, const void *v,
  * NULL: the pool then supplies it.  Results are deterministic: no atomics. */
 size_t bn_gqa_prefill_backward_workspace_size(int batch, int seq_q, int seq_kv,
                                               int n_heads, int n_kv_heads,
-                                              int head_dim);
+                                              int head_dim, int causal);
 int bn_gqa_prefill_backward(int dtype, const void *q, const void *k,
                             const void *v, const void *o, const void *dout,
                             const float *lse, void *dq, void *dk, void *dv,

@@ -181,13 +181,17 @@ def test_prefill_backward_validation(kw, status):
 
 def test_prefill_backward_workspace_size_and_empty():
     L = B.lib()
-    # config 2: D (fp32 per query row) + fp32 dK/dV partials of 8 one-head chunks
-    assert L.bn_gqa_prefill_backward_workspace_size(4, 2048, 2048, 32, 4, 64) == \
-        4 * 32 * 2048 * 4 + 4 * 4 * 8 * 2 * 2048 * 64 * 4
+    # config 2, causal: D (fp32 per query row) + fp32 dK/dV partials of 4
+    # two-head chunks (one-head chunks would pass 0.5 byte per 1000 flops)
+    assert L.bn_gqa_prefill_backward_workspace_size(4, 2048, 2048, 32, 4, 64, 1) == \
+        4 * 32 * 2048 * 4 + 4 * 4 * 4 * 2 * 2048 * 64 * 4
+    # non-causal: 512 workgroups are enough, 4-head chunks
+    assert L.bn_gqa_prefill_backward_workspace_size(4, 2048, 2048, 32, 4, 64, 0) == \
+        4 * 32 * 2048 * 4 + 4 * 4 * 2 * 2 * 2048 * 64 * 4
     # one query head per KV head: no partials; D rounded up to 256 bytes
-    assert L.bn_gqa_prefill_backward_workspace_size(1, 100, 100, 8, 8, 64) == 3328
-    assert L.bn_gqa_prefill_backward_workspace_size(0, 2048, 2048, 32, 4, 64) == 0
-    assert L.bn_gqa_prefill_backward_workspace_size(4, 2048, 2048, 32, 4, 128) == 0
+    assert L.bn_gqa_prefill_backward_workspace_size(1, 100, 100, 8, 8, 64, 1) == 3328
+    assert L.bn_gqa_prefill_backward_workspace_size(0, 2048, 2048, 32, 4, 64, 1) == 0
+    assert L.bn_gqa_prefill_backward_workspace_size(4, 2048, 2048, 32, 4, 128, 1) == 0
     assert st("bn_gqa_prefill_backward", *backward_args(batch=0))[0] == B.BN_OK
     assert st("bn_gqa_prefill_backward", *backward_args(seq_q=0, seq_kv=0))[0] == B.BN_OK
 

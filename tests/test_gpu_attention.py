@@ -393,7 +393,7 @@ def test_prefill_backward_workspace_and_repeat():
     q, k, v, do = (dev(a, torch.bfloat16) for a in bwd_inputs(case, 30))
     o, lse = B.gqa_prefill_lse(q, k, v, scale=0.125)
     a = B.gqa_prefill_backward(q, k, v, o, do, lse, scale=0.125)
-    ws = torch.empty(B.lib().bn_gqa_prefill_backward_workspace_size(2, 200, 200, 8, 2, 64) // 4,
+    ws = torch.empty(B.lib().bn_gqa_prefill_backward_workspace_size(2, 200, 200, 8, 2, 64, 1) // 4,
                      dtype=torch.float32, device="cuda")
     b = B.gqa_prefill_backward(q, k, v, o, do, lse, scale=0.125, workspace=ws)
     c = B.gqa_prefill_backward(q, k, v, o, do, lse, scale=0.125, workspace=ws)
