@@ -10,6 +10,7 @@
 //   (:256-310), randgen_seed (bindings.cu:16-18), LLaMAConfig
 //   (llama_bindings.hpp:99-111).
 // Additions (new names only): TensorBF16, Tensor*.rmsnorm_rope, gqa_prefill,
+// gqa_prefill_lse, gqa_prefill_backward,
 // gqa_decode, repeat_kv, add_rmsnorm, silu_mul, pool_stats / pool_trim / pool_set_limit,
 // synchronize, set_stream / get_stream.
 //
@@ -440,6 +441,66 @@ PyTensor<DT> gqa_prefill(const PyTensor<DT> &q, const PyTensor<DT> &k, const PyT
   return out;
 }
 
+// gqa_prefill that also returns lse, TensorF [batch*n_heads, seq_q]: the
+// natural-log row log-sum-exp the backward recomputes the probabilities from
+template <int DT>
+py::tuple gqa_prefill_lse(const PyTensor<DT> &q, const PyTensor<DT> &k, const PyTensor<DT> &v,
+                          int batch, int n_heads, int n_kv_heads, int head_dim, py::object scale,
+                          bool causal, int seq_offset) {
+  const char *op = "GQA prefill";
+  require_rows(q, op, "q");
+  require_rows(k, op, "k");
+  require_rows(v, op, "v");
+  if (batch <= 0 || q.h % batch || k.h % batch || v.h != k.h)
+    throw std::runtime_error("GQA prefill: rows of q and k/v must be batch * seq_len");
+  if (q.w != n_heads * head_dim || k.w != n_kv_heads * head_dim || v.w != k.w)
+    throw std::runtime_error("GQA prefill: widths must be n_heads*head_dim and n_kv_heads*head_dim");
+  if (k.stride_h != v.stride_h) throw std::runtime_error("GQA prefill: k and v row strides differ");
+  float sc = scale.is_none() ? (float)(1.0 / std::sqrt((double)head_dim)) : scale.cast<float>();
+  const int seq_q = q.h / batch, seq_kv = k.h / batch;
+  PyTensor<DT> out(q.h, q.w, true);
+  TF lse(batch * n_heads, seq_q, true);
+  check(bn_gqa_prefill_lse(DT, q.base(), k.base(), v.base(), out.base(), (float *)lse.base(), batch,
+                           seq_q, seq_kv, n_heads, n_kv_heads, head_dim,
+                           (int64_t)seq_q * q.stride_h, q.stride_h, (int64_t)seq_kv * k.stride_h,
+                           k.stride_h, (int64_t)seq_q * out.stride_h, out.stride_h, sc,
+                           causal ? 1 : 0, seq_offset, g_stream));
+  return py::make_tuple(out, lse);
+}
+
+// (dq, dk, dv) of gqa_prefill from its output o, lse and the gradient dout
+// (bf16 kernels; TensorF inputs are rejected by the C ABI)
+template <int DT>
+py::tuple gqa_prefill_backward(const PyTensor<DT> &q, const PyTensor<DT> &k, const PyTensor<DT> &v,
+                               const PyTensor<DT> &o, const PyTensor<DT> &dout, const TF &lse,
+                               int batch, int n_heads, int n_kv_heads, int head_dim,
+                               py::object scale, bool causal, int seq_offset) {
+  const char *op = "GQA prefill backward";
+  for (auto t : {&q, &k, &v, &o, &dout}) require_rows(*t, op, "inputs");
+  if (batch <= 0 || q.h % batch || k.h % batch || v.h != k.h || o.h != q.h || dout.h != q.h)
+    throw std::runtime_error("GQA prefill backward: rows of q/o/dout and k/v must be batch * seq_len");
+  if (q.w != n_heads * head_dim || k.w != n_kv_heads * head_dim || v.w != k.w || o.w != q.w ||
+      dout.w != q.w)
+    throw std::runtime_error("GQA prefill backward: widths must be n_heads*head_dim and n_kv_heads*head_dim");
+  if (k.stride_h != v.stride_h || o.stride_h != dout.stride_h)
+    throw std::runtime_error("GQA prefill backward: k/v and o/dout row strides must match");
+  const int seq_q = q.h / batch, seq_kv = k.h / batch;
+  if (!lse.on_device || !lse.contiguous() || lse.h != batch * n_heads || lse.w != seq_q)
+    throw std::runtime_error("GQA prefill backward: lse must be a contiguous device TensorF [batch*n_heads, seq_q]");
+  float sc = scale.is_none() ? (float)(1.0 / std::sqrt((double)head_dim)) : scale.cast<float>();
+  PyTensor<DT> dq(q.h, q.w, true), dk(k.h, k.w, true), dv(v.h, v.w, true);
+  // dq takes q's row stride, dk/dv k's: fresh tensors are dense, so q/k must be too
+  if (q.stride_h != dq.stride_h || k.stride_h != dk.stride_h)
+    throw std::runtime_error("GQA prefill backward: q and k/v must have dense rows");
+  check(bn_gqa_prefill_backward(DT, q.base(), k.base(), v.base(), o.base(), dout.base(),
+                                (const float *)lse.base(), dq.base(), dk.base(), dv.base(), batch,
+                                seq_q, seq_kv, n_heads, n_kv_heads, head_dim,
+                                (int64_t)seq_q * q.stride_h, q.stride_h, (int64_t)seq_kv * k.stride_h,
+                                k.stride_h, (int64_t)seq_q * o.stride_h, o.stride_h, sc,
+                                causal ? 1 : 0, seq_offset, nullptr, 0, g_stream));
+  return py::make_tuple(dq, dk, dv);
+}
+
 // q [batch, n_heads*head_dim]; caches [batch*max_len, n_kv_heads*head_dim];
 // seq_lens: TensorU32 holding batch lengths
 template <int DT>
@@ -604,6 +665,26 @@ PYBIND11_MODULE(bten, m) {
         py::arg("batch") = 1, py::arg("n_heads") = 32, py::arg("n_kv_heads") = 4,
         py::arg("head_dim") = 64, py::arg("scale") = py::none(), py::arg("causal") = true,
         py::arg("seq_offset") = 0);
+  for (int bf = 0; bf < 2; ++bf) {
+    auto args_lse = [&](auto fn) {
+      m.def("gqa_prefill_lse", fn, py::arg("q"), py::arg("k"), py::arg("v"), py::arg("batch") = 1,
+            py::arg("n_heads") = 32, py::arg("n_kv_heads") = 4, py::arg("head_dim") = 64,
+            py::arg("scale") = py::none(), py::arg("causal") = true, py::arg("seq_offset") = 0);
+    };
+    auto args_bwd = [&](auto fn) {
+      m.def("gqa_prefill_backward", fn, py::arg("q"), py::arg("k"), py::arg("v"), py::arg("o"),
+            py::arg("dout"), py::arg("lse"), py::arg("batch") = 1, py::arg("n_heads") = 32,
+            py::arg("n_kv_heads") = 4, py::arg("head_dim") = 64, py::arg("scale") = py::none(),
+            py::arg("causal") = true, py::arg("seq_offset") = 0);
+    };
+    if (bf) {
+      args_lse(&gqa_prefill_lse<BN_BF16>);
+      args_bwd(&gqa_prefill_backward<BN_BF16>);
+    } else {
+      args_lse(&gqa_prefill_lse<BN_F32>);
+      args_bwd(&gqa_prefill_backward<BN_F32>);
+    }
+  }
   m.def("gqa_decode", &gqa_decode<BN_F32>, py::arg("q"), py::arg("k_cache"), py::arg("v_cache"),
         py::arg("seq_lens"), py::arg("n_heads") = 32, py::arg("n_kv_heads") = 4,
         py::arg("head_dim") = 64, py::arg("scale") = py::none());

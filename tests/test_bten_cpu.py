@@ -79,6 +79,11 @@ def test_gpu_only_ops_raise_on_host_tensors():
         x.rope(0, 48)
     with pytest.raises(RuntimeError, match="only GPU implementation available"):
         bten.gqa_prefill(x, x, x, 1, 1, 1, 64)
+    with pytest.raises(RuntimeError, match="only GPU implementation available"):
+        bten.gqa_prefill_lse(x, x, x, 1, 1, 1, 64)
+    lse = bten.TensorF(1, 4, False)
+    with pytest.raises(RuntimeError, match="only GPU implementation available"):
+        bten.gqa_prefill_backward(x, x, x, x, x, lse, 1, 1, 1, 64)
 
 
 def test_defaults_match_reference_signatures():

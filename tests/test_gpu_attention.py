@@ -429,3 +429,31 @@ def test_prefill_backward_baseline_shape():
             assert np.max(np.abs(got - want)) <= BF16_TOL * np.max(np.abs(want)), (b, g)
             zs = np.abs(gk[b, :, g].astype(np.float64).sum(0))
             assert np.all(zs <= BF16_TOL * np.abs(gk[b, :, g]).sum(0)), (b, g)
+
+
+def test_bten_surface_backward_matches_c_abi():
+    # the pybind11 surface (rows = tokens, [batch*seq, heads*64]) runs the same
+    # kernels: identical bits to the ctypes path, and the oracle's gradients
+    import bten
+    case = (2, 150, 150, 8, 2, 1, 0)
+    Bn, S, _, H, Hkv, _, _ = case
+    q, k, v, do = bwd_inputs(case, 50)
+
+    def t(a):
+        rows, cols = a.shape[0] * a.shape[1], a.shape[2] * a.shape[3]
+        x = bten.TensorBF16(rows, cols, True)
+        x.copy_from_numpy(np.ascontiguousarray(a.reshape(rows, cols)))
+        return x
+
+    tq, tk, tv, tdo = t(q), t(k), t(v), t(do)
+    o, lse = bten.gqa_prefill_lse(tq, tk, tv, Bn, H, Hkv, 64, 0.125)
+    dq, dk, dv = bten.gqa_prefill_backward(tq, tk, tv, o, tdo, lse, Bn, H, Hkv, 64, 0.125)
+    bten.synchronize()
+    got = [x.to_numpy().reshape(sh) for x, sh in ((dq, q.shape), (dk, k.shape), (dv, v.shape))]
+    qd, kd, vd, dod = (dev(a, torch.bfloat16) for a in (q, k, v, do))
+    o2, lse2 = B.gqa_prefill_lse(qd, kd, vd, scale=0.125)
+    ref = B.gqa_prefill_backward(qd, kd, vd, o2, dod, lse2, scale=0.125)
+    assert np.array_equal(lse.to_numpy().reshape(Bn, H, S), host(lse2))
+    for g, r in zip(got, ref):
+        assert np.array_equal(g, host(r))
+    check_backward(got, q, k, v, do, host(o2), host(lse2), 1, 0, "bten")
