@@ -87,6 +87,8 @@ def lib():
         "bn_gqa_prefill": ([i, vp, vp, vp, vp] + [i] * 6 + [i64] * 6 + [f, i, i, vp], i),
         "bn_gqa_prefill_lse": ([i, vp, vp, vp, vp, vp] + [i] * 6 + [i64] * 6 + [f, i, i, vp], i),
         "bn_gqa_prefill_backward_workspace_size": ([i] * 7, sz),
+        "bn_linear_rope_workspace_size": ([i] * 4, sz),
+        "bn_linear_rope": ([V, V, V, i, i, i, f, vp, sz, vp], i),
         "bn_gqa_prefill_backward": ([i] + [vp] * 9 + [i] * 6 + [i64] * 6 + [f, i, i, vp, sz, vp], i),
         "bn_gqa_decode_workspace_size": ([i, i, i, i], sz),
         "bn_gqa_decode": ([i, vp, vp, vp, vp, vp] + [i] * 5 + [f, vp, sz, vp], i),
@@ -210,6 +212,17 @@ def gqa_prefill_backward(q, k, v, o, dout, lse, scale=None, causal=True, seq_off
          B, Sq, Skv, H, Hkv, D, q.stride(0), q.stride(1), k.stride(0), k.stride(1), o.stride(0),
          o.stride(1), sc, int(causal), seq_offset, ws, wsb, stream_of(stream))
     return dq, dk, dv
+
+
+def linear_rope(x, w, y=None, rope_cols=0, position_offset=0, head_dim=64, theta=10000.0,
+                workspace=None, stream=None):
+    """y = x @ w with RoPE on columns [0, rope_cols) (2-D torch, f32 or bf16)."""
+    import torch
+    y = torch.empty((x.shape[0], w.shape[1]), dtype=x.dtype, device=x.device) if y is None else y
+    ws, wsb = (None, 0) if workspace is None else (workspace.data_ptr(), workspace.numel() * workspace.element_size())
+    call("bn_linear_rope", C.byref(view(x)), C.byref(view(w)), C.byref(view(y)), rope_cols,
+         position_offset, head_dim, theta, ws, wsb, stream_of(stream))
+    return y
 
 
 def gqa_decode(q, k_cache, v_cache, seq_lens, o=None, scale=None, workspace=None, stream=None):

@@ -1,0 +1,460 @@
+// bn_linear.hip -- the GQA layer's projections on gfx950 MFMA with RoPE in
+// the epilogue: y = x @ w, then the reference's rotation (op_rope.cuh:55-99)
+// on the first rope_cols columns of y -- the Q and K heads of a fused QKV
+// weight -- at position position_offset + row.  rope_cols = 0 is the plain
+// projection (the output projection, llama_layers.hpp:112).
+//
+// A workgroup computes a 64x64 tile of y^T = w^T x^T with 4 waves of 32x32:
+// lane = output row, registers = 16 output columns, so each rotation pair
+// (2p, 2p+1) sits in adjacent registers of one lane.  w and x tiles are
+// staged through LDS (double-buffered, one barrier per k step).  fp32 runs
+// v_mfma_f32_32x32x2_f32 on w rows and x columns read straight from LDS;
+// bf16 runs v_mfma_f32_32x32x16_bf16 with the w^T fragments read by
+// ds_read_b64_tr_b16 and the x fragments in the same k order.  Small grids
+// split k: each slab writes fp32 partial sums and linear_reduce_kernel adds
+// them in slab order and applies the rotation (deterministic, no atomics).
+#include <algorithm>
+
+#include "bn_common.hpp"
+
+namespace bn {
+namespace {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+constexpr int TN = 64, TM = 64;  // workgroup tile: output columns x output rows
+
+template <typename T>
+struct LinCfg;
+template <>
+struct LinCfg<float> {
+  static constexpr int KT = 32;      // k per LDS stage
+  static constexpr int WP = TN + 4;  // Ws[k][n] pitch, elements
+  static constexpr int XP = KT + 4;  // Xs[m][k] pitch
+};
+template <>
+struct LinCfg<bf16_t> {
+  static constexpr int KT = 64;
+  static constexpr int WP = TN + 8;  // 144 B rows: conflict-free transposed 16-bit reads
+  static constexpr int XP = KT + 8;
+};
+
+struct LinParams {
+  const void *x, *w;
+  void *y;
+  float *part;  // [nsplit][m][n] fp32 partial sums, or null
+  int64_t x_rs, w_rs, y_rs;
+  int m, n, k, kchunk;  // kchunk: k per slab, a multiple of the stage depth
+  int rope_cols, head_dim, pos0;
+};
+
+__device__ __forceinline__ bf16x4_t tr16(const bf16_t *lds) {
+  const s16x4_t r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) s16x4_t *)(__attribute__((address_space(3))) void *)lds);
+  return __builtin_bit_cast(bf16x4_t, r);
+}
+
+template <typename T>
+__device__ __forceinline__ void store4(T *dst, const float (&v)[4]);
+template <>
+__device__ __forceinline__ void store4<float>(float *dst, const float (&v)[4]) {
+  *(float4 *)dst = make_float4(v[0], v[1], v[2], v[3]);
+}
+template <>
+__device__ __forceinline__ void store4<bf16_t>(bf16_t *dst, const float (&v)[4]) {
+  const uint32_t lo = (uint32_t)f32_to_bf16(v[0]) | ((uint32_t)f32_to_bf16(v[1]) << 16);
+  const uint32_t hi = (uint32_t)f32_to_bf16(v[2]) | ((uint32_t)f32_to_bf16(v[3]) << 16);
+  *(uint2 *)dst = make_uint2(lo, hi);
+}
+
+// rotation of the pairs (gn, gn+1) and (gn+2, gn+3) of row gm that lie in
+// the first rope_cols columns (op_rope.cuh:79-98: fp32 angle position*freq)
+__device__ __forceinline__ void rope4(float (&v)[4], int gm, int gn, const LinParams &p,
+                                      const RopeFreqs &fr) {
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int c = gn + 2 * j;
+    if (c < p.rope_cols) {
+      const float ang = (float)(p.pos0 + gm) * fr.f[(c % p.head_dim) >> 1];
+      float sn, cs;
+      sincosf(ang, &sn, &cs);
+      const float x0 = v[2 * j], x1 = v[2 * j + 1];
+      v[2 * j] = x0 * cs - x1 * sn;
+      v[2 * j + 1] = x0 * sn + x1 * cs;
+    }
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256, 2) void linear_kernel(LinParams p, RopeFreqs fr) {
+  using C = LinCfg<T>;
+  constexpr int KT = C::KT, WP = C::WP, XP = C::XP;
+  constexpr int VE = 16 / (int)sizeof(T);  // elements per 16-byte chunk
+  constexpr int WCH = TN / VE, XCH = KT / VE;  // chunks per w row, per x row
+  __shared__ __attribute__((aligned(16))) T Ws[2][KT * WP];  // Ws[k][n]
+  __shared__ __attribute__((aligned(16))) T Xs[2][TM * XP];  // Xs[m][k]
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r32 = lane & 31, hf = lane >> 5;
+  const int n_off = 32 * (wave & 1), m_off = 32 * (wave >> 1);
+  const int n0 = blockIdx.x * TN, m0 = blockIdx.y * TM;
+  const int kb = blockIdx.z * p.kchunk, ke = min(kb + p.kchunk, p.k);
+  const T *X = (const T *)p.x, *W = (const T *)p.w;
+
+  // staging: two 16-byte chunks of w and two of x per thread per stage
+  // (KT x TN of w and TM x KT of x are 512 chunks each)
+  u32x4_t wr[2], xr[2];
+  auto gload = [&](int k0) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int c = tid + 256 * i;
+      const int gk = k0 + c / WCH, gn = n0 + (c % WCH) * VE;
+      wr[i] = (gk < ke && gn < p.n) ? *(const u32x4_t *)(W + gk * p.w_rs + gn) : u32x4_t{0u, 0u, 0u, 0u};
+      const int gm = m0 + c / XCH, gk2 = k0 + (c % XCH) * VE;
+      xr[i] = (gm < p.m && gk2 < ke) ? *(const u32x4_t *)(X + gm * p.x_rs + gk2) : u32x4_t{0u, 0u, 0u, 0u};
+    }
+  };
+  auto lstore = [&](int buf) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int c = tid + 256 * i;
+      *(u32x4_t *)(&Ws[buf][(c / WCH) * WP + (c % WCH) * VE]) = wr[i];
+      *(u32x4_t *)(&Xs[buf][(c / XCH) * XP + (c % XCH) * VE]) = xr[i];
+    }
+  };
+  // two accumulators over alternating k steps: independent MFMA chains
+  f32x16_t acc[2] = {f32x16_t{}, f32x16_t{}};
+  const bool busy = m0 + m_off < p.m && n0 + n_off < p.n;  // wave-uniform
+  const int tr_off = (4 * hf + ((lane & 15) >> 2)) * WP + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+  const int nst = ke > kb ? (ke - kb + KT - 1) / KT : 0;
+  if (nst > 0) gload(kb);
+  for (int s = 0; s < nst; ++s) {
+    const int buf = s & 1;
+    lstore(buf);
+    __syncthreads();  // also: every wave finished stage s-2, the last reader of buf
+    if (s + 1 < nst) gload(kb + (s + 1) * KT);
+    if (!busy) continue;
+    const T *ws = Ws[buf], *xs = Xs[buf];
+    if constexpr (sizeof(T) == 4) {
+      // A = w^T: lane holds w[k = 2kk + hf][n]; B = x^T: lane holds x[m][k]
+#pragma unroll
+      for (int kk = 0; kk < KT / 2; ++kk) {
+        const float a = ws[(2 * kk + hf) * WP + n_off + r32];
+        const float b = xs[(m_off + r32) * XP + 2 * kk + hf];
+        acc[kk & 1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, acc[kk & 1], 0, 0, 0);
+      }
+    } else {
+      // A = w^T by transposed reads: slot j of lane half hf is k = 16u +
+      // 8(j/4) + 4hf + j%4; B = x^T in the same k order
+#pragma unroll
+      for (int u = 0; u < KT / 16; ++u) {
+        const bf16_t *wp = ws + 16 * u * WP + tr_off + n_off;
+        const bf16x4_t alo = tr16(wp), ahi = tr16(wp + 8 * WP);
+        const bf16x8_t a = {alo[0], alo[1], alo[2], alo[3], ahi[0], ahi[1], ahi[2], ahi[3]};
+        const bf16_t *xp = xs + (m_off + r32) * XP + 16 * u + 4 * hf;
+        const bf16x4_t blo = *(const bf16x4_t *)xp, bhi = *(const bf16x4_t *)(xp + 8);
+        const bf16x8_t b = {blo[0], blo[1], blo[2], blo[3], bhi[0], bhi[1], bhi[2], bhi[3]};
+        acc[u & 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc[u & 1], 0, 0, 0);
+      }
+    }
+  }
+  if (!busy) return;
+  const int gm = m0 + m_off + r32;
+  if (gm >= p.m) return;
+  // acc[.][4g + e] = y^T[n = n_off + 8g + 4hf + e][m]: four consecutive columns
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const int gn = n0 + n_off + 8 * g + 4 * hf;
+    if (gn >= p.n) continue;
+    float v[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = acc[0][4 * g + e] + acc[1][4 * g + e];
+    if (p.part) {
+      *(float4 *)(p.part + ((int64_t)blockIdx.z * p.m + gm) * p.n + gn) = make_float4(v[0], v[1], v[2], v[3]);
+    } else {
+      rope4(v, gm, gn, p, fr);
+      store4<T>((T *)p.y + gm * p.y_rs + gn, v);
+    }
+  }
+}
+
+// y = sum of the slabs' partial sums (slab 0 first), then the rotation: one
+// thread per four consecutive columns of one row
+template <typename T>
+__global__ __launch_bounds__(256) void linear_reduce_kernel(LinParams p, RopeFreqs fr, int nsplit) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int q = p.n >> 2;
+  if (idx >= (int64_t)p.m * q) return;
+  const int gm = (int)(idx / q), gn = (int)(idx % q) * 4;
+  const int64_t mn = (int64_t)p.m * p.n;
+  const float *src = p.part + (int64_t)gm * p.n + gn;
+  float v[4] = {0.f, 0.f, 0.f, 0.f};
+  // groups of 16 slabs: all loads of a group in flight, then added in slab order
+  constexpr int G = 16;
+  for (int z0 = 0; z0 < nsplit; z0 += G) {
+    float4 a[G];
+#pragma unroll
+    for (int j = 0; j < G; ++j)
+      a[j] = z0 + j < nsplit ? *(const float4 *)(src + (z0 + j) * mn) : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int j = 0; j < G; ++j) {
+      if (z0 + j < nsplit) {
+        v[0] += a[j].x; v[1] += a[j].y; v[2] += a[j].z; v[3] += a[j].w;
+      }
+    }
+  }
+  rope4(v, gm, gn, p, fr);
+  store4<T>((T *)p.y + gm * p.y_rs + gn, v);
+}
+
+// Few rows (decode steps): streaming w once is the whole cost, so the
+// matrix cores would idle on 31 of 32 rows.  One workgroup per (column strip,
+// k slab): each lane owns 16 bytes of columns, the 4 waves take interleaved k
+// rows of the slab (8 loads of w in flight per lane), x of the slab is staged
+// in LDS and read as a broadcast, and the waves' sums meet in LDS.  The slab
+// sums go to the partials (fp32 [nsplit][m][n]) for linear_reduce_kernel.
+constexpr int SMALL_M = 8;
+constexpr int SK_MAX = 256;  // k rows per slab, at most
+
+template <typename T, int MR>
+__global__ __launch_bounds__(256) void linear_small_kernel(LinParams p) {
+  constexpr int VE = 16 / (int)sizeof(T);
+  constexpr int COLS = 64 * VE;  // columns per workgroup
+  __shared__ float xs[MR][SK_MAX];
+  __shared__ float red[3][MR][COLS];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int gn = blockIdx.x * COLS + lane * VE;
+  const int kb = blockIdx.y * p.kchunk, ke = min(kb + p.kchunk, p.k);
+  const int nk = ke - kb;
+  const T *X = (const T *)p.x, *W = (const T *)p.w;
+  for (int i = tid; i < MR * nk; i += 256) {
+    const int r = i / nk, kk = i % nk;
+    xs[r][kk] = r < p.m ? Elem<T>::load(X + r * p.x_rs + kb + kk) : 0.f;
+  }
+  __syncthreads();
+  float acc[MR][VE];
+#pragma unroll
+  for (int r = 0; r < MR; ++r)
+#pragma unroll
+    for (int e = 0; e < VE; ++e) acc[r][e] = 0.f;
+  const bool col_ok = gn < p.n;
+  constexpr int U = 8;  // loads in flight per lane
+  for (int k0 = wave; k0 < nk; k0 += 4 * U) {
+    u32x4_t wv[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int kk = k0 + 4 * u;
+      wv[u] = (col_ok && kk < nk) ? *(const u32x4_t *)(W + (kb + kk) * p.w_rs + gn)
+                                  : u32x4_t{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int kk = min(k0 + 4 * u, nk - 1);  // a zero w chunk past the slab adds nothing
+      float wf[VE];
+      if constexpr (sizeof(T) == 4) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) wf[e] = __uint_as_float(wv[u][e]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          wf[2 * e] = __uint_as_float(wv[u][e] << 16);
+          wf[2 * e + 1] = __uint_as_float(wv[u][e] & 0xffff0000u);
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < MR; ++r) {
+        const float xv = xs[r][kk];
+#pragma unroll
+        for (int e = 0; e < VE; ++e) acc[r][e] = fmaf(xv, wf[e], acc[r][e]);
+      }
+    }
+  }
+  if (wave > 0) {
+#pragma unroll
+    for (int r = 0; r < MR; ++r)
+#pragma unroll
+      for (int e = 0; e < VE; ++e) red[wave - 1][r][lane * VE + e] = acc[r][e];
+  }
+  __syncthreads();
+  if (wave > 0 || !col_ok) return;
+#pragma unroll
+  for (int r = 0; r < MR; ++r) {
+    if (r >= p.m) break;
+    float v[VE];
+#pragma unroll
+    for (int e = 0; e < VE; ++e)
+      v[e] = ((acc[r][e] + red[0][r][lane * VE + e]) + red[1][r][lane * VE + e]) + red[2][r][lane * VE + e];
+    float *dst = p.part + ((int64_t)blockIdx.y * p.m + r) * p.n + gn;
+#pragma unroll
+    for (int e = 0; e < VE; e += 4) *(float4 *)(dst + e) = make_float4(v[e], v[e + 1], v[e + 2], v[e + 3]);
+  }
+}
+
+// slabs of the few-rows path: about BN_SMALL_WG workgroups, slabs of
+// 32..SK_MAX rows in multiples of 32
+#ifndef BN_SMALL_WG
+#define BN_SMALL_WG 512
+#endif
+void plan_small(int dtype, int n, int k, int *nsplit, int *kchunk) {
+  const int cols = 64 * (dtype == BN_BF16 ? 8 : 4);
+  const int strips = (n + cols - 1) / cols;
+  const int want = std::max(1, BN_SMALL_WG / strips);
+  int kc = (k + want - 1) / want;
+  kc = std::min(std::max((kc + 31) / 32 * 32, 32), SK_MAX);
+  *kchunk = kc;
+  *nsplit = k > 0 ? (k + kc - 1) / kc : 1;
+}
+
+// k slabs: as many as still fit the grid in one round of resident
+// workgroups (BN_LIN_SLOTS: 4 per compute unit of an MI355X -- 36 KB of LDS
+// each), each slab at least two stages deep.  A fixed device size keeps the
+// plan, and so the workspace size, independent of the device queried.
+#ifndef BN_LIN_SLOTS
+#define BN_LIN_SLOTS 1024
+#endif
+void plan_split(int dtype, int m, int n, int k, int *nsplit, int *kchunk) {
+  const int KT = dtype == BN_BF16 ? LinCfg<bf16_t>::KT : LinCfg<float>::KT;
+  const int64_t tiles = (int64_t)((n + TN - 1) / TN) * ((m + TM - 1) / TM);
+  const int stages = (k + KT - 1) / KT;
+  int ns = (int)std::min<int64_t>(BN_LIN_SLOTS / tiles, std::max(1, stages / 2));
+  ns = std::max(ns, 1);
+  const int per = (stages + ns - 1) / ns;
+  *kchunk = std::max(per, 1) * KT;
+  *nsplit = k > 0 ? (k + *kchunk - 1) / *kchunk : 1;
+}
+
+}  // namespace
+}  // namespace bn
+
+using namespace bn;
+
+// the few-rows path always goes through the partials (its reduction applies
+// the rotation); the tiled path only when it splits k
+static void plan(int dtype, int m, int n, int k, bool *small, int *nsplit, int *kchunk) {
+  *small = m <= SMALL_M && k > 0;
+  if (*small)
+    plan_small(dtype, n, k, nsplit, kchunk);
+  else
+    plan_split(dtype, m, n, k, nsplit, kchunk);
+}
+
+extern "C" size_t bn_linear_rope_workspace_size(int dtype, int m, int n, int k) {
+  if ((dtype != BN_F32 && dtype != BN_BF16) || m <= 0 || n <= 0 || k <= 0) return 0;
+  int ns, kc;
+  bool small;
+  plan(dtype, m, n, k, &small, &ns, &kc);
+  return (small || ns > 1) ? (size_t)ns * m * n * sizeof(float) : 0;
+}
+
+extern "C" int bn_linear_rope(const bn_view *x, const bn_view *w, const bn_view *y, int rope_cols,
+                              int position_offset, int head_dim, float theta, void *workspace,
+                              size_t workspace_bytes, void *stream) {
+  const char *op = "Linear";
+  const unsigned mask = (1u << BN_F32) | (1u << BN_BF16);
+  int st;
+  if ((st = check_view(x, op, "x", mask))) return st;
+  if ((st = check_view(w, op, "w", mask))) return st;
+  if ((st = check_view(y, op, "y", mask))) return st;
+  if (x->dtype != w->dtype || x->dtype != y->dtype)
+    return fail(BN_ERR_UNSUPPORTED, std::string(op) + ": x, w and y must share one dtype");
+  if (x->w != w->h || y->h != x->h || y->w != w->w)
+    return fail(BN_ERR_SHAPE, std::string(op) + ": shape mismatch x:(" + std::to_string(x->h) +
+                                  ", " + std::to_string(x->w) + "), w:(" + std::to_string(w->h) +
+                                  ", " + std::to_string(w->w) + "), y:(" + std::to_string(y->h) +
+                                  ", " + std::to_string(y->w) + ")");
+  RopeFreqs fr{};
+  if (rope_cols != 0) {
+    if ((st = make_rope_freqs(op, head_dim, theta, &fr))) return st;
+    if (rope_cols < 0 || rope_cols > y->w || rope_cols % head_dim != 0)
+      return fail(BN_ERR_SHAPE, std::string(op) +
+                                    ": rope_cols must be a multiple of head_dim within the output width");
+  }
+  const int dt = x->dtype;
+  const int64_t ve = dt == BN_BF16 ? 8 : 4;  // elements per 16 bytes
+  const size_t es = dtype_size(dt);
+  // views with no elements (k = 0) are never read: their layout is free
+  auto ok = [&](const bn_view *v) {
+    if ((int64_t)v->h * v->w == 0) return true;
+    return v->stride_w == 1 && v->stride_h % ve == 0 &&
+           ((reinterpret_cast<uintptr_t>(v->data) + (uintptr_t)(v->offset * (int64_t)es)) & 15u) == 0;
+  };
+  auto unit = [](const bn_view *v) { return (int64_t)v->h * v->w == 0 || v->stride_w == 1; };
+  if (!unit(x) || !unit(w) || !unit(y))
+    return fail(BN_ERR_UNSUPPORTED, std::string(op) + ": rows must be contiguous (stride_w == 1)");
+  if (!ok(x) || !ok(w) || !ok(y) || x->w % ve || y->w % ve)
+    return fail(BN_ERR_UNSUPPORTED, std::string(op) +
+                                        ": rows must start 16-byte aligned and widths be multiples of 16 bytes");
+  if ((st = require_device(op, {x, w, y}))) return st;
+  if (y->h == 0 || y->w == 0) return BN_OK;
+  const int m = y->h, n = y->w, k = x->w;
+  int nsplit, kchunk;
+  bool small;
+  plan(dt, m, n, k, &small, &nsplit, &kchunk);
+  const size_t need = (small || nsplit > 1) ? (size_t)nsplit * m * n * sizeof(float) : 0;
+  if (workspace && workspace_bytes < need)
+    return fail(BN_ERR_INVALID_ARG, std::string(op) + ": workspace of " +
+                                        std::to_string(workspace_bytes) + " bytes, need " +
+                                        std::to_string(need));
+  if (workspace && (reinterpret_cast<uintptr_t>(workspace) & 15u))
+    return fail(BN_ERR_UNSUPPORTED, std::string(op) + ": workspace must be 16-byte aligned");
+  if ((st = ensure_device())) return st;
+  hipStream_t s = as_stream(stream);
+  void *ws = workspace;
+  bool own = false;
+  if (need && !ws) {
+    if ((st = bn_alloc(&ws, need, stream))) return st;
+    own = true;
+  }
+  LinParams p;
+  p.x = (const char *)x->data + x->offset * (int64_t)es;
+  p.w = (const char *)w->data + w->offset * (int64_t)es;
+  p.y = (char *)y->data + y->offset * (int64_t)es;
+  p.part = need ? (float *)ws : nullptr;
+  p.x_rs = x->stride_h; p.w_rs = w->stride_h; p.y_rs = y->stride_h;
+  p.m = m; p.n = n; p.k = k; p.kchunk = kchunk;
+  p.rope_cols = rope_cols; p.head_dim = rope_cols ? head_dim : 2; p.pos0 = position_offset;
+  if (small) {
+    const int cols = 64 * (dt == BN_BF16 ? 8 : 4);
+    dim3 grid((unsigned)((n + cols - 1) / cols), (unsigned)nsplit);
+#define BN_SMALL(T, MR) hipLaunchKernelGGL((linear_small_kernel<T, MR>), grid, dim3(256), 0, s, p)
+    if (dt == BN_F32) {
+      if (m <= 1) BN_SMALL(float, 1);
+      else if (m <= 2) BN_SMALL(float, 2);
+      else if (m <= 4) BN_SMALL(float, 4);
+      else BN_SMALL(float, 8);
+    } else {
+      if (m <= 1) BN_SMALL(bf16_t, 1);
+      else if (m <= 2) BN_SMALL(bf16_t, 2);
+      else if (m <= 4) BN_SMALL(bf16_t, 4);
+      else BN_SMALL(bf16_t, 8);
+    }
+#undef BN_SMALL
+  } else {
+    dim3 grid((unsigned)((n + TN - 1) / TN), (unsigned)((m + TM - 1) / TM), (unsigned)nsplit);
+    if (dt == BN_F32)
+      hipLaunchKernelGGL(linear_kernel<float>, grid, dim3(256), 0, s, p, fr);
+    else
+      hipLaunchKernelGGL(linear_kernel<bf16_t>, grid, dim3(256), 0, s, p, fr);
+  }
+  hipError_t e = hipGetLastError();
+  if (e == hipSuccess && need) {
+    const int64_t th = (int64_t)m * (n / 4);
+    const dim3 rg((unsigned)((th + 255) / 256));
+    if (dt == BN_F32)
+      hipLaunchKernelGGL(linear_reduce_kernel<float>, rg, dim3(256), 0, s, p, fr, nsplit);
+    else
+      hipLaunchKernelGGL(linear_reduce_kernel<bf16_t>, rg, dim3(256), 0, s, p, fr, nsplit);
+    e = hipGetLastError();
+  }
+  st = e == hipSuccess ? BN_OK : hip_fail(e, __FILE__, __LINE__);
+  if (own) {
+    const int st2 = bn_free(ws, stream);
+    if (st == BN_OK) st = st2;
+  }
+  return st;
+}

@@ -16,12 +16,14 @@ kernel.  Per-head GQA semantics (query head h reads KV head h // 8).
 RMSNorm (plain and fused with the residual add), RoPE, prefill attention,
 decode attention and the SwiGLU activation run on the HIP kernels through the
 C ABI (bnhip).  The Q, K and V projections are one GEMM against the
-concatenated weight [hidden, (H + 2*Hkv)*64]; RoPE rotates the Q and K columns
-of its output in place in one launch (same positions for every head block),
-and attention reads Q, K and V as column slices of that row.  The dense
-projections and the embedding gather are plain torch GPU operations (library
-GEMMs): they are not part of the attention path, and the config's metric
-times only the attention, RoPE and RMSNorm kernels.  ``path_ms`` accumulates hip-event time around those
+concatenated weight [hidden, (H + 2*Hkv)*64]; attention reads Q, K and V as
+column slices of its output.  Decode steps (rows <= SMALL_ROWS) run every
+projection -- QKV, O, the concatenated gate/up, down and lm_head -- on
+bn_linear_rope's few-rows kernel, with the Q/K rotation fused into the QKV
+projection; the prompt runs the library GEMM (torch) and rotates the Q and K
+columns in place in one bn_rope launch.  The embedding gather is a torch GPU
+operation.  The config's metric times the attention, RoPE (standalone or
+fused into the decode QKV projection) and RMSNorm kernels.  ``path_ms`` accumulates hip-event time around those
 kernel launches (an upper bound on their device time; the rocprofv3 kernel
 trace gives the exact per-kernel durations).
 """
@@ -53,6 +55,13 @@ class TinyLlamaConfig:
 
 
 class TinyLlama:
+    # Rows up to which the projections run on bn_linear_rope's few-rows kernel
+    # (one pass over the weights, the QKV rotation fused into its reduction).
+    # Longer prompts take the library GEMM and a separate RoPE launch: at 512
+    # rows hipBLASLt's fp32 GEMM plus bn_rope (45 + 4 us) beats the hand-written
+    # tiled kernel (66 us).
+    SMALL_ROWS = 8
+
     def __init__(self, cfg: TinyLlamaConfig, max_len: int, seed: int = 1, std: float = 0.02,
                  dtype=torch.float32):
         if dtype != torch.float32:
@@ -69,9 +78,11 @@ class TinyLlama:
         self.layers = []
         for _ in range(cfg.num_hidden_layers):
             wq, wk, wv = w(h, h), w(h, kv), w(h, kv)
+            wo = w(h, h)
+            wg, wu = w(h, inter), w(h, inter)
             self.layers.append(dict(
                 ln1=torch.ones((1, h), device="cuda"), wqkv=torch.cat([wq, wk, wv], dim=1),
-                wo=w(h, h), ln2=torch.ones((1, h), device="cuda"), wg=w(h, inter), wu=w(h, inter),
+                wo=wo, ln2=torch.ones((1, h), device="cuda"), wgu=torch.cat([wg, wu], dim=1),
                 wd=w(inter, h),
                 k_cache=torch.zeros((1, max_len, cfg.num_key_value_heads, cfg.head_dim), device="cuda"),
                 v_cache=torch.zeros((1, max_len, cfg.num_key_value_heads, cfg.head_dim), device="cuda")))
@@ -79,6 +90,10 @@ class TinyLlama:
         self.lm_head = w(h, cfg.vocab_size)
         self.length = 0
         self.ws = bnhip.decode_workspace(1, max_len, cfg.num_attention_heads, cfg.head_dim)
+        # few-rows projections (decode steps): split-k partial sums of the largest one
+        shapes = [(h, h + 2 * kv), (h, h), (h, 2 * inter), (inter, h), (h, cfg.vocab_size)]
+        n_ws = max(bnhip.lib().bn_linear_rope_workspace_size(0, self.SMALL_ROWS, n, k) for k, n in shapes)
+        self.lin_ws = torch.empty(max(n_ws // 4, 1), device="cuda")
         self.path_ms = 0.0
         self.timing = False
         self.trace = None  # list of (kernel, inputs, output) when set
@@ -143,6 +158,23 @@ class TinyLlama:
                      head_dim=self.cfg.head_dim, theta=self.cfg.rope_theta)
         return x
 
+    def linear(self, x, w, rope_cols=0, pos0=0):
+        """x @ w on the few-rows projection kernel; RoPE at positions pos0.. on
+        the first rope_cols columns (the Q and K heads of the fused QKV)."""
+        y = torch.empty((x.shape[0], w.shape[1]), device="cuda")
+
+        def run():
+            bnhip.linear_rope(x, w, y, rope_cols=rope_cols, position_offset=pos0,
+                              head_dim=self.cfg.head_dim, theta=self.cfg.rope_theta,
+                              workspace=self.lin_ws)
+        if rope_cols:
+            self._timed(run)  # carries the RoPE of the step
+            self._record("linear_rope", [x, w], y, rope_cols=rope_cols, offset=pos0,
+                         head_dim=self.cfg.head_dim, theta=self.cfg.rope_theta)
+        else:
+            run()
+        return y
+
     def prefill_attention(self, q, k, v):
         cfg = self.cfg
         S = q.shape[0]
@@ -170,8 +202,12 @@ class TinyLlama:
         cfg = self.cfg
         n = x.shape[0]
         hq, hk = cfg.hidden_size, cfg.num_key_value_heads * cfg.head_dim
-        qkv = x @ L["wqkv"]                       # [n, hq + 2*hk]
-        self.rope_(qkv[:, :hq + hk], pos0)        # Q and K columns, one launch
+        few = n <= self.SMALL_ROWS
+        if few:                                   # [n, hq + 2*hk], Q and K rotated
+            qkv = self.linear(x, L["wqkv"], hq + hk, pos0)
+        else:
+            qkv = x @ L["wqkv"]
+            self.rope_(qkv[:, :hq + hk], pos0)    # Q and K columns, one launch
         q, k, v = qkv[:, :hq], qkv[:, hq:hq + hk], qkv[:, hq + hk:]
         L["k_cache"][0, pos0:pos0 + n] = k.view(n, cfg.num_key_value_heads, cfg.head_dim)
         L["v_cache"][0, pos0:pos0 + n] = v.view(n, cfg.num_key_value_heads, cfg.head_dim)
@@ -179,7 +215,7 @@ class TinyLlama:
             o = self.prefill_attention(q, k, v)
         else:
             o = self.decode_attention(q, L, pos0 + 1)
-        return o @ L["wo"]
+        return self.linear(o, L["wo"]) if few else o @ L["wo"]
 
     def _forward(self, hdn, pos0):
         """Decoder layers over rows hdn (positions pos0..); returns the final
@@ -188,7 +224,13 @@ class TinyLlama:
         x = self.rmsnorm(hdn, self.layers[0]["ln1"])
         for i, L in enumerate(self.layers):
             hdn, x = self.add_rmsnorm(hdn, self._attention(x, L, pos0), L["ln2"])
-            mlp = self.silu_mul(x @ L["wg"], x @ L["wu"]) @ L["wd"]
+            inter = self.cfg.intermediate_size
+            if x.shape[0] <= self.SMALL_ROWS:
+                gu = self.linear(x, L["wgu"])
+                mlp = self.linear(self.silu_mul(gu[:, :inter], gu[:, inter:]), L["wd"])
+            else:
+                gu = x @ L["wgu"]
+                mlp = self.silu_mul(gu[:, :inter], gu[:, inter:]) @ L["wd"]
             nxt = self.layers[i + 1]["ln1"] if i + 1 < len(self.layers) else self.ln_f
             hdn, x = self.add_rmsnorm(hdn, mlp, nxt)
         return x
@@ -205,7 +247,7 @@ class TinyLlama:
         assert self.length < self.max_len
         xf = self._forward(self.embed[token.view(1)], self.length)
         self.length += 1
-        return xf @ self.lm_head
+        return self.linear(xf, self.lm_head)
 
     def generate(self, ids: torch.Tensor, new_tokens: int, time_path: bool = False):
         """Greedy decode; returns the generated ids and the path-kernel ms."""

@@ -16,6 +16,8 @@ Also measured in the same run and reported as sub-objects:
   prefill_long  config 5's prefill, B=1, S=16384, bf16
   add_rmsnorm   fused residual add + RMSNorm, bf16 [16384, 2048], GB/s
   silu_mul      SwiGLU activation, bf16 [16384, 5632], GB/s
+  linear_rope   config 4's fused QKV projection with RoPE in the epilogue, fp32:
+                prompt (M=512, TFLOP/s) and decode step (M=1, GB/s of weights)
   prefill_backward  config 2's flash-style backward (dQ, dK, dV), bf16,
                 TFLOP/s of 2.5x the forward's algorithmic flops
 Each carries a ``roofline`` object priced against MI355X peaks (bf16 MFMA
@@ -146,6 +148,49 @@ def bench_backward(steps, warmup, seed=5):
     return {"value": round(tflops, 3), "unit": "TFLOP/s", "ms_per_launch": round(ms, 5),
             "flops_per_launch": fl, "config": "config 2 backward, bf16",
             "roofline": roofline("mfma", tflops, PEAK_BF16_TFLOPS, "TFLOP/s")}
+
+
+def bench_linear(steps, warmup, seed=6):
+    """Config 4's fused QKV projection with RoPE on its Q/K columns, fp32:
+    x [M, 2048] @ w [2048, 2560], rope_cols 2304, for the prompt (M = 512,
+    MFMA-bound, flops 2*M*K*N) and a decode step (M = 1, HBM-bound on w,
+    bytes K*N*4 + x + y).  Beside it, the unfused path it replaces: torch's
+    library GEMM (x @ w) followed by bn_rope on the Q/K columns."""
+    import torch
+    import bnhip
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    K, N, RC = 2048, 2560, 2304
+    w = torch.randn((K, N), generator=g, device="cuda") / 45.0
+    out = {}
+    for M in (512, 1):
+        x = torch.randn((M, K), generator=g, device="cuda")
+        y = torch.empty((M, N), device="cuda")
+        ws = torch.empty(max(bnhip.lib().bn_linear_rope_workspace_size(0, M, N, K) // 4, 1),
+                         device="cuda")
+        ms = time_launches(lambda i: bnhip.linear_rope(x, w, y, rope_cols=RC, position_offset=7,
+                                                       workspace=ws), steps, warmup)
+        yt = torch.empty((M, N), device="cuda")
+
+        def unfused(i):
+            torch.matmul(x, w, out=yt)
+            q = yt[:, :RC]
+            bnhip.call("bn_rope", bnhip.C.byref(bnhip.view(q)), bnhip.C.byref(bnhip.view(q)), 7, 64,
+                       1e4, bnhip.stream_of())
+        ms_ref = time_launches(unfused, steps, warmup)
+        fl = 2 * M * K * N
+        byt = 4 * (K * N + M * K + M * N)
+        if M > 1:
+            v = fl / (ms * 1e-3) / 1e12
+            out["prompt"] = {"value": round(v, 3), "unit": "TFLOP/s", "ms_per_launch": round(ms, 5),
+                             "m": M, "unfused_ms": round(ms_ref, 5),
+                             "roofline": roofline("mfma", v, PEAK_FP32_TFLOPS, "TFLOP/s")}
+        else:
+            v = byt / (ms * 1e-3) / 1e9
+            out["decode_step"] = {"value": round(v, 1), "unit": "GB/s", "ms_per_launch": round(ms, 5),
+                                  "m": M, "unfused_ms": round(ms_ref, 5),
+                                  "roofline": roofline("hbm", v, PEAK_HBM_GBS, "GB/s")}
+    out["config"] = "config 4 QKV projection + RoPE, fp32, K=2048, N=2560, rope_cols=2304"
+    return out
 
 
 def bench_decode(ragged, steps, warmup, seed=2):
@@ -334,8 +379,9 @@ def bench_tinyllama(prompt=512, new_tokens=128, cpu=True, warmup_tokens=2):
     wall = time.perf_counter() - t0
     res = {"prompt": prompt, "new_tokens": new_tokens, "wall_s": round(wall, 3),
            "path_ms": round(path_ms, 3),
-           "path_kernels": "RMSNorm (plain and fused with the residual add), RoPE, GQA prefill, "
-                           "GQA decode (fp32)",
+           "path_kernels": "RMSNorm (plain and fused with the residual add), RoPE (prompt: "
+                           "bn_rope; decode steps: fused into the QKV projection kernel), GQA "
+                           "prefill, GQA decode (fp32)",
            "first_tokens": [int(t) for t in toks[:8].cpu()], "cache_length_end": m.length}
     if cpu:
         res["cpu_baseline"] = cpu_baseline_tinyllama(m, ids)
@@ -425,7 +471,7 @@ def main():
                          "so a kernel trace holds exactly one prefill + 128 steps)")
     ap.add_argument("--only", default="",
                     help="comma list of extra workloads (default: all but copy): "
-                         "decode,ragged,fp32,norm,long,addnorm,swiglu,bwd,block,tinyllama,copy; "
+                         "decode,ragged,fp32,norm,long,addnorm,swiglu,linear,bwd,block,tinyllama,copy; "
                          "'head' = headline prefill only")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -475,6 +521,9 @@ def main():
     if want("swiglu"):
         out["silu_mul"] = bench_silu_mul(K, W)
         print(f"silu_mul: {out['silu_mul']['value']} GB/s", file=sys.stderr, flush=True)
+    if want("linear"):
+        out["linear_rope"] = bench_linear(K, W)
+        print(f"linear_rope: {out['linear_rope']}", file=sys.stderr, flush=True)
     if want("bwd"):
         out["prefill_backward"] = bench_backward(K, W)
         print(f"prefill backward: {out['prefill_backward']['value']} TFLOP/s "

@@ -135,6 +135,22 @@ int bn_softmax_backward(const bn_view *y, const bn_view *dy, const bn_view *dx,
                         void *stream);
 /* op_mm (src/ops/op_mm.cuh:39-57): c = a @ b, fp32, any strides. */
 int bn_matmul(const bn_view *a, const bn_view *b, const bn_view *c, void *stream);
+/* Projection with RoPE in the epilogue: y = x @ w (x [M, K], w [K, N],
+ * y [M, N], one dtype, BN_F32 or BN_BF16; rows contiguous and 16-byte
+ * aligned, K and N multiples of 16 bytes), then op_rope's rotation (adjacent
+ * pairs, freq = 1/theta^(2p/head_dim), position = position_offset + row) on
+ * columns [0, rope_cols), a multiple of head_dim (0: no rotation).  Replaces
+ * op_mm for the Q, K and V projections followed by op_rope on Q and K
+ * (llama_layers.hpp:72-81) -- one call on the concatenated weight
+ * [hidden, (H + 2*Hkv)*head_dim] with rope_cols = (H + Hkv)*head_dim -- and
+ * op_mm for the output projection (:112, rope_cols = 0).  fp32 accumulation;
+ * y must not overlap x or w.  Split-k partial sums take
+ * bn_linear_rope_workspace_size(dtype, M, N, K) bytes of workspace (16-byte
+ * aligned; NULL: the pool supplies them). */
+size_t bn_linear_rope_workspace_size(int dtype, int m, int n, int k);
+int bn_linear_rope(const bn_view *x, const bn_view *w, const bn_view *y,
+                   int rope_cols, int position_offset, int head_dim, float theta,
+                   void *workspace, size_t workspace_bytes, void *stream);
 /* repeat_kv (src/llama/llama_layers.hpp:131-175, llama_layers.py:105-138):
  * out column block kv_h*n_rep + r = kv column block kv_h, on the device. */
 int bn_repeat_kv(const bn_view *kv, const bn_view *out, int head_dim, int n_rep,

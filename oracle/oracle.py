@@ -170,6 +170,18 @@ def matmul(a, b):
     return c
 
 
+def linear_rope(x, w, rope_cols=0, position_offset=0, head_dim=64, theta=10000.0):
+    """The Q/K/V projection followed by RoPE on its Q and K columns
+    (llama_layers.hpp:72-81): y = x @ w -- op_mm (op_mm.cuh:23-36), here in
+    fp64 and rounded to float32 -- then op_rope (or_rope, op_rope.cuh:55-99)
+    on columns [0, rope_cols) at position position_offset + row.  Returns
+    float32 [M, N]."""
+    y = (np.asarray(x, np.float64) @ np.asarray(w, np.float64)).astype(np.float32)
+    if rope_cols:
+        y[:, :rope_cols] = rope(y[:, :rope_cols], position_offset, head_dim, theta)
+    return y
+
+
 def matmul_views(a: OrView, b: OrView, c: OrView):
     lib().or_matmul(a, b, c)
 

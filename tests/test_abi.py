@@ -202,3 +202,39 @@ def test_prefill_lse_validation():
     assert s == B.BN_ERR_INVALID_ARG and m.startswith("GQA prefill:")
     s, m = st("bn_gqa_prefill_lse", *args[:5], 0x6002, *args[5:])
     assert s == B.BN_ERR_UNSUPPORTED
+
+
+def test_linear_rope_validation():
+    F, H = B.BN_F32, B.BN_BF16
+    ok = (V(4, 64), V(64, 128), V(4, 128))
+    s, m = st("bn_linear_rope", V(4, 64), V(32, 128), V(4, 128), 0, 0, 64, 1e4, None, 0, None)
+    assert s == B.BN_ERR_SHAPE and m.startswith("Linear: shape mismatch")
+    s, m = st("bn_linear_rope", V(4, 64), V(64, 128, dtype=H), V(4, 128), 0, 0, 64, 1e4, None, 0, None)
+    assert s == B.BN_ERR_UNSUPPORTED and "one dtype" in m
+    s, m = st("bn_linear_rope", *ok, 96, 0, 64, 1e4, None, 0, None)
+    assert s == B.BN_ERR_SHAPE and "rope_cols" in m
+    s, m = st("bn_linear_rope", *ok, 256, 0, 64, 1e4, None, 0, None)
+    assert s == B.BN_ERR_SHAPE
+    s, m = st("bn_linear_rope", *ok, 64, 0, 63, 1e4, None, 0, None)
+    assert s == B.BN_ERR_SHAPE and "head_dim" in m
+    s, m = st("bn_linear_rope", V(4, 64, stride_w=2, stride_h=128), V(64, 128), V(4, 128), 0, 0, 64,
+              1e4, None, 0, None)
+    assert s == B.BN_ERR_UNSUPPORTED and "contiguous" in m
+    s, m = st("bn_linear_rope", V(4, 66), V(66, 128), V(4, 128), 0, 0, 64, 1e4, None, 0, None)
+    assert s == B.BN_ERR_UNSUPPORTED  # k not a multiple of 16 bytes
+    s, m = st("bn_linear_rope", *ok, 64, 0, 64, 1e4, None, 0, None)
+    assert s == B.BN_ERR_NOT_DEVICE and m == "Linear: only GPU implementation available"
+
+
+def test_linear_rope_workspace_size():
+    L = B.lib()
+    # config 4 decode step (few rows): 10 strips of 256 columns x 32 slabs of 64 rows
+    assert L.bn_linear_rope_workspace_size(B.BN_F32, 1, 2560, 2048) == 32 * 2560 * 4
+    # bf16: 5 strips of 512 columns x 64 slabs of 32 rows
+    assert L.bn_linear_rope_workspace_size(B.BN_BF16, 4, 2560, 2048) == 64 * 4 * 2560 * 4
+    # 512 rows: 320 tiles, k split three ways (960 workgroups fit 1024 slots)
+    assert L.bn_linear_rope_workspace_size(B.BN_F32, 512, 2560, 2048) == 3 * 512 * 2560 * 4
+    assert L.bn_linear_rope_workspace_size(B.BN_BF16, 512, 2560, 2048) == 3 * 512 * 2560 * 4
+    # enough tiles: no split
+    assert L.bn_linear_rope_workspace_size(B.BN_F32, 4096, 4096, 2048) == 0
+    assert L.bn_linear_rope_workspace_size(B.BN_U32, 4, 4, 4) == 0

@@ -68,9 +68,9 @@ def small_llama(layers=2, vocab=512, max_len=96):
 
 
 def test_tinyllama_kernels_teacher_forced():
-    """Every RMSNorm (plain and fused with the residual add) / RoPE / prefill /
-    decode launch of a 2-layer run is recomputed by the oracle from the inputs
-    the GPU used."""
+    """Every RMSNorm (plain and fused with the residual add) / RoPE / QKV
+    projection with fused RoPE (decode steps) / prefill / decode launch of a
+    2-layer run is recomputed by the oracle from the inputs the GPU used."""
     m = small_llama()
     m.trace = []
     ids = torch.from_numpy(np.random.default_rng(3).integers(0, 512, 64)).cuda()
@@ -84,13 +84,16 @@ def test_tinyllama_kernels_teacher_forced():
             ref = np.stack(O.add_rmsnorm(ins[0], ins[1], ins[2], kw["eps"]))
         elif name == "rope":
             ref = O.rope(ins[0], kw["offset"], kw["head_dim"], kw["theta"])
+        elif name == "linear_rope":
+            ref = O.linear_rope(ins[0], ins[1], kw["rope_cols"], kw["offset"], kw["head_dim"],
+                                kw["theta"])
         elif name == "prefill":
             ref = O.gqa_prefill(ins[0], ins[1], ins[2], 0.125, True, 0)
         else:
             q, kc, vc = ins
             ref = O.gqa_decode(q, kc, vc, np.array([kw["length"]], np.int32), 0.125)
         assert_close(out, ref, FP32_TOL, f"{name} {kw}")
-    assert seen == {"rmsnorm", "add_rmsnorm", "rope", "prefill", "decode"}
+    assert seen == {"rmsnorm", "add_rmsnorm", "rope", "linear_rope", "prefill", "decode"}
 
 
 def test_tinyllama_cache_matches_recompute():

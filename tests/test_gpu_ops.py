@@ -305,3 +305,68 @@ def test_pool_stream_ordered_alloc_free():
     B.call("bn_pool_set_limit", 0)
     B.call("bn_alloc", C.byref(p), 4096, None)
     B.call("bn_free", p, None)
+
+
+# ------------------------------------------------- projection + RoPE epilogue
+LINEAR_CASES = [
+    # M, K, N, rope_cols, position_offset
+    (1, 2048, 2560, 2304, 37),      # config 4 decode step: fused QKV, split k
+    (512, 2048, 2560, 2304, 0),     # config 4 prompt: fused QKV
+    (512, 2048, 2048, 0, 0),        # output projection, no rotation
+    (130, 72, 264, 128, 5),         # ragged rows, k not a multiple of the stage
+    (3, 40, 200, 64, 1000),         # tiny, far position
+    (64, 256, 512, 512, 3),         # every column rotated
+    (2, 512, 512, 256, 3),          # few-rows path, 2 rows
+    (5, 2048, 2560, 2304, 100),     # few-rows path, 8-row variant
+    (8, 64, 128, 64, 0),            # few-rows path, one slab
+    (9, 96, 264, 128, 1),           # first row count on the tiled path
+]
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("case", LINEAR_CASES)
+def test_linear_rope(case, dtype):
+    M, K, N, rc, off = case
+    r = rng(60)
+    x = r.standard_normal((M, K)).astype(np.float32)
+    w = (r.standard_normal((K, N)) / np.sqrt(K)).astype(np.float32)
+    if dtype == "bf16":
+        x, w = bf16_round(x), bf16_round(w)
+    td = torch.float32 if dtype == "f32" else torch.bfloat16
+    y = B.linear_rope(dev(x, td), dev(w, td), rope_cols=rc, position_offset=off)
+    ref = O.linear_rope(x, w, rc, off, 64, 1e4)
+    assert_close(host(y), ref, FP32_TOL if dtype == "f32" else BF16_TOL, f"linear {case} {dtype}")
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_linear_rope_strided_views_and_workspace(dtype):
+    # x a column slice of a wider buffer, w the Q/K part of a fused weight,
+    # y written into a column slice; a caller workspace gives the pool's bits
+    td = torch.float32 if dtype == "f32" else torch.bfloat16
+    r = rng(61)
+    xb = r.standard_normal((9, 288)).astype(np.float32)
+    wb = (r.standard_normal((256, 400)) / 16).astype(np.float32)
+    if dtype == "bf16":
+        xb, wb = bf16_round(xb), bf16_round(wb)
+    xt, wt = dev(xb, td), dev(wb, td)
+    x, w = xt[:, 16:272], wt[:, :320]
+    yb = torch.full((9, 400), 7.0, dtype=td, device="cuda")
+    y = yb[:, 40:360]
+    B.linear_rope(x, w, y, rope_cols=256, position_offset=11)
+    ref = O.linear_rope(xb[:, 16:272], wb[:, :320], 256, 11, 64, 1e4)
+    got = host(yb)
+    assert_close(got[:, 40:360], ref, FP32_TOL if dtype == "f32" else BF16_TOL, "strided")
+    assert np.all(got[:, :40] == 7.0) and np.all(got[:, 360:] == 7.0)
+    dt = B.BN_F32 if dtype == "f32" else B.BN_BF16
+    n = B.lib().bn_linear_rope_workspace_size(dt, 9, 320, 256)
+    assert n > 0  # 5 x 1 tiles: k is split
+    ws = torch.empty(n // 4, dtype=torch.float32, device="cuda")
+    y2 = B.linear_rope(x, w, rope_cols=256, position_offset=11, workspace=ws)
+    assert torch.equal(y2, y)
+
+
+def test_linear_rope_empty_k_gives_zeros():
+    x = torch.empty((5, 0), device="cuda")
+    w = torch.empty((0, 64), device="cuda")
+    y = B.linear_rope(x, w, rope_cols=64, position_offset=3)
+    assert torch.count_nonzero(y).item() == 0

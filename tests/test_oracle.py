@@ -493,3 +493,28 @@ def test_backward_from_residuals_equals_chain_form(B, Sq, Skv, H, Hkv, causal, o
         assert relerr(a, b_) < 1e-6
     wrong = O.gqa_prefill_backward_from_residuals(q, k, v, o, lse / math.log(2), do, 0.125, causal, off)
     assert relerr(wrong[0], chain[0]) > 0.05
+
+
+# ---------------------------------------------------- projection + RoPE
+def test_linear_rope_pins():
+    """Without rotation it is op_mm's product; the rotation is the identity at
+    position 0, keeps every pair's norm, is undone by the pinned RoPE backward
+    (the transpose rotation), and leaves columns past rope_cols alone."""
+    r = rng(45)
+    x = r.standard_normal((6, 40)).astype(np.float32)
+    w = r.standard_normal((40, 192)).astype(np.float32)
+    plain = O.linear_rope(x, w)
+    assert relerr(plain, O.matmul(x, w)) < 1e-5
+    y = O.linear_rope(x, w, 128, 0, 64, 1e4)
+    assert np.allclose(y[0], plain[0], rtol=1e-6, atol=1e-6)          # row 0: angle 0
+    assert np.array_equal(y[:, 128:], plain[:, 128:])
+    n_y = np.hypot(y[:, :128:2], y[:, 1:128:2])
+    n_p = np.hypot(plain[:, :128:2], plain[:, 1:128:2])
+    assert np.allclose(n_y, n_p, rtol=1e-5)
+    y7 = O.linear_rope(x, w, 128, 7, 64, 1e4)
+    back = O.rope_backward(y7[:, :128], 7, 64, 1e4)
+    assert relerr(back, plain[:, :128]) < 1e-5
+    # a planted slip: rotating the V columns too moves them
+    wrong = plain.copy()
+    wrong[:, :] = O.rope(plain, 7, 64, 1e4)
+    assert relerr(wrong[:, 128:], y7[:, 128:]) > 1e-2
