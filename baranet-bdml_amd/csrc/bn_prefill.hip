@@ -166,6 +166,32 @@ __device__ __forceinline__ Work decode_work_xcd(const PrefillParams &p) {
   return w;
 }
 
+// Head-packed work items (bf16, group = 4*RT): one workgroup per (batch, KV
+// head, 32 query rows) covering all the group's query heads, wave w on heads
+// RT*w .. RT*w + RT-1 of the group.  Every wave then sees the same causal key
+// range -- no wave idles in the diagonal blocks -- and only the last 32-key
+// tile of the range needs a mask.  Row tiles heaviest first; the workgroups of
+// one (batch, KV head) share an XCD when batch*n_kv is a multiple of 8.
+__device__ __forceinline__ Work decode_work_packed(const PrefillParams &p) {
+  const int n_kv = p.n_heads / p.group;
+  const int NG = p.batch * n_kv;
+  const int L = blockIdx.x;
+  Work w;
+  int gi;
+  if (NG % 8 == 0) {
+    const int x = L & 7, j = L >> 3, per_mt = NG >> 3;
+    w.mt = p.n_mt - 1 - j / per_mt;
+    gi = (j % per_mt) * 8 + x;
+  } else {
+    w.mt = p.n_mt - 1 - L / NG;
+    gi = L % NG;
+  }
+  w.b = gi / n_kv;
+  w.g = gi % n_kv;
+  w.h = w.g * p.group;  // first head of the group
+  return w;
+}
+
 // Kernel structure -- the softmax does little VALU work per score and runs
 // while the matrix cores work:
 //   * the fast path is p = exp2(s * c - m * c), c = scale*log2(e), against a
@@ -202,32 +228,36 @@ constexpr float kSumLimit = 65536.f;
 #define BN_PIPE_V1 5  // VALU instructions after each MFMA
 #endif
 
-template <int RT, int OCC>
+template <int RT, int OCC, bool HP>
 __global__ __launch_bounds__(256, OCC) void prefill_bf16_kernel(PrefillParams p) {
   __shared__ __attribute__((aligned(16))) bf16_t smem[2 * KBUF + 2 * VBUF];
   bf16_t *const kring = smem;
   bf16_t *const vring = smem + 2 * KBUF;
-  constexpr int WROWS = 32 * RT, WGROWS = 4 * WROWS;
+  // rows per wave / per workgroup of one head; head-packed: 32 rows of RT heads
+  constexpr int WROWS = HP ? 32 : 32 * RT, WGROWS = HP ? 32 : 4 * WROWS;
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r32 = lane & 31, hf = lane >> 5;
-  const Work w = decode_work_xcd(p);
+  const Work w = HP ? decode_work_packed(p) : decode_work_xcd(p);
   const bf16_t *Q = (const bf16_t *)p.q + w.b * p.q_bs + (int64_t)w.h * HD;
   const bf16_t *K = (const bf16_t *)p.k + w.b * p.kv_bs + (int64_t)w.g * HD;
   const bf16_t *V = (const bf16_t *)p.v + w.b * p.kv_bs + (int64_t)w.g * HD;
   bf16_t *O = (bf16_t *)p.o + w.b * p.o_bs + (int64_t)w.h * HD;
   const float c = p.c;
 
-  const int q_wave0 = w.mt * WGROWS + wave * WROWS;
+  const int q_wave0 = w.mt * WGROWS + (HP ? 0 : wave * WROWS);
+  // row tile rt: rows q_wave0 + row_step*rt .., head w.h + head_of(rt)
+  constexpr int row_step = HP ? 0 : 32;
+  auto head_of = [&](int rt) { return HP ? RT * wave + rt : 0; };
 
   // Q^T operands: lane holds Q[row][16t + 8hf .. +7], t = 0..3
   bf16x8_t qreg[RT][4];
   int qlimit[RT];
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
-    const int qrow = q_wave0 + 32 * rt + r32;
-    const bf16_t *qp = Q + (int64_t)min(qrow, p.seq_q - 1) * p.q_rs + 8 * hf;
+    const int qrow = q_wave0 + row_step * rt + r32;
+    const bf16_t *qp = Q + (int64_t)head_of(rt) * HD + (int64_t)min(qrow, p.seq_q - 1) * p.q_rs + 8 * hf;
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
       qreg[rt][t] = *(const bf16x8_t *)(qp + 16 * t);
@@ -491,13 +521,13 @@ __global__ __launch_bounds__(256, OCC) void prefill_bf16_kernel(PrefillParams p)
 
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
-    const int qrow = q_wave0 + 32 * rt + r32;
+    const int qrow = q_wave0 + row_step * rt + r32;
     const float lt = l[rt] + __shfl_xor(l[rt], 32, 64);
     const float inv = lt > 0.f ? 1.0f / lt : 0.f;  // no visible key -> zeros
     if (p.lse && hf == 0 && qrow < p.seq_q)
-      p.lse[((int64_t)w.b * p.n_heads + w.h) * p.seq_q + qrow] = row_lse(m[rt], lt, c);
+      p.lse[((int64_t)w.b * p.n_heads + w.h + head_of(rt)) * p.seq_q + qrow] = row_lse(m[rt], lt, c);
     if (qrow < p.seq_q) {
-      bf16_t *orow = O + (int64_t)qrow * p.o_rs;
+      bf16_t *orow = O + (int64_t)head_of(rt) * HD + (int64_t)qrow * p.o_rs;
 #pragma unroll
       for (int dt = 0; dt < 2; ++dt)
 #pragma unroll
@@ -692,9 +722,16 @@ static int prefill_impl(int dtype, const void *q, const void *k, const void *v, 
 #define BN_RT2_MIN_WG 1024
 #endif
   const int rt16 = ((int64_t)batch * n_heads * ((seq_q + 255) / 256) >= BN_RT2_MIN_WG) ? 2 : 1;
-  const int rows_per_wg = dtype == BN_BF16 ? 4 * 32 * rt16 : BM;
+  // bf16 with 4 or 8 query heads per KV head: head-packed work items (all of
+  // a group's heads over 32 rows per workgroup) when BN_PACKED is set
+#ifndef BN_PACKED
+#define BN_PACKED 1
+#endif
+  const int group = n_heads / n_kv_heads;
+  const bool packed = BN_PACKED && dtype == BN_BF16 && (group == 8 || group == 4);
+  const int rows_per_wg = packed ? 32 : dtype == BN_BF16 ? 4 * 32 * rt16 : BM;
   const int n_mt = (seq_q + rows_per_wg - 1) / rows_per_wg;
-  const int64_t n_wg = (int64_t)batch * n_heads * n_mt;
+  const int64_t n_wg = (int64_t)batch * (packed ? n_kv_heads : n_heads) * n_mt;
   if (n_wg > 0x7fffffff) return fail(BN_ERR_UNSUPPORTED, std::string(op) + ": problem too large");
   int st = ensure_device();
   if (st) return st;
@@ -711,10 +748,14 @@ static int prefill_impl(int dtype, const void *q, const void *k, const void *v, 
   p.lse = lse;
   hipStream_t s = as_stream(stream);
   if (dtype == BN_BF16) {
-    if (rt16 == 2)
-      hipLaunchKernelGGL((prefill_bf16_kernel<2, BN_PIPE_OCC2>), dim3((unsigned)n_wg), dim3(256), 0, s, p);
+    if (packed && group == 8)
+      hipLaunchKernelGGL((prefill_bf16_kernel<2, BN_PIPE_OCC2, true>), dim3((unsigned)n_wg), dim3(256), 0, s, p);
+    else if (packed)
+      hipLaunchKernelGGL((prefill_bf16_kernel<1, BN_PIPE_OCC1, true>), dim3((unsigned)n_wg), dim3(256), 0, s, p);
+    else if (rt16 == 2)
+      hipLaunchKernelGGL((prefill_bf16_kernel<2, BN_PIPE_OCC2, false>), dim3((unsigned)n_wg), dim3(256), 0, s, p);
     else
-      hipLaunchKernelGGL((prefill_bf16_kernel<1, BN_PIPE_OCC1>), dim3((unsigned)n_wg), dim3(256), 0, s, p);
+      hipLaunchKernelGGL((prefill_bf16_kernel<1, BN_PIPE_OCC1, false>), dim3((unsigned)n_wg), dim3(256), 0, s, p);
   } else
     hipLaunchKernelGGL(prefill_f32_kernel, dim3((unsigned)n_wg), dim3(256), 0, s, p);
   BN_LAUNCH_CHECK();
