@@ -312,10 +312,12 @@ __global__ __launch_bounds__(256, OCC) void prefill_bf16_kernel(PrefillParams p)
   };
 
   float m[RT], l[RT];  // reference max (raw score units), row-sum partial
+  float mcv[RT];       // m * c, kept with m (it moves only in the fixup)
   f32x16_t o[RT][2];
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
     m[rt] = -INFINITY;
+    mcv[rt] = -INFINITY;
     l[rt] = 0.f;
     o[rt][0] = f32x16_t{};
     o[rt][1] = f32x16_t{};
@@ -409,11 +411,14 @@ __global__ __launch_bounds__(256, OCC) void prefill_bf16_kernel(PrefillParams p)
 #pragma unroll
       for (int i = 0; i < 16; ++i) o[rt][dt][i] *= alpha;
     m[rt] = m_new;
+    mcv[rt] = m_new * c;
     exps(s, mn * c, pb, rs);
   };
-  auto finish = [&](int ok, const f32x16_t (&sc)[RT], bf16x8_t (&pb)[RT][2], float (&rs)[RT])
+  // bad: this lane's row sum is above the limit or NaN; one ballot, no
+  // bool materialised per lane
+  auto finish = [&](bool bad, const f32x16_t (&sc)[RT], bf16x8_t (&pb)[RT][2], float (&rs)[RT])
       __attribute__((always_inline)) {
-    if (!__all(ok)) {
+    if (__builtin_amdgcn_ballot_w64(bad) != 0) {
 #pragma unroll
       for (int rt = 0; rt < RT; ++rt) fixup(rt, sc[rt], pb[rt], rs[rt]);
     }
@@ -443,11 +448,11 @@ __global__ __launch_bounds__(256, OCC) void prefill_bf16_kernel(PrefillParams p)
     pv(va, pp);
     scores(ka, sn);
     float rs[RT];
-    int ok = 1;
+    bool bad = false;
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
-      exps(sc[rt], m[rt] * c, pc[rt], rs[rt]);  // m = -inf: inf/NaN -> fixup
-      ok = ok && rs[rt] <= kSumLimit;
+      exps(sc[rt], mcv[rt], pc[rt], rs[rt]);  // m = -inf: inf/NaN -> fixup
+      bad = bad || !(rs[rt] <= kSumLimit);
     }
 #if BN_PIPE_SCHED
     // LDS reads first, then one MFMA every few VALU instructions
@@ -459,7 +464,7 @@ __global__ __launch_bounds__(256, OCC) void prefill_bf16_kernel(PrefillParams p)
       __builtin_amdgcn_sched_group_barrier(0x002, BN_PIPE_V1, 0);
     }
 #endif
-    finish(ok, sc, pc, rs);
+    finish(bad, sc, pc, rs);
   };
 
   f32x16_t sa[RT], sb[RT];
@@ -483,13 +488,13 @@ __global__ __launch_bounds__(256, OCC) void prefill_bf16_kernel(PrefillParams p)
     scores(ka, sb);
     mask(0, sa);
     float rs[RT];
-    int ok = 1;
+    bool bad = false;
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
-      exps(sa[rt], m[rt] * c, pa[rt], rs[rt]);  // m = -inf: inf/NaN -> fixup
-      ok = ok && rs[rt] <= kSumLimit;
+      exps(sa[rt], mcv[rt], pa[rt], rs[rt]);  // m = -inf: inf/NaN -> fixup
+      bad = bad || !(rs[rt] <= kSumLimit);
     }
-    finish(ok, sa, pa, rs);
+    finish(bad, sa, pa, rs);
   }
   // iteration j: steps 2j+1 (P of tile 2j, scores of 2j+2, softmax of 2j+1)
   // and 2j+2 (P of 2j+1, scores of 2j+3, softmax of 2j+2).  The leading
