@@ -402,6 +402,9 @@ extern "C" int bn_linear_rope(const bn_view *x, const bn_view *w, const bn_view 
                                         std::to_string(need));
   if (workspace && (reinterpret_cast<uintptr_t>(workspace) & 15u))
     return fail(BN_ERR_UNSUPPORTED, std::string(op) + ": workspace must be 16-byte aligned");
+  // grid limits: row tiles on grid y (at most 65535), reduction threads
+  if ((!small && (m + TM - 1) / TM > 65535) || (int64_t)m * (n / 4) / 256 >= 0x7fffffff)
+    return fail(BN_ERR_UNSUPPORTED, std::string(op) + ": problem too large");
   if ((st = ensure_device())) return st;
   hipStream_t s = as_stream(stream);
   void *ws = workspace;
