@@ -1,6 +1,6 @@
 """TinyLLaMA-1.1B forward with a KV cache, built on the attention path.
 
-Drives BASELINE config 4: 22 layers, hidden 2048, 32/4 GQA heads, head_dim 64,
+Drives config 4: 22 layers, hidden 2048, 32/4 GQA heads, head_dim 64,
 SwiGLU 5632, vocab 32000, RMSNorm, RoPE theta 10000, fp32, random weights;
 a prompt prefill followed by greedy decode steps.
 

@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the MI355X GQA attention path (one JSON line on stdout).
 
-Headline (``value``): causal GQA prefill, BASELINE config 2 in bf16
+Headline (``value``): causal GQA prefill, config 2 in bf16
 (B=4, S=2048, 32 query / 4 KV heads, head_dim 64, scale 1/8), in TFLOP/s of
 algorithmic work 4*B*H*D*S(S+1)/2 (unmasked QK^T and PV MACs x 2).
 One step = one prefill launch over the whole batch, inputs resident in HBM.
@@ -512,7 +512,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
-              "(the attention path has no multi-GPU code; see DESIGN.md for how it would shard)",
+              "(the attention path has no multi-GPU code)",
               file=sys.stderr)
         sys.exit(2)
     import torch
@@ -529,7 +529,7 @@ def main():
            "steps": K, "warmup": W, "ms_per_step": head["ms_per_launch"],
            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
            "data": "synthetic N(0,1) from a fixed seed (torch.Generator 0)",
-           "config": {"workload": "causal GQA prefill (BASELINE config 2)", "batch": 4,
+           "config": {"workload": "causal GQA prefill (config 2)", "batch": 4,
                       "seq_len": 2048, "n_heads": 32, "n_kv_heads": 4, "head_dim": 64,
                       "scale": 0.125, "flops_per_step": head["flops_per_launch"]},
            "roofline": head["roofline"]}

@@ -1,7 +1,7 @@
 """GPU parity of the fused GQA prefill and KV-cache decode kernels.
 
 Small shapes are compared with the CPU oracle element for element (every
-head, every row); the BASELINE shapes (B=4, S=2048 prefill; B=64, L=4096
+head, every row); the full benchmark shapes (B=4, S=2048 prefill; B=64, L=4096
 decode) are checked on sampled (batch, head) pairs against the oracle and on
 size-independent properties (Q=0 gives prefix means of V; constant-per-head
 V exposes the GQA head mapping; decode equals the prefill's last row).
@@ -94,7 +94,7 @@ def test_prefill_head_mapping(dtype):
 
 @pytest.mark.parametrize("dtype", ["bf16", "f32"])
 def test_prefill_baseline_shape(dtype):
-    """B=4, S=2048, 32/4 heads, D=64, causal, scale 1/8."""
+    """config 2: B=4, S=2048, 32/4 heads, D=64, causal, scale 1/8."""
     Bn, S, H, Hkv = 4, 2048, 32, 4
     rngs = np.random.default_rng(0)
     q = rngs.standard_normal((Bn, S, H, 64)).astype(np.float32)
@@ -249,7 +249,7 @@ def test_decode_workspace_reuse(dtype, Hkv):
 
 @pytest.mark.parametrize("ragged", [False, True])
 def test_decode_baseline_shape(ragged):
-    """B=64, bf16 cache of 4096, 32/4 heads; ragged lengths in [512, 4096]."""
+    """config 3: B=64, bf16 cache of 4096, 32/4 heads; ragged lengths in [512, 4096]."""
     Bn, L, H, Hkv = 64, 4096, 32, 4
     r = np.random.default_rng(2)
     lens = r.integers(512, 4097, Bn).astype(np.int32) if ragged else np.full(Bn, L, np.int32)

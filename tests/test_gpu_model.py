@@ -1,4 +1,4 @@
-"""GPU parity of the layer-level paths: BASELINE config 1 (one attention block
+"""GPU parity of the layer-level paths: config 1 (one attention block
 through the `bten` surface, fused-head as the reference computes it and
 per-head GQA) and config 4's TinyLLaMA driver (teacher-forced, kernel by
 kernel, against the CPU oracle on the inputs the GPU run produced)."""
