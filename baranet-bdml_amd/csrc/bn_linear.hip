@@ -249,7 +249,8 @@ __global__ __launch_bounds__(256) void linear_small_kernel(LinParams p) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int kk = k0 + 4 * u;
-      wv[u] = (col_ok && kk < nk) ? *(const u32x4_t *)(W + (kb + kk) * p.w_rs + gn)
+      // w is read once per call: non-temporal, kept out of L2/MALL
+      wv[u] = (col_ok && kk < nk) ? __builtin_nontemporal_load((const u32x4_t *)(W + (kb + kk) * p.w_rs + gn))
                                   : u32x4_t{0u, 0u, 0u, 0u};
     }
 #pragma unroll
