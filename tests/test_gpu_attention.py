@@ -457,3 +457,22 @@ def test_bten_surface_backward_matches_c_abi():
     for g, r in zip(got, ref):
         assert np.array_equal(g, host(r))
     check_backward(got, q, k, v, do, host(o2), host(lse2), 1, 0, "bten")
+
+
+@pytest.mark.parametrize("Sq,Skv", [(0, 96), (70, 0)])
+def test_prefill_backward_empty_sides(Sq, Skv):
+    # no query rows: every key gets dK = dV = 0 (written, not left as they
+    # were); no keys: every row gets dQ = 0
+    H, Hkv = 8, 2
+    q = torch.zeros((1, Sq, H, 64), dtype=torch.bfloat16, device="cuda")
+    k = torch.randn((1, Skv, Hkv, 64), device="cuda").to(torch.bfloat16)
+    v = torch.randn((1, Skv, Hkv, 64), device="cuda").to(torch.bfloat16)
+    o = torch.zeros_like(q)
+    do = torch.randn((1, Sq, H, 64), device="cuda").to(torch.bfloat16)
+    lse = torch.full((1, H, Sq), float("-inf"), device="cuda")
+    dq, dk, dv = B.gqa_prefill_backward(q, k, v, o, do, lse, scale=0.125, dq=nan_like(q),
+                                        dk=nan_like(k), dv=nan_like(v))
+    torch.cuda.synchronize()
+    assert torch.count_nonzero(dq.float()).item() == 0 and not torch.isnan(dq.float()).any()
+    assert torch.count_nonzero(dk.float()).item() == 0 and not torch.isnan(dk.float()).any()
+    assert torch.count_nonzero(dv.float()).item() == 0 and not torch.isnan(dv.float()).any()

@@ -370,3 +370,10 @@ def test_linear_rope_empty_k_gives_zeros():
     w = torch.empty((0, 64), device="cuda")
     y = B.linear_rope(x, w, rope_cols=64, position_offset=3)
     assert torch.count_nonzero(y).item() == 0
+
+
+def test_linear_rope_empty_rows_is_noop():
+    x = torch.empty((0, 64), device="cuda")
+    w = torch.randn((64, 128), device="cuda")
+    y = B.linear_rope(x, w, rope_cols=64)
+    assert y.shape == (0, 128)
