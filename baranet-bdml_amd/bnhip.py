@@ -37,6 +37,17 @@ class BnPoolStats(C.Structure):
                                           "bytes_reserved", "n_allocs", "n_frees", "n_live")]
 
 
+class BnLlamaConfig(C.Structure):
+    _fields_ = [(n, C.c_int) for n in ("n_layers", "hidden", "n_heads", "n_kv_heads",
+                                       "intermediate", "vocab", "max_len")] + \
+               [("rms_eps", C.c_float), ("rope_theta", C.c_float)]
+
+
+class BnLlamaLayer(C.Structure):
+    _fields_ = [(n, C.c_void_p) for n in ("ln1", "wqkv", "wo", "ln2", "wgu", "wd",
+                                          "k_cache", "v_cache")]
+
+
 class BnError(RuntimeError):
     def __init__(self, status, msg):
         super().__init__(msg)
@@ -90,6 +101,9 @@ def lib():
         "bn_linear_rope_workspace_size": ([i] * 4, sz),
         "bn_linear_rope": ([V, V, V, i, i, i, f, vp, sz, vp], i),
         "bn_gqa_prefill_backward": ([i] + [vp] * 9 + [i] * 6 + [i64] * 6 + [f, i, i, vp, sz, vp], i),
+        "bn_llama_decode_workspace_size": ([C.POINTER(BnLlamaConfig)], sz),
+        "bn_llama_decode": ([C.POINTER(BnLlamaConfig), vp, vp, vp, C.POINTER(BnLlamaLayer),
+                             i, i, i, vp, vp, sz, vp], i),
         "bn_gqa_decode_workspace_size": ([i, i, i, i], sz),
         "bn_gqa_decode": ([i, vp, vp, vp, vp, vp] + [i] * 5 + [f, vp, sz, vp], i),
     }

@@ -1,0 +1,221 @@
+// bn_llama.hip -- greedy decode of a LLaMA-style decoder (TinyLLaMA's
+// layout: pre-norm GQA attention + SwiGLU MLP, fp32) with per-layer KV caches,
+// driven from the host without a synchronisation per token: each step's
+// token stays on the device, where the next step's embedding gather reads it.
+// The reference has no KV cache and reruns the whole prefix for every token
+// (llama_model.py:135-141, llama_model.hpp:161-198); its decoder layer is
+// llama_layers.hpp:241-272.  Every step is the path's own kernels:
+// bn_linear_rope (projections, the QKV rotation in its epilogue),
+// bn_gqa_decode, bn_add_rmsnorm, bn_silu_mul, bn_rmsnorm and bn_argmax.
+#include <algorithm>
+
+#include "bn_common.hpp"
+
+namespace bn {
+namespace {
+
+// x = embed[token]; the token comes from `tok` (device) or, when tok is
+// null, from `first`; ids past the table are clamped (argmax never gives one)
+__global__ __launch_bounds__(256) void embed_gather_kernel(const float *embed, const uint32_t *tok,
+                                                           uint32_t first, int vocab, float *x,
+                                                           int hidden) {
+  uint32_t t = tok ? *tok : first;
+  t = t < (uint32_t)vocab ? t : (uint32_t)(vocab - 1);
+  const float *row = embed + (int64_t)t * hidden;
+  for (int i = threadIdx.x; i < hidden; i += 256) x[i] = row[i];
+}
+
+// lens[i] = first + i + 1 (the cache length after step i)
+__global__ __launch_bounds__(256) void fill_lens_kernel(int32_t *lens, int first, int n) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i < n) lens[i] = first + i + 1;
+}
+
+bn_view fview(const void *p, int h, int w, int stride_h) {
+  bn_view v;
+  v.data = const_cast<void *>(p);
+  v.offset = 0;
+  v.h = h;
+  v.w = w;
+  v.stride_h = stride_h;
+  v.stride_w = 1;
+  v.dtype = BN_F32;
+  v.on_device = 1;
+  return v;
+}
+
+size_t a256(size_t n) { return (n + 255) & ~(size_t)255; }
+
+// workspace regions, in bytes from the start
+struct Plan {
+  size_t hdn, xn, qkv, o, attn, gu, act, mlp, logits, tok, lens, lin, dec, total;
+  size_t lin_bytes, dec_bytes;
+};
+
+Plan plan_of(const bn_llama_config *c) {
+  const int hd = c->hidden / c->n_heads, kv = c->n_kv_heads * hd;
+  const int shapes[5][2] = {{c->hidden, c->hidden + 2 * kv}, {c->hidden, c->hidden},
+                            {c->hidden, 2 * c->intermediate}, {c->intermediate, c->hidden},
+                            {c->hidden, c->vocab}};
+  size_t lin = 0;
+  for (const auto &s : shapes) lin = std::max(lin, bn_linear_rope_workspace_size(BN_F32, 1, s[1], s[0]));
+  Plan p;
+  size_t at = 0;
+  auto take = [&](size_t bytes) { const size_t r = at; at += a256(bytes); return r; };
+  p.hdn = take(4 * (size_t)c->hidden);
+  p.xn = take(4 * (size_t)c->hidden);
+  p.qkv = take(4 * (size_t)(c->hidden + 2 * kv));
+  p.o = take(4 * (size_t)c->hidden);
+  p.attn = take(4 * (size_t)c->hidden);
+  p.gu = take(4 * (size_t)2 * c->intermediate);
+  p.act = take(4 * (size_t)c->intermediate);
+  p.mlp = take(4 * (size_t)c->hidden);
+  p.logits = take(4 * (size_t)c->vocab);
+  p.tok = take(4);
+  p.lens = take(4 * (size_t)c->max_len);
+  p.lin_bytes = lin;
+  p.lin = take(lin);
+  p.dec_bytes = bn_gqa_decode_workspace_size(1, c->max_len, c->n_heads, hd);
+  p.dec = take(p.dec_bytes);
+  p.total = at;
+  return p;
+}
+
+int check_config(const bn_llama_config *c) {
+  const char *op = "LLaMA decode";
+  if (!c) return fail(BN_ERR_INVALID_ARG, std::string(op) + ": NULL config");
+  if (c->n_layers <= 0 || c->hidden <= 0 || c->n_heads <= 0 || c->n_kv_heads <= 0 ||
+      c->intermediate <= 0 || c->vocab <= 0 || c->max_len <= 0)
+    return fail(BN_ERR_SHAPE, std::string(op) + ": sizes must be positive");
+  if (c->hidden % c->n_heads != 0 || c->hidden / c->n_heads != 64 || c->n_heads % c->n_kv_heads != 0)
+    return fail(BN_ERR_UNSUPPORTED,
+                std::string(op) + ": head_dim (hidden / n_heads) must be 64 and n_heads a multiple of n_kv_heads");
+  if (c->hidden % 4 || c->intermediate % 4 || c->vocab % 4)
+    return fail(BN_ERR_UNSUPPORTED, std::string(op) + ": hidden, intermediate and vocab must be multiples of 4");
+  return BN_OK;
+}
+
+}  // namespace
+}  // namespace bn
+
+using namespace bn;
+
+extern "C" size_t bn_llama_decode_workspace_size(const bn_llama_config *config) {
+  if (check_config(config)) return 0;
+  return plan_of(config).total;
+}
+
+extern "C" int bn_llama_decode(const bn_llama_config *c, const float *embed, const float *ln_f,
+                               const float *lm_head, const bn_llama_layer_weights *layers,
+                               int first_token, int position, int n_tokens, uint32_t *tokens_out,
+                               void *workspace, size_t workspace_bytes, void *stream) {
+  const char *op = "LLaMA decode";
+  int st;
+  if ((st = check_config(c))) return st;
+  if (n_tokens < 0 || position < 0 || (int64_t)position + n_tokens > c->max_len)
+    return fail(BN_ERR_SHAPE, std::string(op) + ": position + n_tokens must stay within max_len");
+  if (first_token < 0 || first_token >= c->vocab)
+    return fail(BN_ERR_INVALID_ARG, std::string(op) + ": first_token outside the vocabulary");
+  if (n_tokens == 0) return BN_OK;
+  if (!embed || !ln_f || !lm_head || !layers || !tokens_out)
+    return fail(BN_ERR_INVALID_ARG, std::string(op) + ": NULL pointer");
+  for (int l = 0; l < c->n_layers; ++l) {
+    const bn_llama_layer_weights &L = layers[l];
+    if (!L.ln1 || !L.wqkv || !L.wo || !L.ln2 || !L.wgu || !L.wd || !L.k_cache || !L.v_cache)
+      return fail(BN_ERR_INVALID_ARG, std::string(op) + ": NULL pointer in layer " + std::to_string(l));
+  }
+  const Plan pl = plan_of(c);
+  if (workspace && workspace_bytes < pl.total)
+    return fail(BN_ERR_INVALID_ARG, std::string(op) + ": workspace of " + std::to_string(workspace_bytes) +
+                                        " bytes, need " + std::to_string(pl.total));
+  if (workspace && (reinterpret_cast<uintptr_t>(workspace) & 255u))
+    return fail(BN_ERR_UNSUPPORTED, std::string(op) + ": workspace must be 256-byte aligned");
+  if ((st = ensure_device())) return st;
+  hipStream_t s = as_stream(stream);
+  void *ws = workspace;
+  bool own = false;
+  if (!ws) {
+    if ((st = bn_alloc(&ws, pl.total, stream))) return st;
+    own = true;
+  }
+  char *W = (char *)ws;
+  float *hdn = (float *)(W + pl.hdn), *xn = (float *)(W + pl.xn), *qkv = (float *)(W + pl.qkv);
+  float *o = (float *)(W + pl.o), *attn = (float *)(W + pl.attn), *gu = (float *)(W + pl.gu);
+  float *act = (float *)(W + pl.act), *mlp = (float *)(W + pl.mlp), *logits = (float *)(W + pl.logits);
+  int32_t *lens = (int32_t *)(W + pl.lens);
+  void *lin_ws = W + pl.lin, *dec_ws = pl.dec_bytes ? W + pl.dec : nullptr;
+
+  const int hid = c->hidden, hd = 64, kv = c->n_kv_heads * hd, I = c->intermediate;
+  const float scale = 0.125f;  // 1 / sqrt(64)
+  const bn_view v_hdn = fview(hdn, 1, hid, hid), v_xn = fview(xn, 1, hid, hid);
+  const bn_view v_qkv = fview(qkv, 1, hid + 2 * kv, hid + 2 * kv);
+  const bn_view v_o = fview(o, 1, hid, hid), v_attn = fview(attn, 1, hid, hid);
+  const bn_view v_gu = fview(gu, 1, 2 * I, 2 * I);
+  bn_view v_gate = fview(gu, 1, I, 2 * I), v_up = fview(gu + I, 1, I, 2 * I);
+  const bn_view v_act = fview(act, 1, I, I), v_mlp = fview(mlp, 1, hid, hid);
+  const bn_view v_logits = fview(logits, 1, c->vocab, c->vocab);
+  const bn_view v_lnf = fview(ln_f, 1, hid, hid), v_lm = fview(lm_head, hid, c->vocab, c->vocab);
+
+  hipLaunchKernelGGL(fill_lens_kernel, dim3((unsigned)((n_tokens + 255) / 256)), dim3(256), 0, s, lens,
+                     position, n_tokens);
+  hipError_t e = hipGetLastError();
+  st = e == hipSuccess ? BN_OK : hip_fail(e, __FILE__, __LINE__);
+  for (int t = 0; st == BN_OK && t < n_tokens; ++t) {
+    const int pos = position + t;
+    hipLaunchKernelGGL(embed_gather_kernel, dim3(1), dim3(256), 0, s, embed,
+                       t ? (const uint32_t *)(tokens_out + t - 1) : (const uint32_t *)nullptr,
+                       (uint32_t)first_token, c->vocab, hdn, hid);
+    if ((e = hipGetLastError()) != hipSuccess) {
+      st = hip_fail(e, __FILE__, __LINE__);
+      break;
+    }
+    const bn_view ln10 = fview(layers[0].ln1, 1, hid, hid);
+    if ((st = bn_rmsnorm(&v_hdn, &ln10, &v_xn, c->rms_eps, stream))) break;
+    for (int l = 0; l < c->n_layers && st == BN_OK; ++l) {
+      const bn_llama_layer_weights &L = layers[l];
+      const bn_view wqkv = fview(L.wqkv, hid, hid + 2 * kv, hid + 2 * kv);
+      const bn_view wo = fview(L.wo, hid, hid, hid), wgu = fview(L.wgu, hid, 2 * I, 2 * I);
+      const bn_view wd = fview(L.wd, I, hid, hid), ln2 = fview(L.ln2, 1, hid, hid);
+      const bn_view nxt = l + 1 < c->n_layers ? fview(layers[l + 1].ln1, 1, hid, hid) : v_lnf;
+      // Q, K and V (Q and K rotated at position pos), K and V appended to the caches
+      if ((st = bn_linear_rope(&v_xn, &wqkv, &v_qkv, hid + kv, pos, hd, c->rope_theta, lin_ws,
+                               pl.lin_bytes, stream)))
+        break;
+      const bn_view kq = fview(qkv + hid, 1, kv, kv), vq = fview(qkv + hid + kv, 1, kv, kv);
+      const bn_view kc = fview(L.k_cache + (int64_t)pos * kv, 1, kv, kv);
+      const bn_view vc = fview(L.v_cache + (int64_t)pos * kv, 1, kv, kv);
+      if ((st = bn_copy(&kq, &kc, stream)) || (st = bn_copy(&vq, &vc, stream))) break;
+      if ((st = bn_gqa_decode(BN_F32, qkv, L.k_cache, L.v_cache, lens + t, o, 1, c->max_len, c->n_heads,
+                              c->n_kv_heads, hd, scale, dec_ws, pl.dec_bytes, stream)))
+        break;
+      if ((st = bn_linear_rope(&v_o, &wo, &v_attn, 0, 0, hd, c->rope_theta, lin_ws, pl.lin_bytes, stream)))
+        break;
+      if ((st = bn_add_rmsnorm(&v_hdn, &v_attn, &ln2, &v_hdn, &v_xn, c->rms_eps, stream))) break;
+      if ((st = bn_linear_rope(&v_xn, &wgu, &v_gu, 0, 0, hd, c->rope_theta, lin_ws, pl.lin_bytes, stream)))
+        break;
+      if ((st = bn_silu_mul(&v_gate, &v_up, &v_act, stream))) break;
+      if ((st = bn_linear_rope(&v_act, &wd, &v_mlp, 0, 0, hd, c->rope_theta, lin_ws, pl.lin_bytes, stream)))
+        break;
+      if ((st = bn_add_rmsnorm(&v_hdn, &v_mlp, &nxt, &v_hdn, &v_xn, c->rms_eps, stream))) break;
+    }
+    if (st) break;
+    if ((st = bn_linear_rope(&v_xn, &v_lm, &v_logits, 0, 0, hd, c->rope_theta, lin_ws, pl.lin_bytes,
+                             stream)))
+      break;
+    bn_view tout;
+    tout.data = tokens_out + t;
+    tout.offset = 0;
+    tout.h = 1;
+    tout.w = 1;
+    tout.stride_h = 1;
+    tout.stride_w = 1;
+    tout.dtype = BN_U32;
+    tout.on_device = 1;
+    if ((st = bn_argmax(&v_logits, &tout, stream))) break;
+  }
+  if (own) {
+    const int st2 = bn_free(ws, stream);
+    if (st == BN_OK) st = st2;
+  }
+  return st;
+}

@@ -263,3 +263,45 @@ class TinyLlama:
             self.path_ms = sum(s.elapsed_time(e) for s, e in self._events)
         self.timing = False
         return torch.stack(out), self.path_ms
+
+    # ------------------------------------------------------- native decoding
+    def native_config(self) -> bnhip.BnLlamaConfig:
+        cfg = self.cfg
+        return bnhip.BnLlamaConfig(cfg.num_hidden_layers, cfg.hidden_size, cfg.num_attention_heads,
+                                   cfg.num_key_value_heads, cfg.intermediate_size, cfg.vocab_size,
+                                   self.max_len, cfg.rms_norm_eps, cfg.rope_theta)
+
+    def generate_native(self, ids: torch.Tensor, new_tokens: int):
+        """Greedy decode with the decode loop in native code: the prompt runs
+        through prefill(), then one bn_llama_decode call runs every decode
+        step (embedding gather, layers, lm_head, argmax) on the current
+        stream with no host round trip.  Same kernels in the same order as
+        generate(), so the tokens and the KV caches match it exactly."""
+        logits = self.prefill(ids)
+        t0 = int(torch.argmax(logits[-1]))
+        out = torch.empty(new_tokens + 1, dtype=torch.int32, device="cuda")
+        out[0] = t0
+        if new_tokens > 0:                        # out[1 + t] = argmax after step t
+            self.decode_native(t0, new_tokens, out[1:])
+        return out[:new_tokens].long()
+
+    def decode_native(self, first_token: int, n_tokens: int, tokens_out: torch.Tensor):
+        """n_tokens decode steps from position `length`: step t feeds
+        first_token (t = 0) or the token step t-1 chose (tokens_out[t-1]) and
+        writes its own argmax to tokens_out[t]."""
+        cfg = self.cfg
+        c = self.native_config()
+        layers = (bnhip.BnLlamaLayer * cfg.num_hidden_layers)(*[
+            bnhip.BnLlamaLayer(L["ln1"].data_ptr(), L["wqkv"].data_ptr(), L["wo"].data_ptr(),
+                               L["ln2"].data_ptr(), L["wgu"].data_ptr(), L["wd"].data_ptr(),
+                               L["k_cache"].data_ptr(), L["v_cache"].data_ptr())
+            for L in self.layers])
+        if not hasattr(self, "native_ws"):
+            n = bnhip.lib().bn_llama_decode_workspace_size(C.byref(c))
+            self.native_ws = torch.empty(max(n // 4, 1), device="cuda")
+        assert tokens_out.dtype == torch.int32 and tokens_out.is_cuda and tokens_out.numel() >= n_tokens
+        bnhip.call("bn_llama_decode", C.byref(c), self.embed.data_ptr(), self.ln_f.data_ptr(),
+                   self.lm_head.data_ptr(), layers, first_token, self.length, n_tokens,
+                   tokens_out.data_ptr(), self.native_ws.data_ptr(), self.native_ws.numel() * 4,
+                   torch.cuda.current_stream().cuda_stream)
+        self.length += n_tokens

@@ -419,6 +419,22 @@ def bench_tinyllama(prompt=512, new_tokens=128, cpu=True, warmup_tokens=2):
                            "bn_rope; decode steps: fused into the QKV projection kernel), GQA "
                            "prefill, GQA decode (fp32)",
            "first_tokens": [int(t) for t in toks[:8].cpu()], "cache_length_end": m.length}
+    # the same generation with the decode loop in native code (bn_llama_decode):
+    # one call runs every decode step, no host round trip per token
+    def reset():
+        for L in m.layers:
+            L["k_cache"].zero_()
+            L["v_cache"].zero_()
+        m.length = 0
+    reset()
+    m.generate_native(ids, max(warmup_tokens, 1))
+    reset()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ntoks = m.generate_native(ids, new_tokens)
+    torch.cuda.synchronize()
+    res["native_wall_s"] = round(time.perf_counter() - t0, 3)
+    res["native_tokens_match"] = bool(torch.equal(ntoks.cpu(), toks.cpu()))
     if cpu:
         res["cpu_baseline"] = cpu_baseline_tinyllama(m, ids)
     return res

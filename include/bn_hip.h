@@ -243,6 +243,39 @@ int bn_gqa_prefill_backward(int dtype, const void *q, const void *k,
                             void *workspace, size_t workspace_bytes,
                             void *stream);
 
+/* ------------------------------------------------------- decode driver
+ * Greedy decode of a LLaMA-style decoder (pre-norm GQA attention + SwiGLU
+ * MLP, llama_layers.hpp:241-272; fp32, head_dim 64) with per-layer KV caches
+ * [max_len, n_kv_heads*64].  Step t processes token t (first_token for t = 0,
+ * else tokens_out[t-1]) at position `position + t`: embedding row, every layer
+ * (QKV projection with RoPE, K/V appended to the caches at that row,
+ * bn_gqa_decode over the cache, O projection, residual add + RMSNorm, gate|up
+ * projection, SwiGLU, down projection, residual add + RMSNorm), lm_head, and
+ * writes the argmax of the logits to tokens_out[t] (device, uint32).  Nothing
+ * waits for the host between steps.  Replaces the reference's generate loop
+ * (llama_model.py:112-168), which has no cache and reruns the prefix per
+ * token (:135-141); the reference samples from softmax(logits / T) with an
+ * optional top-k and stops at eos_token_id (:145-162), this loop is its
+ * deterministic limit (top_k = 1, argmax) and runs all n steps.  Weight layouts are x @ W: wqkv [hidden, (H + 2*Hkv)*64]
+ * (Q | K | V), wo [hidden, hidden], wgu [hidden, 2*intermediate] (gate | up),
+ * wd [intermediate, hidden], embed [vocab, hidden], lm_head [hidden, vocab];
+ * norm weights [hidden].  workspace (256-byte aligned,
+ * bn_llama_decode_workspace_size bytes) may be NULL: the pool supplies it. */
+typedef struct bn_llama_config {
+  int n_layers, hidden, n_heads, n_kv_heads, intermediate, vocab, max_len;
+  float rms_eps, rope_theta;
+} bn_llama_config;
+typedef struct bn_llama_layer_weights {
+  const float *ln1, *wqkv, *wo, *ln2, *wgu, *wd;
+  float *k_cache, *v_cache;
+} bn_llama_layer_weights;
+size_t bn_llama_decode_workspace_size(const bn_llama_config *config);
+int bn_llama_decode(const bn_llama_config *config, const float *embed,
+                    const float *ln_f, const float *lm_head,
+                    const bn_llama_layer_weights *layers, int first_token,
+                    int position, int n_tokens, uint32_t *tokens_out,
+                    void *workspace, size_t workspace_bytes, void *stream);
+
 /* KV-cache decode: one new query token per sequence.  The reference has no
  * KV cache (llama_model.py:135-141 recomputes the prefix); this is the last
  * row of bn_gqa_prefill with seq_offset = seq_lens[b]-1 over keys

@@ -238,3 +238,51 @@ def test_linear_rope_workspace_size():
     # enough tiles: no split
     assert L.bn_linear_rope_workspace_size(B.BN_F32, 4096, 4096, 2048) == 0
     assert L.bn_linear_rope_workspace_size(B.BN_U32, 4, 4, 4) == 0
+
+
+def llama_cfg(**kw):
+    d = dict(n_layers=22, hidden=2048, n_heads=32, n_kv_heads=4, intermediate=5632, vocab=32000,
+             max_len=640, rms_eps=1e-5, rope_theta=1e4)
+    d.update(kw)
+    return B.BnLlamaConfig(*d.values())
+
+
+def test_llama_decode_validation():
+    L = B.lib()
+    c = llama_cfg()
+    n = L.bn_llama_decode_workspace_size(C.byref(c))
+    # residual + norm + qkv + o + attn + gate/up + act + mlp + logits rows, lens, and the
+    # linear and decode partial sums: at least the activations of one step
+    assert n >= 4 * (5 * 2048 + 2560 + 2 * 5632 + 5632 + 32000 + 640)
+    assert L.bn_llama_decode_workspace_size(C.byref(llama_cfg(hidden=2048, n_heads=16))) == 0
+    assert L.bn_llama_decode_workspace_size(None) == 0
+    layers = (B.BnLlamaLayer * 22)()
+    fake = 4096
+
+    def dec(cfg, first, pos, n_tok, lay=layers, ptr=fake):
+        return st("bn_llama_decode", C.byref(cfg), ptr, ptr, ptr, lay, first, pos, n_tok, ptr,
+                  None, 0, None)
+
+    s, m = dec(llama_cfg(n_heads=16), 0, 0, 1)
+    assert s == B.BN_ERR_UNSUPPORTED and "head_dim" in m
+    s, m = dec(llama_cfg(vocab=32002), 0, 0, 1)
+    assert s == B.BN_ERR_UNSUPPORTED and "multiples of 4" in m
+    s, m = dec(llama_cfg(n_layers=0), 0, 0, 1)
+    assert s == B.BN_ERR_SHAPE
+    s, m = dec(c, 0, 600, 41)
+    assert s == B.BN_ERR_SHAPE and "max_len" in m
+    assert dec(c, 0, 600, 40)[0] != B.BN_ERR_SHAPE
+    s, m = dec(c, 32000, 0, 1)
+    assert s == B.BN_ERR_INVALID_ARG and "vocabulary" in m
+    assert dec(c, 0, 0, 0) == (B.BN_OK, "")           # nothing to do: no device needed
+    s, m = dec(c, 0, 0, 1, ptr=None)
+    assert s == B.BN_ERR_INVALID_ARG and "NULL pointer" in m
+    s, m = dec(c, 0, 0, 1)                            # layer pointers all NULL
+    assert s == B.BN_ERR_INVALID_ARG and "layer 0" in m
+    full = (B.BnLlamaLayer * 22)(*[B.BnLlamaLayer(*[fake] * 8) for _ in range(22)])
+    s, m = st("bn_llama_decode", C.byref(c), fake, fake, fake, full, 0, 0, 1, fake,
+              C.c_void_p(fake), 256, None)
+    assert s == B.BN_ERR_INVALID_ARG and "need" in m
+    s, m = st("bn_llama_decode", C.byref(c), fake, fake, fake, full, 0, 0, 1, fake,
+              C.c_void_p(fake + 16), n, None)
+    assert s == B.BN_ERR_UNSUPPORTED and "256-byte" in m

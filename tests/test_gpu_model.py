@@ -8,6 +8,7 @@ import numpy as np
 import pytest
 import torch
 
+import bnhip
 import bten
 from gpu_util import FP32_TOL, assert_close, require_gpu
 from llama_layers import GroupedQueryAttention, RMSNorm
@@ -109,3 +110,40 @@ def test_tinyllama_cache_matches_recompute():
     ref_logits = fresh.prefill(torch.cat([ids, tok.view(1)]))
     a, b = step_logits.cpu().numpy(), ref_logits.cpu().numpy()
     assert float(np.max(np.abs(a - b)) / np.max(np.abs(b))) < 1e-4
+
+
+@pytest.mark.parametrize("prompt,new", [(40, 12), (7, 1), (1, 30)])
+def test_native_decode_matches_generate(prompt, new):
+    """bn_llama_decode runs the decode loop natively (gather, layers, lm_head,
+    argmax, next token fed on the device).  It launches the same kernels in
+    the same order as the Python step loop, so the generated tokens and every
+    layer's KV cache are bit-identical to generate()."""
+    ids = torch.from_numpy(np.random.default_rng(7 + prompt).integers(0, 512, prompt)).cuda()
+    a, b = small_llama(), small_llama()
+    ref, _ = a.generate(ids, new)
+    got = b.generate_native(ids, new)
+    torch.cuda.synchronize()
+    assert torch.equal(ref.cpu(), got.cpu()), (ref.tolist(), got.tolist())
+    assert a.length == b.length == prompt + new
+    for La, Lb in zip(a.layers, b.layers):
+        assert torch.equal(La["k_cache"], Lb["k_cache"]) and torch.equal(La["v_cache"], Lb["v_cache"])
+
+
+def test_native_decode_continues_and_rejects_overflow():
+    """Two native calls in a row continue where the first stopped (the second
+    starts from the first call's last token at the next position); a call
+    that would pass max_len is refused before any launch."""
+    ids = torch.from_numpy(np.random.default_rng(3).integers(0, 512, 20)).cuda()
+    a, b = small_llama(max_len=64), small_llama(max_len=64)
+    ref, _ = a.generate(ids, 16)
+    b.prefill(ids)
+    first = int(ref[0])
+    out = torch.empty(16, dtype=torch.int32, device="cuda")
+    b.decode_native(first, 6, out[:6])
+    torch.cuda.synchronize()
+    b.decode_native(int(out[5]), 10, out[6:])
+    assert torch.equal(torch.cat([ref[:1].cpu().int(), out[:15].cpu()]), ref.cpu().int())
+    for La, Lb in zip(a.layers, b.layers):
+        assert torch.equal(La["k_cache"], Lb["k_cache"])
+    with pytest.raises(bnhip.BnError, match="max_len"):
+        b.decode_native(0, 64 - b.length + 1, torch.empty(64, dtype=torch.int32, device="cuda"))
