@@ -32,6 +32,9 @@ namespace {
 
 constexpr int HD = 64;
 constexpr int NT = 8;  // keys per lane group between softmax rescales
+#ifndef BN_DECODE_SINGLE_NT
+#define BN_DECODE_SINGLE_NT 10  // single pass: up to 640 keys (16 waves x 4 groups x 10) in one load round
+#endif
 
 template <typename T> struct DecVec;
 template <> struct DecVec<float> {
@@ -78,6 +81,7 @@ struct DecodeParams {
 template <typename T, int G, int WV, bool SINGLE>
 __global__ __launch_bounds__(64 * WV) void decode_split_kernel(DecodeParams p) {
   constexpr int VEC = DecVec<T>::VEC;
+  constexpr int NT = SINGLE ? BN_DECODE_SINGLE_NT : bn::NT;
   constexpr int LPK = HD / VEC;  // lanes per key
   constexpr int KPI = 64 / LPK;  // keys per wave per load instruction
   __shared__ float red_m[WV][G], red_l[WV][G];
