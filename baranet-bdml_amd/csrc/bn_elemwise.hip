@@ -276,20 +276,53 @@ __global__ void sum_kernel(DView<const T> x, DView<T> y, int axis) {
   }
 }
 
+// argmax: one workgroup per row.  The sequential rule (accumulator starts at
+// column 0, takes x when x > accumulator) returns column 0 when x[0] is NaN
+// (nothing compares greater) and otherwise the first column holding the
+// largest non-NaN value (a NaN elsewhere never compares greater).  Each
+// thread scans columns t, t + 256, ... keeping its first maximum; the
+// candidates merge by larger value, then smaller column -- the same answer.
 template <typename T>
-__global__ void argmax_kernel(DView<const T> x, DView<uint32_t> y) {
-  const int r = blockIdx.x * 256 + threadIdx.x;
-  if (r >= x.h) return;
-  T best = x.at(r, 0);
-  uint32_t bi = 0;
-  for (int c = 1; c < x.w; ++c) {
-    T v = x.at(r, c);
-    if (v > best) {
+__device__ __forceinline__ bool is_nan_val(T v) {
+  if constexpr (std::is_same<T, float>::value) return v != v;
+  else return false;
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void argmax_kernel(DView<const T> x, DView<uint32_t> y) {
+  constexpr uint32_t NONE = 0xffffffffu;
+  __shared__ T sv[256];
+  __shared__ uint32_t si[256];
+  const int r = blockIdx.x, t = threadIdx.x;
+  if (is_nan_val(x.at(r, 0))) {
+    if (t == 0) y.at(r, 0) = 0;
+    return;
+  }
+  T best = T{};
+  uint32_t bi = NONE;
+  for (int c = t; c < x.w; c += 256) {
+    const T v = x.at(r, c);
+    if (!is_nan_val(v) && (bi == NONE || v > best)) {
       best = v;
       bi = (uint32_t)c;
     }
   }
-  y.at(r, 0) = bi;
+  sv[t] = best;
+  si[t] = bi;
+  __syncthreads();
+  for (int half = 128; half > 0; half >>= 1) {
+    if (t < half) {
+      const T v = sv[t + half];
+      const uint32_t i = si[t + half];
+      // equal values: the smaller column wins
+      if (i != NONE && (si[t] == NONE || v > sv[t] || (v == sv[t] && i < si[t]))) {
+        sv[t] = v;
+        si[t] = i;
+      }
+    }
+    __syncthreads();
+  }
+  if (t == 0) y.at(r, 0) = si[0];
 }
 
 inline dim3 grid1d(int64_t n) { return dim3((unsigned)((n + 255) / 256)); }
@@ -591,11 +624,12 @@ int bn_argmax(const bn_view *x, const bn_view *y, void *stream) {
   if ((st = require_device("argmax", {x, y}))) return st;
   if ((st = ensure_device())) return st;
   if (x->h == 0 || x->w == 0) return BN_OK;
+  if (x->h > 0x7fffffff) return fail(BN_ERR_UNSUPPORTED, "argmax: too many rows");
   if (x->dtype == BN_F32)
-    hipLaunchKernelGGL(argmax_kernel<float>, grid1d(x->h), dim3(256), 0, as_stream(stream),
+    hipLaunchKernelGGL(argmax_kernel<float>, dim3((unsigned)x->h), dim3(256), 0, as_stream(stream),
                        dview<const float>(x), dview<uint32_t>(y));
   else
-    hipLaunchKernelGGL(argmax_kernel<uint32_t>, grid1d(x->h), dim3(256), 0, as_stream(stream),
+    hipLaunchKernelGGL(argmax_kernel<uint32_t>, dim3((unsigned)x->h), dim3(256), 0, as_stream(stream),
                        dview<const uint32_t>(x), dview<uint32_t>(y));
   BN_LAUNCH_CHECK();
   return BN_OK;

@@ -377,3 +377,46 @@ def test_linear_rope_empty_rows_is_noop():
     w = torch.randn((64, 128), device="cuda")
     y = B.linear_rope(x, w, rope_cols=64)
     assert y.shape == (0, 128)
+
+
+def _argmax_sequential(row):
+    """The reference's rule (op_reduction.cuh:36-92 with MaxAccumFunc): the
+    accumulator starts at column 0 and takes x when x > accumulator."""
+    best, bi = row[0], 0
+    for c in range(1, len(row)):
+        if row[c] > best:
+            best, bi = row[c], c
+    return bi
+
+
+def test_argmax_rows_ties_nan_strided():
+    r = rng(12)
+    a = r.standard_normal((7, 32000)).astype(np.float32)
+    a[1, [5, 17000, 31999]] = 9.0                 # ties: the first one
+    a[2, 0] = np.nan                              # NaN at column 0: index 0
+    a[3, [3, 300]] = np.nan                       # NaN elsewhere never wins
+    a[3, 20000] = 7.0
+    a[4, :] = -np.inf                             # all equal: index 0
+    a[5, :] = 1.0
+    a[5, 0] = 0.5                                 # equal maxima after column 0: first one
+    a[6, 31999] = 50.0                            # maximum in the last column
+    ad = dev(a)
+    am = torch.empty((7, 1), dtype=torch.int32, device="cuda")
+    B.call("bn_argmax", V(ad), V(am), S0)
+    want = [_argmax_sequential(row) for row in a]
+    assert want[1] == 5 and want[2] == 0 and want[3] == 20000 and want[4] == 0 and want[5] == 1
+    np.testing.assert_array_equal(host(am)[:, 0], want)
+    # strided view (every other column of a wider buffer) and one short row
+    wide = dev(np.repeat(a[:, :1000], 2, axis=1))
+    B.call("bn_argmax", V(wide[:, ::2]), V(am), S0)
+    np.testing.assert_array_equal(host(am)[:, 0], [_argmax_sequential(row) for row in a[:, :1000]])
+    one = torch.empty((1, 1), dtype=torch.int32, device="cuda")
+    B.call("bn_argmax", V(ad[6:7, :1]), V(one), S0)
+    assert int(one.item()) == 0
+    # uint32 input
+    u = r.integers(0, 1 << 31, (3, 5000)).astype(np.int32)
+    u[0, [10, 4000]] = (1 << 31) - 1
+    ud = torch.from_numpy(u).cuda()
+    um = torch.empty((3, 1), dtype=torch.int32, device="cuda")
+    B.call("bn_argmax", V(ud), V(um), S0)
+    np.testing.assert_array_equal(host(um)[:, 0], [_argmax_sequential(row) for row in u])
