@@ -32,6 +32,9 @@ namespace {
 
 constexpr int HD = 64;
 constexpr int NT = 8;  // keys per lane group between softmax rescales
+#ifndef BN_DECODE_SINGLE_XCD
+#define BN_DECODE_SINGLE_XCD 1  // single pass: one KV head's query heads on one XCD
+#endif
 #ifndef BN_DECODE_SINGLE_NT
 #define BN_DECODE_SINGLE_NT 10  // single pass: up to 640 keys (16 waves x 4 groups x 10) in one load round
 #endif
@@ -92,7 +95,12 @@ __global__ __launch_bounds__(64 * WV) void decode_split_kernel(DecodeParams p) {
   const int grp = lane / LPK;  // key slot within the wave
   static_assert(!SINGLE || G == 1, "single pass: one query head per workgroup");
   const int split = SINGLE ? 0 : blockIdx.x % p.n_split;
-  const int bg = SINGLE ? blockIdx.x : blockIdx.x / p.n_split;
+  // SINGLE: consecutive (sequence, query head) units -- the query heads of one
+  // KV head -- go to one XCD (workgroups are dealt to the 8 XCDs in turn), so
+  // they read that KV head's cache rows from one L2
+  int bg = SINGLE ? blockIdx.x : blockIdx.x / p.n_split;
+  if (SINGLE && BN_DECODE_SINGLE_XCD && (gridDim.x & 7) == 0)
+    bg = (blockIdx.x & 7) * (gridDim.x >> 3) + (blockIdx.x >> 3);
   const int units = SINGLE ? p.n_heads : p.n_kv_heads;
   const int b = bg / units;
   // KV head g; query heads h0 .. h0 + G - 1
