@@ -300,11 +300,18 @@ __global__ __launch_bounds__(256) void argmax_kernel(DView<const T> x, DView<uin
   }
   T best = T{};
   uint32_t bi = NONE;
-  for (int c = t; c < x.w; c += 256) {
-    const T v = x.at(r, c);
-    if (!is_nan_val(v) && (bi == NONE || v > best)) {
-      best = v;
-      bi = (uint32_t)c;
+  constexpr int U = 8;  // loads in flight per thread; columns still visited in order
+  for (int c0 = t; c0 < x.w; c0 += 256 * U) {
+    T v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) v[u] = c0 + 256 * u < x.w ? x.at(r, c0 + 256 * u) : T{};
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int c = c0 + 256 * u;
+      if (c < x.w && !is_nan_val(v[u]) && (bi == NONE || v[u] > best)) {
+        best = v[u];
+        bi = (uint32_t)c;
+      }
     }
   }
   sv[t] = best;
