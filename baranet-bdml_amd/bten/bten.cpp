@@ -702,8 +702,15 @@ PYBIND11_MODULE(bten, m) {
 
   // ------------------------------------------------------ runtime / pool
   m.def("synchronize", []() { check(bn_stream_synchronize(g_stream)); });
-  m.def("set_stream", [](uintptr_t s) { g_stream = reinterpret_cast<void *>(s); }, py::arg("stream"),
-        "Launch on this hipStream_t handle (0 = legacy default stream)");
+  // Tensors free stream-ordered on the stream current at their destruction.
+  // Switching streams first waits for the outgoing stream, so every kernel
+  // that touched a tensor has finished or is ordered before its free.
+  m.def("set_stream", [](uintptr_t s) {
+          void *next = reinterpret_cast<void *>(s);
+          if (next != g_stream) check(bn_stream_synchronize(g_stream));
+          g_stream = next;
+        }, py::arg("stream"),
+        "Launch on this hipStream_t handle (0 = legacy default stream); waits for the current stream first");
   m.def("get_stream", []() { return reinterpret_cast<uintptr_t>(g_stream); });
   m.def("pool_stats", []() {
     bn_pool_stats s;

@@ -866,7 +866,7 @@ template <typename T>
 __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeParams p) {
   // one thread per 4 consecutive d of one (sequence, head); the partial loads
   // of 8 chunks are issued together with the length load (slots past the
-  // valid chunks read an in-range partial and get weight 0)
+  // valid chunks read an in-range record and are skipped in the merge)
   const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (idx >= (int64_t)p.batch * p.n_heads * (HD / 4)) return;
   const int d0 = (int)(idx % (HD / 4)) * 4;
@@ -898,11 +898,18 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeParams p) {
     const float fo = __builtin_amdgcn_exp2f(M - mu);  // M = -inf -> 0
     L *= fo;
     A[0] *= fo; A[1] *= fo; A[2] *= fo; A[3] *= fo;
+    // slots past the valid chunks hold whatever the workspace held before
+    // (possibly Inf or NaN): they are skipped by a select, never multiplied
+    // by a zero weight
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const float f = s0 + j < nvalid ? __builtin_amdgcn_exp2f(ms[j] - mu) : 0.f;
-      L += ls[j] * f;
-      A[0] += as[j].x * f; A[1] += as[j].y * f; A[2] += as[j].z * f; A[3] += as[j].w * f;
+      const bool ok = s0 + j < nvalid;
+      const float f = __builtin_amdgcn_exp2f(ms[j] - mu);
+      L = ok ? fmaf(ls[j], f, L) : L;
+      A[0] = ok ? fmaf(as[j].x, f, A[0]) : A[0];
+      A[1] = ok ? fmaf(as[j].y, f, A[1]) : A[1];
+      A[2] = ok ? fmaf(as[j].z, f, A[2]) : A[2];
+      A[3] = ok ? fmaf(as[j].w, f, A[3]) : A[3];
     }
     M = mx;
   };

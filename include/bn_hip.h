@@ -281,8 +281,9 @@ int bn_llama_decode(const bn_llama_config *config, const float *embed,
  * row of bn_gqa_prefill with seq_offset = seq_lens[b]-1 over keys
  * [0, seq_lens[b]).  q, o: [batch, n_heads, head_dim] contiguous; caches:
  * [batch, max_len, n_kv_heads, head_dim] contiguous; seq_lens: device int32
- * [batch], each in [1, max_len] (checked on the device: out-of-range lengths
- * are clamped and reported as zeros).  workspace: device memory of
+ * [batch], each in [1, max_len] (read on the device: a length <= 0 gives a
+ * zero output row, a length above max_len is treated as max_len, i.e. the
+ * whole cache is attended).  workspace: device memory of
  * bn_gqa_decode_workspace_size() bytes (NULL: taken from the pool when the
  * call needs it); single-pass calls use none: bf16 caches with
  * batch*n_kv_heads >= the device's compute units, fp32 caches of at most 1024

@@ -247,6 +247,31 @@ def test_decode_workspace_reuse(dtype, Hkv):
             assert_close(got[b:b + 1], ref, TOL[dtype], f"call {call} b={b} len={Lb}")
 
 
+@pytest.mark.parametrize("dtype,H,Hkv,L", [("bf16", 32, 4, 3000),   # whole-row split kernel
+                                           ("bf16", 16, 2, 3000),   # per-KV-head split kernel
+                                           ("f32", 32, 4, 3000)])   # fp32 split kernel
+def test_decode_workspace_holding_nan(dtype, H, Hkv, L):
+    """A reused workspace may hold anything (NaN, Inf) in the partial slots of
+    chunks past a sequence's length: the combine never lets them reach the
+    output.  Short ragged lengths leave most chunk slots unwritten."""
+    Bn = 5
+    lens = np.array([1, 129, 3000, 40, 700], np.int32)
+    ws = B.decode_workspace(Bn, L, H)
+    ws.view(torch.float32).fill_(float("nan"))
+    ws.view(torch.float32)[1::7] = float("inf")
+    q = draw((Bn, H, 64), 60, dtype)
+    kc = draw((Bn, L, Hkv, 64), 61, dtype)
+    vc = draw((Bn, L, Hkv, 64), 62, dtype)
+    got = host(B.gqa_decode(dev(q, TD[dtype]), dev(kc, TD[dtype]), dev(vc, TD[dtype]),
+                            torch.from_numpy(lens).cuda(), scale=0.125, workspace=ws))
+    assert np.all(np.isfinite(got))
+    for b in range(Bn):
+        Lb = int(lens[b])
+        ref = O.gqa_decode(q[b:b + 1], kc[b:b + 1, :Lb], vc[b:b + 1, :Lb],
+                           np.array([Lb], np.int32), 0.125)
+        assert_close(got[b:b + 1], ref, TOL[dtype], f"b={b} len={Lb}")
+
+
 @pytest.mark.parametrize("ragged", [False, True])
 def test_decode_baseline_shape(ragged):
     """config 3: B=64, bf16 cache of 4096, 32/4 heads; ragged lengths in [512, 4096]."""

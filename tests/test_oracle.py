@@ -204,6 +204,43 @@ def test_softmax_backward_analytic():
     assert relerr(O.softmax_backward(y, dy), ref) < 1e-5
 
 
+@pytest.mark.parametrize("rows,w,causal,off", [(6, 50, False, 0), (9, 300, True, 0),
+                                               (4, 700, True, 400), (5, 33, True, -2)])
+def test_softmax_backward_vs_torch_autograd(rows, w, causal, off):
+    """op_softmax_backward (op_softmax.cuh:182-246) pinned by torch fp64
+    autograd through a masked softmax: dx = d/dx <softmax(x), dy>.  Masked
+    positions get exactly zero gradient (y = 0 there)."""
+    r = rng(31)
+    x = (2 * r.standard_normal((rows, w))).astype(np.float32)
+    dy = r.standard_normal((rows, w)).astype(np.float32)
+    xt = torch.from_numpy(x.astype(np.float64)).requires_grad_(True)
+    if causal:
+        vis = torch.arange(w)[None, :] <= (torch.arange(rows)[:, None] + off)
+        z = torch.where(vis, xt, torch.tensor(float("-inf"), dtype=torch.float64))
+        yt = torch.softmax(z, dim=1)
+        yt = torch.where(vis, yt, torch.zeros((), dtype=torch.float64))  # fully masked rows: 0
+    else:
+        yt = torch.softmax(xt, dim=1)
+    (yt * torch.from_numpy(dy.astype(np.float64))).sum().backward()
+    want = xt.grad.numpy()
+    y = O.softmax(x, causal, off)
+    got = O.softmax_backward(y, dy)
+    assert relerr(got, want) < 1e-5
+    if causal:
+        assert np.all(got[~vis.numpy()] == 0.0)
+
+
+def test_softmax_backward_planted_slip_fails_autograd_pin():
+    # a softmax backward that drops the y * sum(y * dy) term must miss the pin
+    r = rng(32)
+    x = r.standard_normal((3, 40)).astype(np.float32)
+    dy = r.standard_normal((3, 40)).astype(np.float32)
+    xt = torch.from_numpy(x.astype(np.float64)).requires_grad_(True)
+    (torch.softmax(xt, 1) * torch.from_numpy(dy.astype(np.float64))).sum().backward()
+    y = O.softmax(x).astype(np.float64)
+    assert relerr(y * dy, xt.grad.numpy()) > 1e-2
+
+
 # ---------------------------------------------------------------- matmul / views
 def test_matmul_and_views():
     r = rng(10)
