@@ -106,6 +106,7 @@ def lib():
                              i, i, i, vp, vp, sz, vp], i),
         "bn_gqa_decode_workspace_size": ([i, i, i, i], sz),
         "bn_gqa_decode": ([i, vp, vp, vp, vp, vp] + [i] * 5 + [f, vp, sz, vp], i),
+        "bn_gqa_decode_noalloc": ([i, vp, vp, vp, vp, vp] + [i] * 5 + [f, vp], i),
     }
     for name, (args, res) in sig.items():
         fn = getattr(L, name)

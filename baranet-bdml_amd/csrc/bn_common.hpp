@@ -38,6 +38,11 @@ inline hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s);
 
 // Makes sure the library's device is current on the calling thread.
 int ensure_device();
+// The device bn_init selected (valid after ensure_device()).
+int library_device();
+// Looks up, once per device, the device address of the decode scratch array
+// (bn_decode.hip); called by bn_init with `device` current.
+int decode_scratch_setup(int device);
 // Compute units of the library's device (0 if the query fails); call after
 // ensure_device().
 int device_cu_count();

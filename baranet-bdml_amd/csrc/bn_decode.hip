@@ -21,7 +21,15 @@
 //     with the log-sum-exp rule: in-wave by shuffles, in-workgroup through LDS,
 //     across chunks by a small combine kernel over (m, l, acc) partials.
 // Scores live in the log2 domain: s = (q.k) * scale*log2(e), p = exp2(s - m).
+#include <mutex>
+
 #include "bn_common.hpp"
+
+// Chunk partials of bn_gqa_decode_noalloc: a file-scope device array, one
+// copy per GPU, held until the process ends.  Host code never passes its name
+// to a kernel (on the host the name is only a stand-in); it uses the device
+// address hipGetSymbolAddress returns for the current device.
+static __device__ __align__(256) float scratch[BN_GQA_DECODE_SCRATCH_BYTES / sizeof(float)];
 
 #ifndef BN_DECODE_NT
 #define BN_DECODE_NT 1  // K/V cache loads non-temporal: streamed once, kept out of L2/MALL (+24% on config 3)
@@ -989,6 +997,35 @@ int launch_decode(const DecodeParams &p, int G, hipStream_t s) {
 }
 
 }  // namespace
+
+// Device address of `scratch` per device, looked up once per device by
+// bn_init (with that device current).  Each GPU holds its own copy of the
+// array at its own address.
+constexpr int kMaxScratchDevices = 64;
+static std::mutex g_scratch_mu;
+static void *g_scratch_ptr[kMaxScratchDevices];
+
+int decode_scratch_setup(int device) {
+  if (device < 0 || device >= kMaxScratchDevices)
+    return fail(BN_ERR_UNSUPPORTED, "bn_init: device " + std::to_string(device) +
+                                        " above the decode scratch table (" +
+                                        std::to_string(kMaxScratchDevices) + " devices)");
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (g_scratch_ptr[device]) return BN_OK;
+  void *ptr = nullptr;
+  BN_HIP_TRY(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+  if (!ptr) return fail(BN_ERR_HIP, "bn_init: decode scratch has no device address");
+  g_scratch_ptr[device] = ptr;
+  return BN_OK;
+}
+
+namespace {
+void *decode_scratch(int device) {
+  if (device < 0 || device >= kMaxScratchDevices) return nullptr;
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  return g_scratch_ptr[device];
+}
+}  // namespace
 }  // namespace bn
 
 using namespace bn;
@@ -1003,11 +1040,18 @@ size_t bn_gqa_decode_workspace_size(int batch, int max_len, int n_heads, int hea
   return (size_t)batch * n_heads * n_split * (HD + 2) * sizeof(float);
 }
 
-int bn_gqa_decode(int dtype, const void *q, const void *k_cache, const void *v_cache,
-                  const int32_t *seq_lens, void *o, int batch, int max_len, int n_heads,
-                  int n_kv_heads, int head_dim, float scale, void *workspace,
-                  size_t workspace_bytes, void *stream) {
-  const char *op = "GQA decode";
+}  // extern "C"
+
+namespace bn {
+namespace {
+// bn_gqa_decode and bn_gqa_decode_noalloc: the same validation, kernels and
+// launch shapes; they differ only in where the split-K partials live (the
+// caller's workspace or the pool, against the file-scope scratch array).
+int gqa_decode_impl(int dtype, const void *q, const void *k_cache, const void *v_cache,
+                    const int32_t *seq_lens, void *o, int batch, int max_len, int n_heads,
+                    int n_kv_heads, int head_dim, float scale, void *workspace,
+                    size_t workspace_bytes, bool noalloc, void *stream) {
+  const char *op = noalloc ? "GQA decode (no allocation)" : "GQA decode";
   if (dtype != BN_F32 && dtype != BN_BF16)
     return fail(BN_ERR_UNSUPPORTED, std::string(op) + ": dtype must be F32 or BF16");
   if (batch < 0 || max_len < 0)
@@ -1081,12 +1125,23 @@ int bn_gqa_decode(int dtype, const void *q, const void *k_cache, const void *v_c
   p.n_split = (max_len + p.chunk - 1) / p.chunk;
   p.c = scale * 1.4426950408889634f;
   const size_t need = (size_t)batch * n_heads * p.n_split * (HD + 2) * sizeof(float);
+  if (noalloc && need > (size_t)BN_GQA_DECODE_SCRATCH_BYTES)
+    return fail(BN_ERR_UNSUPPORTED, std::string(op) + ": the call needs " + std::to_string(need) +
+                                        " bytes of chunk partials, above the " +
+                                        std::to_string((size_t)BN_GQA_DECODE_SCRATCH_BYTES) +
+                                        "-byte scratch");
   int st = ensure_device();
   if (st) return st;
   hipStream_t s = as_stream(stream);
   void *ws = workspace;
   bool own = false;
-  if (!ws) {
+  if (noalloc) {
+    // every record the combine reads is written by this call's split kernel
+    // first, so the scratch needs no clearing
+    ws = decode_scratch(library_device());
+    if (!ws) return fail(BN_ERR_HIP, std::string(op) + ": scratch address not set up for device " +
+                                         std::to_string(library_device()));
+  } else if (!ws) {
     if ((st = bn_alloc(&ws, need, stream))) return st;
     own = true;
   }
@@ -1097,6 +1152,25 @@ int bn_gqa_decode(int dtype, const void *q, const void *k_cache, const void *v_c
     if (st == BN_OK) st = st2;
   }
   return st;
+}
+}  // namespace
+}  // namespace bn
+
+extern "C" {
+
+int bn_gqa_decode(int dtype, const void *q, const void *k_cache, const void *v_cache,
+                  const int32_t *seq_lens, void *o, int batch, int max_len, int n_heads,
+                  int n_kv_heads, int head_dim, float scale, void *workspace,
+                  size_t workspace_bytes, void *stream) {
+  return gqa_decode_impl(dtype, q, k_cache, v_cache, seq_lens, o, batch, max_len, n_heads,
+                         n_kv_heads, head_dim, scale, workspace, workspace_bytes, false, stream);
+}
+
+int bn_gqa_decode_noalloc(int dtype, const void *q, const void *k_cache, const void *v_cache,
+                          const int32_t *seq_lens, void *o, int batch, int max_len, int n_heads,
+                          int n_kv_heads, int head_dim, float scale, void *stream) {
+  return gqa_decode_impl(dtype, q, k_cache, v_cache, seq_lens, o, batch, max_len, n_heads,
+                         n_kv_heads, head_dim, scale, nullptr, 0, true, stream);
 }
 
 }  // extern "C"

@@ -43,6 +43,10 @@ static int init_locked(int device) {
     return fail(BN_ERR_INVALID_ARG, "bn_init: device " + std::to_string(device) +
                                         " out of range (" + std::to_string(n) + " devices)");
   BN_HIP_TRY(hipSetDevice(device));
+  // the no-allocation decode entry point's scratch array: its address on
+  // this device, looked up once while the device is current
+  int st = decode_scratch_setup(device);
+  if (st != BN_OK) return st;
   hipMemPool_t pool = nullptr;
   BN_HIP_TRY(hipDeviceGetDefaultMemPool(&pool, device));
   uint64_t threshold = UINT64_MAX;  // keep freed memory cached in the pool
@@ -67,6 +71,8 @@ int ensure_device() {
   }
   return BN_OK;
 }
+
+int library_device() { return g_device; }
 
 int device_cu_count() {
   static int cached_device = -1, cached_count = 0;

@@ -296,6 +296,24 @@ int bn_gqa_decode(int dtype, const void *q, const void *k_cache,
                   int head_dim, float scale, void *workspace,
                   size_t workspace_bytes, void *stream);
 
+/* No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): bn_gqa_decode with the same arguments, kernels and
+ * results, minus the workspace.  Its split-K chunk partials live in a
+ * file-scope device array of BN_GQA_DECODE_SCRATCH_BYTES per GPU (held until
+ * the process ends; its address is looked up once per device by bn_init).
+ * It calls no hipMalloc, hipFree or pool allocation; a call whose partials
+ * would exceed the array fails with BN_ERR_UNSUPPORTED before any device
+ * work.  Every call on one GPU shares that GPU's array and leaves its last
+ * contents there (nothing needs clearing: each call writes every record it
+ * reads), so calls that overlap on one GPU -- on different streams, or from
+ * different threads -- race; serialise them. */
+#define BN_GQA_DECODE_SCRATCH_BYTES (32u << 20)
+int bn_gqa_decode_noalloc(int dtype, const void *q, const void *k_cache,
+                          const void *v_cache, const int32_t *seq_lens, void *o,
+                          int batch, int max_len, int n_heads, int n_kv_heads,
+                          int head_dim, float scale, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -128,6 +128,35 @@ def test_decode_validation(kw, status):
     assert m.startswith("GQA decode:")
 
 
+@pytest.mark.parametrize("kw,status", [
+    (dict(H=24), B.BN_ERR_UNSUPPORTED),
+    (dict(D=32), B.BN_ERR_UNSUPPORTED),
+    (dict(lens=0), B.BN_ERR_INVALID_ARG),
+    (dict(q=0x1008), B.BN_ERR_UNSUPPORTED),
+])
+def test_decode_noalloc_validation(kw, status):
+    # the no-allocation variant validates exactly as bn_gqa_decode does
+    a = dict(dt=B.BN_BF16, q=0x1000, k=0x2000, v=0x3000, lens=0x5000, o=0x4000, B=64,
+             L=4096, H=32, Hkv=4, D=64, sc=0.125)
+    a.update(kw)
+    s, m = st("bn_gqa_decode_noalloc", a["dt"], a["q"], a["k"], a["v"], a["lens"], a["o"],
+              a["B"], a["L"], a["H"], a["Hkv"], a["D"], a["sc"], None)
+    assert s == status, m
+    assert m.startswith("GQA decode (no allocation):")
+
+
+def test_decode_noalloc_refuses_partials_above_scratch():
+    """fp32 split path: 16 sequences of 2^20 keys in 1024-key chunks need
+    16*32*1024*66*4 bytes of partials, above the 32 MiB array; the refusal
+    happens on the host before any device call (fake pointers, no GPU)."""
+    s, m = st("bn_gqa_decode_noalloc", B.BN_F32, 0x1000, 0x2000, 0x3000, 0x5000, 0x4000,
+              16, 1 << 20, 32, 4, 64, 0.125, None)
+    assert s == B.BN_ERR_UNSUPPORTED, m
+    assert m == ("GQA decode (no allocation): the call needs 138412032 bytes of chunk "
+                 "partials, above the 33554432-byte scratch"), m
+    assert 16 * 32 * 1024 * 66 * 4 == 138412032
+
+
 def test_decode_workspace_size():
     L = B.lib()
     n = L.bn_gqa_decode_workspace_size(64, 4096, 32, 64)
