@@ -95,6 +95,9 @@ def lib():
         "bn_binary": ([i, V, V, V, vp], i), "bn_unary": ([i, V, f, V, vp], i),
         "bn_unary_backward": ([i, V, V, V, vp], i), "bn_fill": ([V, C.c_double, vp], i),
         "bn_sum": ([V, V, i, vp], i), "bn_argmax": ([V, V, vp], i), "bn_copy": ([V, V, vp], i),
+        "bn_fill_uniform": ([V, f, f, C.c_uint64, vp], i),
+        "bn_embedding": ([V, vp, i, V, vp], i),
+        "bn_mem_get_info": ([C.POINTER(sz), C.POINTER(sz)], i),
         "bn_gqa_prefill": ([i, vp, vp, vp, vp] + [i] * 6 + [i64] * 6 + [f, i, i, vp], i),
         "bn_gqa_prefill_lse": ([i, vp, vp, vp, vp, vp] + [i] * 6 + [i64] * 6 + [f, i, i, vp], i),
         "bn_gqa_prefill_backward_workspace_size": ([i] * 7, sz),

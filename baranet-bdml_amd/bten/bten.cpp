@@ -7,8 +7,8 @@
 // Same module, class, method and argument names and defaults as the
 // reference, so mygrad/llama callers run unchanged:
 //   TensorF / TensorU32 (py_tensor_shim.hh:184-254), float-only ops
-//   (:256-310), randgen_seed (bindings.cu:16-18), LLaMAConfig
-//   (llama_bindings.hpp:99-111).
+//   (:256-310), randgen_seed (bindings.cu:16-18), LLaMAConfig and
+//   LLaMAModelCpp (llama_bindings.hpp:31-122).
 // Additions (new names only): TensorBF16, Tensor*.rmsnorm_rope, gqa_prefill,
 // gqa_prefill_lse, gqa_prefill_backward,
 // gqa_decode, repeat_kv, add_rmsnorm, silu_mul, pool_stats / pool_trim / pool_set_limit,
@@ -22,6 +22,7 @@
 #include <pybind11/numpy.h>
 #include <pybind11/pybind11.h>
 
+#include <chrono>
 #include <cmath>
 #include <cstdint>
 #include <cstdlib>
@@ -565,6 +566,265 @@ void bind_float_ops(py::class_<PyTensor<DT>> &cls) {
          py::arg("head_dim") = 64, py::arg("theta") = 10000.0f);
 }
 
+// ---------------------------------------------------------------- LLaMA
+// Same fields and defaults as llama_config.hpp:13-32 (TinyLLaMA-1.1B).
+struct LlamaCfg {
+  int vocab_size = 32000, hidden_size = 2048, intermediate_size = 5632, num_hidden_layers = 22,
+      num_attention_heads = 32, num_key_value_heads = 4, max_position_embeddings = 2048;
+  float rms_norm_eps = 1e-6f, rope_theta = 10000.0f;
+  int head_dim() const { return hidden_size / num_attention_heads; }
+  void validate() const {  // llama_config.hpp:42-51
+    if (num_attention_heads <= 0 || hidden_size % num_attention_heads != 0)
+      throw std::runtime_error("hidden_size must be divisible by num_attention_heads");
+    if (num_key_value_heads <= 0 || num_attention_heads % num_key_value_heads != 0)
+      throw std::runtime_error("num_attention_heads must be divisible by num_key_value_heads");
+  }
+  // llama_config.hpp:82-105, in size_t throughout (the reference forms
+  // vocab_size * hidden_size in int)
+  size_t count_parameters() const {
+    const size_t h = hidden_size, kv = (size_t)num_key_value_heads * head_dim(),
+                 I = intermediate_size, V = vocab_size;
+    const size_t per_layer = h * h + 2 * h * kv + h * h + 3 * h * I + 2 * h;
+    return V * h + per_layer * (size_t)num_hidden_layers + h + h * V;
+  }
+  std::string to_string() const {  // llama_config.hpp:68-78
+    return "LLaMAConfig(\n  vocab_size=" + std::to_string(vocab_size) + ",\n  hidden_size=" +
+           std::to_string(hidden_size) + ",\n  num_layers=" + std::to_string(num_hidden_layers) +
+           ",\n  num_heads=" + std::to_string(num_attention_heads) + ",\n  num_kv_heads=" +
+           std::to_string(num_key_value_heads) + ",\n  intermediate_size=" +
+           std::to_string(intermediate_size) + "\n)";
+  }
+};
+
+// Host twin of the device uniform fill (bn_fill_uniform): SplitMix64 of the
+// seed and the logical index, so host and device models get equal weights.
+float uniform01_host(uint64_t seed, uint64_t index) {
+  uint64_t z = seed + (index + 1) * 0x9E3779B97F4A7C15ull;
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  z ^= z >> 31;
+  return (float)(uint32_t)(z >> 40) * (1.0f / 16777216.0f);
+}
+
+void fill_uniform(TF &t, float lo, float hi, uint64_t seed) {
+  if (t.on_device) {
+    bn_view v = t.view();
+    check(bn_fill_uniform(&v, lo, hi, seed, g_stream));
+    return;
+  }
+  float *p = (float *)t.base();
+  for (int64_t i = 0; i < (int64_t)t.h * t.w; ++i)
+    p[i] = std::fma(uniform01_host(seed, (uint64_t)i), hi - lo, lo);
+}
+
+// LLaMAModel (llama_model.hpp:19-198) behind the PyLLaMAModel binding
+// (llama_bindings.hpp:31-96): token ids -> logits through the decoder layers
+// (llama_layers.hpp:241-272), all on the path's kernels.
+//   * Weights: embed_tokens and lm_head uniform in [-0.02, 0.02] as the
+//     reference fills them (llama_model.hpp:27,37; op_uniform_fill with the
+//     randgen_seed), norm weights ones; the projections, which the reference
+//     leaves uninitialised (bare cudaMalloc), get the same uniform fill.  Each
+//     tensor has its own stream of the seed.
+//   * Layout: Q|K|V and gate|up are stored concatenated ([hidden, (H+2Hkv)D],
+//     [hidden, 2I]) so each is one GEMM; weights() returns the reference's
+//     per-projection tensors as column views of them (loading through those
+//     views writes the model's weights).
+//   * attention = "fused_head" (default) computes the reference's chain as it
+//     is (llama_layers.hpp:96-109: Q K_rep^T over all heads at once, scale,
+//     causal softmax, @ V_rep); "per_head" runs per-head GQA on bn_gqa_prefill.
+//   * Embedding gathers on the device (bn_embedding) instead of copying the
+//     whole table to the host and back (llama_model.hpp:161-198).
+class LlamaModelCpp {
+ public:
+  LlamaModelCpp(const LlamaCfg &cfg, bool on_device, const std::string &attention)
+      : cfg_(cfg), on_device_(on_device) {
+    cfg_.validate();
+    if (attention != "fused_head" && attention != "per_head")
+      throw std::runtime_error("LLaMAModelCpp: attention must be 'fused_head' or 'per_head'");
+    per_head_ = attention == "per_head";
+    const int h = cfg_.hidden_size, kv = cfg_.num_key_value_heads * cfg_.head_dim(),
+              I = cfg_.intermediate_size;
+    uint64_t stream_id = 0;
+    auto uniform = [&](int rows, int cols) {
+      TF t(rows, cols, on_device_);
+      fill_uniform(t, -0.02f, 0.02f, g_randgen_seed * 0x100000001B3ull + (++stream_id));
+      return t;
+    };
+    auto ones = [&]() {
+      TF t(1, h, on_device_);
+      t.fill(1.0);
+      return t;
+    };
+    embed_ = uniform(cfg_.vocab_size, h);
+    for (int l = 0; l < cfg_.num_hidden_layers; ++l) {
+      Layer L;
+      L.ln1 = ones();
+      L.wqkv = uniform(h, h + 2 * kv);
+      L.wo = uniform(h, h);
+      L.ln2 = ones();
+      L.wgu = uniform(h, 2 * I);
+      L.wd = uniform(I, h);
+      layers_.push_back(std::move(L));
+    }
+    ln_f_ = ones();
+    lm_head_ = uniform(h, cfg_.vocab_size);
+    if (on_device_) check(bn_stream_synchronize(g_stream));
+  }
+
+  // llama_bindings.hpp:37-58: ids (batch,) -> logits (batch, vocab)
+  py::array forward(py::array_t<uint32_t, py::array::c_style | py::array::forcecast> ids) {
+    TF logits = run(ids);
+    return logits.to_numpy();
+  }
+
+  // llama_bindings.hpp:60-71 / llama_model.hpp:86-118: milliseconds of one
+  // forward (ids already on the device), host clock between stream syncs
+  float forward_timed(py::array_t<uint32_t, py::array::c_style | py::array::forcecast> ids) {
+    TU dev_ids = upload_ids(ids);
+    if (on_device_) check(bn_stream_synchronize(g_stream));
+    const auto t0 = std::chrono::steady_clock::now();
+    TF logits = run_device(dev_ids);
+    if (on_device_) check(bn_stream_synchronize(g_stream));
+    const auto t1 = std::chrono::steady_clock::now();
+    return std::chrono::duration<float, std::milli>(t1 - t0).count();
+  }
+
+  // llama_model.hpp:209-266: token id 1 in every row, warm-up, mean time
+  py::dict benchmark(int batch_size, int num_warmup, int num_iterations) {
+    if (batch_size <= 0 || num_iterations <= 0)
+      throw std::runtime_error("benchmark: batch_size and num_iterations must be positive");
+    py::array_t<uint32_t> ids(batch_size);
+    for (int i = 0; i < batch_size; ++i) ids.mutable_at(i) = 1;
+    for (int i = 0; i < num_warmup; ++i) run(ids);
+    float total = 0.f;
+    for (int i = 0; i < num_iterations; ++i) total += forward_timed(ids);
+    py::dict d;
+    const float ms = total / num_iterations;
+    d["forward_time_ms"] = ms;
+    d["tokens_per_second"] = batch_size * 1000.0f / ms;
+    d["memory_used_bytes"] = get_gpu_memory_usage();
+    d["num_parameters"] = count_parameters();
+    return d;
+  }
+
+  size_t count_parameters() const { return cfg_.count_parameters(); }
+
+  size_t get_gpu_memory_usage() const {  // llama_model.hpp:125-131
+    if (!on_device_) return 0;
+    size_t free_b = 0, total_b = 0;
+    check(bn_mem_get_info(&free_b, &total_b));
+    return total_b - free_b;
+  }
+
+  // Additive: the weights as TensorF views under the reference's accessor
+  // names (llama_model.hpp:140-143, llama_layers.hpp accessors).
+  py::dict weights() const {
+    const int h = cfg_.hidden_size, kv = cfg_.num_key_value_heads * cfg_.head_dim(),
+              I = cfg_.intermediate_size;
+    py::dict d;
+    d["embed_tokens"] = embed_;
+    d["final_norm"] = ln_f_;
+    d["lm_head"] = lm_head_;
+    py::list layers;
+    for (const Layer &L : layers_) {
+      py::dict ld;
+      ld["input_layernorm"] = L.ln1;
+      ld["q_proj"] = L.wqkv.slice_view(0, h, 0, h);
+      ld["k_proj"] = L.wqkv.slice_view(0, h, h, h + kv);
+      ld["v_proj"] = L.wqkv.slice_view(0, h, h + kv, h + 2 * kv);
+      ld["o_proj"] = L.wo;
+      ld["post_attention_layernorm"] = L.ln2;
+      ld["gate_proj"] = L.wgu.slice_view(0, h, 0, I);
+      ld["up_proj"] = L.wgu.slice_view(0, h, I, 2 * I);
+      ld["down_proj"] = L.wd;
+      layers.append(ld);
+    }
+    d["layers"] = layers;
+    return d;
+  }
+
+ private:
+  struct Layer {
+    TF ln1, wqkv, wo, ln2, wgu, wd;
+  };
+  LlamaCfg cfg_;
+  bool on_device_;
+  bool per_head_ = false;
+  TF embed_, ln_f_, lm_head_;
+  std::vector<Layer> layers_;
+
+  TU upload_ids(const py::array_t<uint32_t, py::array::c_style | py::array::forcecast> &ids) {
+    if (ids.ndim() != 1) throw std::runtime_error("LLaMAModelCpp: input_ids must be 1-D (batch,)");
+    const int n = (int)ids.shape(0);
+    for (int i = 0; i < n; ++i)
+      if (ids.at(i) >= (uint32_t)cfg_.vocab_size)
+        throw std::runtime_error("LLaMAModelCpp: token id " + std::to_string(ids.at(i)) +
+                                 " outside the vocabulary of " + std::to_string(cfg_.vocab_size));
+    TU t(n, 1, on_device_);
+    if (n) t.upload_raw(ids.data());
+    return t;
+  }
+
+  TF run(const py::array_t<uint32_t, py::array::c_style | py::array::forcecast> &ids) {
+    return run_device(upload_ids(ids));
+  }
+
+  // llama_model.hpp:52-80 with the layer of llama_layers.hpp:241-272; each
+  // residual add runs fused with the RMSNorm that follows it (bn_add_rmsnorm:
+  // the same sum, then the same normalisation)
+  TF run_device(const TU &ids) {
+    const int n = ids.h, h = cfg_.hidden_size, D = cfg_.head_dim(),
+              kv = cfg_.num_key_value_heads * D, I = cfg_.intermediate_size,
+              G = cfg_.num_attention_heads / cfg_.num_key_value_heads;
+    const float eps = cfg_.rms_norm_eps, theta = cfg_.rope_theta;
+    // the first op on a host model is the reference's first throw
+    if (!on_device_) throw std::runtime_error("RMSNorm: only GPU implementation available");
+    if (n == 0) return TF(0, cfg_.vocab_size, true);
+    TF hdn(n, h, true);
+    {
+      bn_view tv = embed_.view(), ov = hdn.view();
+      check(bn_embedding(&tv, (const uint32_t *)ids.base(), n, &ov, g_stream));
+    }
+    TF x = rmsnorm<BN_F32>(hdn, layers_[0].ln1, eps);
+    for (size_t l = 0; l < layers_.size(); ++l) {
+      const Layer &L = layers_[l];
+      TF qkv = matmul(x, L.wqkv);
+      {  // RoPE on the Q and K columns, in place (one launch)
+        TF qk = qkv.slice_view(0, n, 0, h + kv);
+        bn_view v = qk.view();
+        check(bn_rope(&v, &v, 0, D, theta, g_stream));
+      }
+      TF q = qkv.slice_view(0, n, 0, h), k = qkv.slice_view(0, n, h, h + kv),
+         v = qkv.slice_view(0, n, h + kv, h + 2 * kv);
+      TF attn;
+      if (per_head_) {
+        attn = gqa_prefill<BN_F32>(q, k, v, 1, cfg_.num_attention_heads, cfg_.num_key_value_heads,
+                                   D, py::none(), true, 0);
+      } else {
+        TF krep = G > 1 ? repeat_kv<BN_F32>(k, G, D) : k;
+        TF vrep = G > 1 ? repeat_kv<BN_F32>(v, G, D) : v;
+        TF scores = matmul(q, krep.transpose());
+        TF scaled = unary(BN_MUL_SCALAR, scores, (float)(1.0 / std::sqrt((double)D)));
+        attn = matmul(softmax<BN_F32>(scaled, true, 0), vrep);
+      }
+      TF o = matmul(attn, L.wo);
+      TF x2 = hdn.like();
+      {
+        bn_view hv = hdn.view(), ov = o.view(), wv = L.ln2.view(), yv = x2.view();
+        check(bn_add_rmsnorm(&hv, &ov, &wv, &hv, &yv, eps, g_stream));  // hdn += o
+      }
+      TF gu = matmul(x2, L.wgu);
+      TF act = silu_mul<BN_F32>(gu.slice_view(0, n, 0, I), gu.slice_view(0, n, I, 2 * I));
+      TF mlp = matmul(act, L.wd);
+      const TF &next_w = l + 1 < layers_.size() ? layers_[l + 1].ln1 : ln_f_;
+      x = hdn.like();
+      bn_view hv = hdn.view(), mv = mlp.view(), wv = next_w.view(), yv = x.view();
+      check(bn_add_rmsnorm(&hv, &mv, &wv, &hv, &yv, eps, g_stream));  // hdn += mlp
+    }
+    return matmul(x, lm_head_);
+  }
+};
+
 }  // namespace
 
 PYBIND11_MODULE(bten, m) {
@@ -734,13 +994,9 @@ PYBIND11_MODULE(bten, m) {
   });
 
   // --------------------------------------------------------- LLaMAConfig
-  // Same fields and defaults as llama_config.hpp:13-32 (TinyLLaMA-1.1B).
-  struct Config {
-    int vocab_size = 32000, hidden_size = 2048, intermediate_size = 5632,
-        num_hidden_layers = 22, num_attention_heads = 32, num_key_value_heads = 4,
-        max_position_embeddings = 2048;
-    float rms_norm_eps = 1e-6f, rope_theta = 10000.0f;
-  };
+  // llama_bindings.hpp:99-111 (plus the eps/theta/max_position fields of
+  // llama_config.hpp:21-24, readable and writable here)
+  using Config = LlamaCfg;
   py::class_<Config>(m, "LLaMAConfig")
     .def(py::init<>())
     .def_readwrite("vocab_size", &Config::vocab_size)
@@ -752,22 +1008,28 @@ PYBIND11_MODULE(bten, m) {
     .def_readwrite("max_position_embeddings", &Config::max_position_embeddings)
     .def_readwrite("rms_norm_eps", &Config::rms_norm_eps)
     .def_readwrite("rope_theta", &Config::rope_theta)
-    .def("head_dim", [](const Config &c) { return c.hidden_size / c.num_attention_heads; })
+    .def("head_dim", &Config::head_dim)
     .def("num_kv_groups", [](const Config &c) { return c.num_attention_heads / c.num_key_value_heads; })
-    .def("validate", [](const Config &c) {
-      if (c.hidden_size % c.num_attention_heads != 0)
-        throw std::runtime_error("hidden_size must be divisible by num_attention_heads");
-      if (c.num_attention_heads % c.num_key_value_heads != 0)
-        throw std::runtime_error("num_attention_heads must be divisible by num_key_value_heads");
-      return true;
+    .def("validate", &Config::validate)
+    .def("count_parameters", &Config::count_parameters)
+    .def_static("tinyllama_1_1b", []() {
+      Config c;
+      c.validate();
+      return c;
     })
-    .def_static("tinyllama_1_1b", []() { return Config(); })
-    .def("__repr__", [](const Config &c) {
-      std::ostringstream o;
-      o << "LLaMAConfig(vocab_size=" << c.vocab_size << ", hidden_size=" << c.hidden_size
-        << ", intermediate_size=" << c.intermediate_size << ", num_hidden_layers="
-        << c.num_hidden_layers << ", num_attention_heads=" << c.num_attention_heads
-        << ", num_key_value_heads=" << c.num_key_value_heads << ")";
-      return o.str();
-    });
+    .def("__repr__", &Config::to_string);
+
+  // ------------------------------------------------------- LLaMAModelCpp
+  // llama_bindings.hpp:113-122; `attention` is additive (default: the
+  // reference's fused-head chain), weights() too
+  py::class_<LlamaModelCpp>(m, "LLaMAModelCpp")
+    .def(py::init<const Config &, bool, const std::string &>(), py::arg("config"),
+         py::arg("on_device") = true, py::arg("attention") = "fused_head")
+    .def("forward", &LlamaModelCpp::forward, py::arg("input_ids"))
+    .def("forward_timed", &LlamaModelCpp::forward_timed, py::arg("input_ids"))
+    .def("benchmark", &LlamaModelCpp::benchmark, py::arg("batch_size"), py::arg("num_warmup") = 5,
+         py::arg("num_iterations") = 100)
+    .def("count_parameters", &LlamaModelCpp::count_parameters)
+    .def("get_gpu_memory_usage", &LlamaModelCpp::get_gpu_memory_usage)
+    .def("weights", &LlamaModelCpp::weights);
 }

@@ -247,6 +247,28 @@ __global__ void fill_kernel(DView<T> y, T v) {
   y.at((int)(idx / y.w), (int)(idx % y.w)) = v;
 }
 
+// Uniform [lo, hi) fill from a counter-based generator: element (i, j) of an
+// h x w view gets the SplitMix64 output (Steele, Lea & Flood, "Fast
+// splittable pseudorandom number generators", OOPSLA 2014) of
+// seed + (i*w + j + 1) * 0x9E3779B97F4A7C15, whose top 24 bits scale to
+// [0, 1).  The value depends only on (seed, logical index): the same for any
+// launch shape, stride or device.
+__device__ __forceinline__ float uniform01(uint64_t seed, uint64_t index) {
+  uint64_t z = seed + (index + 1) * 0x9E3779B97F4A7C15ull;
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  z ^= z >> 31;
+  return (float)(uint32_t)(z >> 40) * (1.0f / 16777216.0f);
+}
+
+template <typename T>
+__global__ void fill_uniform_kernel(DView<T> y, float lo, float span, uint64_t seed) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (int64_t)y.h * y.w) return;
+  const float v = fmaf(uniform01(seed, (uint64_t)idx), span, lo);
+  Elem<T>::store(&y.at((int)(idx / y.w), (int)(idx % y.w)), v);
+}
+
 template <typename Tin, typename Tout>
 __global__ void copy_kernel(DView<const Tin> x, DView<Tout> y) {
   const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -596,6 +618,27 @@ int bn_fill(const bn_view *y, double value, void *stream) {
     hipLaunchKernelGGL(fill_kernel<bf16_t>, grid1d(n), dim3(256), 0, s, dview<bf16_t>(y),
                        (bf16_t)(u >> 16));
   }
+  BN_LAUNCH_CHECK();
+  return BN_OK;
+}
+
+int bn_fill_uniform(const bn_view *y, float lo, float hi, uint64_t seed, void *stream) {
+  const unsigned mask = (1u << BN_F32) | (1u << BN_BF16);
+  int st;
+  if ((st = check_view(y, "uniform fill", "tensor", mask))) return st;
+  if (!std::isfinite(lo) || !std::isfinite(hi) || !(hi > lo))
+    return fail(BN_ERR_INVALID_ARG, "uniform fill: need finite lo < hi");
+  if ((st = require_device("uniform fill", {y}))) return st;
+  if ((st = ensure_device())) return st;
+  const int64_t n = (int64_t)y->h * y->w;
+  if (n == 0) return BN_OK;
+  hipStream_t s = as_stream(stream);
+  if (y->dtype == BN_F32)
+    hipLaunchKernelGGL(fill_uniform_kernel<float>, grid1d(n), dim3(256), 0, s, dview<float>(y), lo,
+                       hi - lo, seed);
+  else
+    hipLaunchKernelGGL(fill_uniform_kernel<bf16_t>, grid1d(n), dim3(256), 0, s, dview<bf16_t>(y),
+                       lo, hi - lo, seed);
   BN_LAUNCH_CHECK();
   return BN_OK;
 }

@@ -25,6 +25,18 @@ __global__ __launch_bounds__(256) void embed_gather_kernel(const float *embed, c
   for (int i = threadIdx.x; i < hidden; i += 256) x[i] = row[i];
 }
 
+// out row r = table row ids[r] (one workgroup per row); an id outside the
+// table gives a zero row
+template <typename T>
+__global__ __launch_bounds__(256) void embed_rows_kernel(DView<const T> table, const uint32_t *ids,
+                                                         DView<T> out) {
+  const int r = blockIdx.x;
+  const uint32_t id = ids[r];
+  const bool ok = id < (uint32_t)table.h;
+  for (int j = threadIdx.x; j < out.w; j += 256)
+    out.at(r, j) = ok ? table.at((int)id, j) : T(0);
+}
+
 // lens[i] = first + i + 1 (the cache length after step i)
 __global__ __launch_bounds__(256) void fill_lens_kernel(int32_t *lens, int first, int n) {
   const int i = blockIdx.x * 256 + threadIdx.x;
@@ -218,4 +230,33 @@ extern "C" int bn_llama_decode(const bn_llama_config *c, const float *embed, con
     if (st == BN_OK) st = st2;
   }
   return st;
+}
+
+// LLaMAModel::embed (llama_model.hpp:161-198) copies the whole table to the
+// host, looks the rows up there and copies them back; this gathers on the
+// device.
+extern "C" int bn_embedding(const bn_view *table, const uint32_t *ids, int n, const bn_view *out,
+                            void *stream) {
+  const char *op = "embedding";
+  const unsigned mask = (1u << BN_F32) | (1u << BN_BF16);
+  int st;
+  if ((st = check_view(table, op, "table", mask))) return st;
+  if ((st = check_view(out, op, "output", mask))) return st;
+  if (n < 0) return fail(BN_ERR_SHAPE, std::string(op) + ": negative number of ids");
+  if (out->h != n || out->w != table->w)
+    return fail(BN_ERR_SHAPE, std::string(op) + ": output must be [n_ids, hidden]");
+  if (out->dtype != table->dtype) return fail(BN_ERR_UNSUPPORTED, std::string(op) + ": dtypes differ");
+  if ((st = require_device(op, {table, out}))) return st;
+  if (n == 0 || out->w == 0) return BN_OK;
+  if (!ids) return fail(BN_ERR_INVALID_ARG, std::string(op) + ": NULL ids");
+  if ((st = ensure_device())) return st;
+  hipStream_t s = as_stream(stream);
+  if (table->dtype == BN_F32)
+    hipLaunchKernelGGL(embed_rows_kernel<float>, dim3((unsigned)n), dim3(256), 0, s,
+                       dview<const float>(table), ids, dview<float>(out));
+  else
+    hipLaunchKernelGGL(embed_rows_kernel<bf16_t>, dim3((unsigned)n), dim3(256), 0, s,
+                       dview<const bf16_t>(table), ids, dview<bf16_t>(out));
+  BN_LAUNCH_CHECK();
+  return BN_OK;
 }

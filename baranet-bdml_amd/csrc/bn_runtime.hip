@@ -185,6 +185,14 @@ int bn_device_synchronize(void) {
   return BN_OK;
 }
 
+int bn_mem_get_info(size_t *free_bytes, size_t *total_bytes) {
+  if (!free_bytes || !total_bytes) return fail(BN_ERR_INVALID_ARG, "bn_mem_get_info: NULL output");
+  int st = ensure_device();
+  if (st) return st;
+  BN_HIP_TRY(hipMemGetInfo(free_bytes, total_bytes));
+  return BN_OK;
+}
+
 int bn_alloc(void **ptr, size_t bytes, void *stream) {
   if (!ptr) return fail(BN_ERR_INVALID_ARG, "bn_alloc: NULL output pointer");
   *ptr = nullptr;

@@ -63,6 +63,9 @@ int bn_stream_create(void **stream);
 int bn_stream_destroy(void *stream);
 int bn_stream_synchronize(void *stream);
 int bn_device_synchronize(void);
+/* Free and total device memory of the library's device: replaces the
+ * cudaMemGetInfo of LLaMAModel::get_gpu_memory_usage (llama_model.hpp:125-131). */
+int bn_mem_get_info(size_t *free_bytes, size_t *total_bytes);
 
 /* ------------------------------------------------------------- memory pool
  * Replaces CudaMemoryPool / PooledMemory (src/utils/memory_pool.cuh:15-125)
@@ -172,6 +175,16 @@ int bn_unary_backward(int op, const bn_view *x, const bn_view *dy,
                       const bn_view *dx, void *stream);
 /* op_const_fill; value is reinterpreted for U32 views. */
 int bn_fill(const bn_view *y, double value, void *stream);
+/* op_uniform_fill (op_elemwise.cuh:487-507; cuRAND there): values uniform in
+ * [lo, hi] (F32 or BF16), element (i, j) from a counter-based generator
+ * (SplitMix64) of seed and the logical index i*w + j, so the result does not
+ * depend on strides, launch shape or device. */
+int bn_fill_uniform(const bn_view *y, float lo, float hi, uint64_t seed, void *stream);
+/* LLaMAModel::embed (llama_model.hpp:161-198): out row r = table row ids[r];
+ * ids device uint32 [n]; table [vocab, hidden] and out [n, hidden] of one
+ * dtype (F32 or BF16).  An id >= vocab gives a zero row. */
+int bn_embedding(const bn_view *table, const uint32_t *ids, int n, const bn_view *out,
+                 void *stream);
 /* op_sum (axis 0 -> [1, w], axis 1 -> [h, 1]) and op_argmax (row-wise, U32). */
 int bn_sum(const bn_view *x, const bn_view *y, int axis, void *stream);
 int bn_argmax(const bn_view *x, const bn_view *y, void *stream);

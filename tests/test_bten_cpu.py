@@ -101,8 +101,82 @@ def test_defaults_match_reference_signatures():
     c = bten.LLaMAConfig.tinyllama_1_1b()
     assert (c.hidden_size, c.num_attention_heads, c.num_key_value_heads, c.head_dim(),
             c.num_kv_groups()) == (2048, 32, 4, 64, 8)
-    assert c.validate()
+    assert c.validate() is None            # void in llama_config.hpp:42-51
+    with pytest.raises(RuntimeError, match="divisible by num_key_value_heads"):
+        bad = bten.LLaMAConfig()
+        bad.num_key_value_heads = 5
+        bad.validate()
     bten.randgen_seed(1234)
+    bten.randgen_seed(42)
+
+
+def splitmix_uniform(seed, n):
+    # SplitMix64 (Steele, Lea & Flood 2014) of seed + (i+1)*golden, top 24 bits
+    M = (1 << 64) - 1
+    out = np.empty(n, np.float32)
+    for i in range(n):
+        z = (seed + (i + 1) * 0x9E3779B97F4A7C15) & M
+        z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & M
+        z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & M
+        z ^= z >> 31
+        out[i] = np.float32(z >> 40) * np.float32(1.0 / 16777216.0)
+    return out
+
+
+def small_cfg():
+    c = bten.LLaMAConfig()
+    (c.vocab_size, c.hidden_size, c.intermediate_size, c.num_hidden_layers,
+     c.num_attention_heads, c.num_key_value_heads) = (96, 128, 160, 2, 2, 1)
+    return c
+
+
+def test_llama_config_count_parameters_and_repr():
+    # llama_config.hpp:82-105 at TinyLLaMA-1.1B
+    c = bten.LLaMAConfig.tinyllama_1_1b()
+    h, kv, I, V, L = 2048, 256, 5632, 32000, 22
+    per_layer = h * h + 2 * h * kv + h * h + 3 * h * I + 2 * h
+    assert c.count_parameters() == V * h + L * per_layer + h + h * V == 1100048384
+    assert repr(c) == ("LLaMAConfig(\n  vocab_size=32000,\n  hidden_size=2048,\n  num_layers=22,\n"
+                       "  num_heads=32,\n  num_kv_heads=4,\n  intermediate_size=5632\n)")
+
+
+def test_llama_model_cpp_on_host():
+    """LLaMAModelCpp(config, on_device=False): built on the host (the
+    reference allocates host tensors), parameter count and memory as the
+    reference reports them, and forward raises where the reference's first
+    GPU-only op (op_rmsnorm, op_rmsnorm.cuh:148-150) throws."""
+    c = small_cfg()
+    m = bten.LLaMAModelCpp(c, False)
+    assert m.count_parameters() == c.count_parameters()
+    assert m.get_gpu_memory_usage() == 0
+    with pytest.raises(RuntimeError, match="RMSNorm: only GPU implementation available"):
+        m.forward(np.array([1, 2, 3], np.uint32))
+    w = m.weights()
+    assert len(w["layers"]) == 2
+    np.testing.assert_array_equal(w["final_norm"].to_numpy(), np.ones((1, 128), np.float32))
+    q = w["layers"][1]["q_proj"].to_numpy()
+    assert q.shape == (128, 128) and w["layers"][1]["k_proj"].shape == (128, 64)
+    assert w["layers"][0]["gate_proj"].shape == (128, 160)
+    emb = w["embed_tokens"].to_numpy()
+    assert emb.shape == (96, 128) and emb.min() >= -0.02 and emb.max() <= 0.02
+    # the uniform fill restated: lo + (hi - lo) * u with u from SplitMix64 of
+    # the tensor's seed stream (embed_tokens is stream 1 of randgen seed 42)
+    seed = (42 * 0x100000001B3 + 1) & ((1 << 64) - 1)
+    u = splitmix_uniform(seed, 96 * 128).astype(np.float64)
+    want = (u * np.float64(np.float32(0.02) - np.float32(-0.02)) + np.float64(np.float32(-0.02)))
+    np.testing.assert_array_equal(emb.ravel(), want.astype(np.float32))
+    # loading through a view writes the model's weight
+    w["layers"][0]["v_proj"].copy_from_numpy(np.full((128, 64), 0.5, np.float32))
+    assert np.all(m.weights()["layers"][0]["v_proj"].to_numpy() == 0.5)
+
+
+def test_llama_model_cpp_signature_defaults():
+    import re
+    doc = bten.LLaMAModelCpp.benchmark.__doc__
+    assert re.search(r"num_warmup: [^=,]*= 5\b", doc) and re.search(r"num_iterations: [^=,]*= 100\b", doc)
+    assert re.search(r"on_device: [^=,]*= True", bten.LLaMAModelCpp.__init__.__doc__)
+    with pytest.raises(RuntimeError, match="fused_head"):
+        bten.LLaMAModelCpp(small_cfg(), False, "bogus")
 
 
 def test_bf16_host_tensor_rounds_to_nearest_even():

@@ -147,3 +147,94 @@ def test_native_decode_continues_and_rejects_overflow():
         assert torch.equal(La["k_cache"], Lb["k_cache"])
     with pytest.raises(bnhip.BnError, match="max_len"):
         b.decode_native(0, 64 - b.length + 1, torch.empty(64, dtype=torch.int32, device="cuda"))
+
+
+# ------------------------------------------------------------ LLaMAModelCpp
+def small_cpp_config():
+    c = bten.LLaMAConfig()
+    (c.vocab_size, c.hidden_size, c.intermediate_size, c.num_hidden_layers,
+     c.num_attention_heads, c.num_key_value_heads) = (512, 256, 384, 2, 4, 2)
+    return c
+
+
+def oracle_model_forward(w, ids, c, per_head):
+    """llama_model.hpp:52-80 with the decoder layer of llama_layers.hpp:241-272,
+    composed from the oracle's restatements (fp64 products rounded to fp32)."""
+    f = lambda a: np.asarray(a, np.float32)
+    mm = lambda a, b: f(np.asarray(a, np.float64) @ np.asarray(b, np.float64))
+    eps, H, Hkv = c.rms_norm_eps, c.num_attention_heads, c.num_key_value_heads
+    x = w["embed_tokens"].to_numpy()[ids]
+    for L in w["layers"]:
+        t = {k: v.to_numpy() for k, v in L.items()}
+        xn = O.rmsnorm(x, t["input_layernorm"], eps)
+        attn = O.gqa_layer(xn, t["q_proj"], t["k_proj"], t["v_proj"], t["o_proj"], H, Hkv,
+                           c.rope_theta, 0, per_head=per_head)
+        h = f(x + attn)
+        xn2 = O.rmsnorm(h, t["post_attention_layernorm"], eps)
+        act = O.silu_mul(mm(xn2, t["gate_proj"]), mm(xn2, t["up_proj"]))
+        x = f(h + mm(act, t["down_proj"]))
+    return mm(O.rmsnorm(x, w["final_norm"].to_numpy(), eps), w["lm_head"].to_numpy())
+
+
+@pytest.mark.parametrize("attention", ["fused_head", "per_head"])
+def test_llama_model_cpp_forward_vs_oracle(attention):
+    """bten.LLaMAModelCpp.forward (llama_bindings.hpp:37-58): the ids are one
+    causal sequence, logits for every row; fused-head is the reference
+    layer's own chain (llama_layers.hpp:96-109)."""
+    c = small_cpp_config()
+    m = bten.LLaMAModelCpp(c, attention=attention)
+    ids = np.random.default_rng(5).integers(0, 512, 24).astype(np.uint32)
+    got = m.forward(ids)
+    assert got.shape == (24, 512) and got.dtype == np.float32
+    ref = oracle_model_forward(m.weights(), ids, c, attention == "per_head")
+    assert_close(got, ref, FP32_TOL, f"LLaMAModelCpp {attention}")
+
+
+def test_llama_model_cpp_device_weights_equal_host_weights():
+    # bn_fill_uniform on the device and the host twin give the same bits
+    c = small_cpp_config()
+    d, h = bten.LLaMAModelCpp(c, True), bten.LLaMAModelCpp(c, False)
+    wd, wh = d.weights(), h.weights()
+    for name in ("embed_tokens", "lm_head"):
+        np.testing.assert_array_equal(wd[name].to_numpy(), wh[name].to_numpy())
+    for Ld, Lh in zip(wd["layers"], wh["layers"]):
+        for k in Ld:
+            np.testing.assert_array_equal(Ld[k].to_numpy(), Lh[k].to_numpy())
+
+
+def test_llama_model_cpp_benchmark_and_memory():
+    c = small_cpp_config()
+    m = bten.LLaMAModelCpp(c)
+    ids = np.ones(8, np.uint32)
+    assert m.forward_timed(ids) > 0.0
+    r = m.benchmark(8, num_warmup=1, num_iterations=3)
+    assert set(r) == {"forward_time_ms", "tokens_per_second", "memory_used_bytes", "num_parameters"}
+    assert r["forward_time_ms"] > 0 and r["tokens_per_second"] > 0
+    assert r["num_parameters"] == c.count_parameters() == m.count_parameters()
+    assert r["memory_used_bytes"] == m.get_gpu_memory_usage() or r["memory_used_bytes"] > 0
+    assert m.get_gpu_memory_usage() > 0
+    with pytest.raises(RuntimeError, match="outside the vocabulary"):
+        m.forward(np.array([1, 512], np.uint32))
+    assert m.forward(np.zeros(0, np.uint32)).shape == (0, 512)
+
+
+def test_embedding_gather_and_uniform_fill():
+    import ctypes as C
+    V = lambda t: C.byref(bnhip.view(t))
+    table = torch.randn(50, 96, device="cuda")
+    ids = torch.tensor([3, 49, 0, 50, 7, -1], dtype=torch.int32, device="cuda")  # -1: id 2^32-1
+    out = torch.full((6, 96), float("nan"), device="cuda")
+    bnhip.call("bn_embedding", V(table), ids.data_ptr(), 6, V(out), None)
+    torch.cuda.synchronize()
+    want = table.cpu().numpy()[[3, 49, 0, 0, 7, 0]]
+    want[[3, 5]] = 0.0                           # ids past the table: zero rows
+    np.testing.assert_array_equal(out.cpu().numpy(), want)
+    for dt in (torch.float32, torch.bfloat16):
+        y = torch.empty((37, 91), dtype=dt, device="cuda")
+        bnhip.call("bn_fill_uniform", V(y), -0.5, 1.5, 12345, None)
+        yt = torch.empty((91, 37), dtype=dt, device="cuda").t()   # strided: same values
+        bnhip.call("bn_fill_uniform", V(yt), -0.5, 1.5, 12345, None)
+        torch.cuda.synchronize()
+        a = y.float().cpu().numpy()
+        assert a.min() >= -0.5 and a.max() <= 1.5 and abs(float(a.mean()) - 0.5) < 0.05
+        np.testing.assert_array_equal(a, yt.float().cpu().numpy())
