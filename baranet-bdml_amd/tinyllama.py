@@ -96,7 +96,11 @@ class TinyLlama:
         self.lin_ws = torch.empty(max(n_ws // 4, 1), device="cuda")
         self.path_ms = 0.0
         self.timing = False
-        self.trace = None  # list of (kernel, inputs, output) when set
+        self.trace = None  # list of (kernel, inputs, output, kw) when set
+        # trace only the launches of the layers / positions this selects
+        # (callable (layer, first position of the rows) -> bool; None: all)
+        self.trace_select = None
+        self._where = (0, 0)
 
     # ------------------------------------------------------------ path kernels
     def _timed(self, fn):
@@ -109,9 +113,14 @@ class TinyLlama:
         self._events.append((s, e))
         return out
 
+    def _tracing(self):
+        return self.trace is not None and (self.trace_select is None or
+                                           self.trace_select(*self._where))
+
     def _record(self, name, inputs, out, **kw):
-        if self.trace is not None:
+        if self._tracing():
             torch.cuda.synchronize()
+            kw = dict(kw, layer=self._where[0], pos0=self._where[1])
             self.trace.append((name, [t.detach().cpu().numpy().copy() for t in inputs],
                                out.detach().cpu().numpy().copy(), kw))
 
@@ -127,7 +136,7 @@ class TinyLlama:
 
     def add_rmsnorm(self, hdn, delta, weight):
         """hdn += delta in place; returns (hdn, RMSNorm(hdn) * weight)."""
-        before = hdn.clone() if self.trace is not None else None
+        before = hdn.clone() if self._tracing() else None
         y = torch.empty_like(hdn)
 
         def run():
@@ -135,7 +144,7 @@ class TinyLlama:
                        C.byref(bnhip.view(weight)), C.byref(bnhip.view(hdn)), C.byref(bnhip.view(y)),
                        self.cfg.rms_norm_eps, bnhip.stream_of())
         self._timed(run)
-        if self.trace is not None:
+        if self._tracing():
             self._record("add_rmsnorm", [before, delta, weight], torch.stack([hdn, y]),
                          eps=self.cfg.rms_norm_eps)
         return hdn, y
@@ -148,7 +157,7 @@ class TinyLlama:
 
     def rope_(self, x, offset):
         """RoPE in place on a (possibly strided) [rows, heads*64] view."""
-        before = x.clone() if self.trace is not None else None
+        before = x.clone() if self._tracing() else None
 
         def run():
             bnhip.call("bn_rope", C.byref(bnhip.view(x)), C.byref(bnhip.view(x)), offset,
@@ -221,8 +230,10 @@ class TinyLlama:
         """Decoder layers over rows hdn (positions pos0..); returns the final
         norm of every row.  Each residual add is fused with the RMSNorm that
         follows it (the next layer's input norm, or the final norm)."""
+        self._where = (0, pos0)
         x = self.rmsnorm(hdn, self.layers[0]["ln1"])
         for i, L in enumerate(self.layers):
+            self._where = (i, pos0)  # launches below belong to layer i
             hdn, x = self.add_rmsnorm(hdn, self._attention(x, L, pos0), L["ln2"])
             inter = self.cfg.intermediate_size
             if x.shape[0] <= self.SMALL_ROWS:
@@ -258,6 +269,7 @@ class TinyLlama:
             tok = torch.argmax(logits[-1])
             out.append(tok)
             logits = self.step(tok)
+        self.last_logits = logits  # of the last token fed (position length - 1)
         torch.cuda.synchronize()
         if time_path:
             self.path_ms = sum(s.elapsed_time(e) for s, e in self._events)
