@@ -21,6 +21,7 @@
 //     with the log-sum-exp rule: in-wave by shuffles, in-workgroup through LDS,
 //     across chunks by a small combine kernel over (m, l, acc) partials.
 // Scores live in the log2 domain: s = (q.k) * scale*log2(e), p = exp2(s - m).
+
 #include <mutex>
 
 #include "bn_common.hpp"
@@ -31,21 +32,17 @@
 // address hipGetSymbolAddress returns for the current device.
 static __device__ __align__(256) float scratch[BN_GQA_DECODE_SCRATCH_BYTES / sizeof(float)];
 
-#ifndef BN_DECODE_NT
-#define BN_DECODE_NT 1  // K/V cache loads non-temporal: streamed once, kept out of L2/MALL (+24% on config 3)
-#endif
+// bf16 K/V cache loads are non-temporal (streamed once, kept out of L2/MALL):
+// +24% on config 3 against plain loads.
 
 namespace bn {
 namespace {
 
 constexpr int HD = 64;
 constexpr int NT = 8;  // keys per lane group between softmax rescales
-#ifndef BN_DECODE_SINGLE_XCD
-#define BN_DECODE_SINGLE_XCD 1  // single pass: one KV head's query heads on one XCD
-#endif
-#ifndef BN_DECODE_SINGLE_NT
-#define BN_DECODE_SINGLE_NT 10  // single pass: up to 640 keys (16 waves x 4 groups x 10) in one load round
-#endif
+// single pass: 10 keys per lane group, up to 640 keys (16 waves x 4 groups x
+// 10) in one load round (3-6% faster than 8 at config 4's lengths)
+constexpr int kSingleNT = 10;
 
 template <typename T> struct DecVec;
 template <> struct DecVec<float> {
@@ -92,7 +89,7 @@ struct DecodeParams {
 template <typename T, int G, int WV, bool SINGLE>
 __global__ __launch_bounds__(64 * WV) void decode_split_kernel(DecodeParams p) {
   constexpr int VEC = DecVec<T>::VEC;
-  constexpr int NT = SINGLE ? BN_DECODE_SINGLE_NT : bn::NT;
+  constexpr int NT = SINGLE ? kSingleNT : bn::NT;
   constexpr int LPK = HD / VEC;  // lanes per key
   constexpr int KPI = 64 / LPK;  // keys per wave per load instruction
   __shared__ float red_m[WV][G], red_l[WV][G];
@@ -107,7 +104,7 @@ __global__ __launch_bounds__(64 * WV) void decode_split_kernel(DecodeParams p) {
   // KV head -- go to one XCD (workgroups are dealt to the 8 XCDs in turn), so
   // they read that KV head's cache rows from one L2
   int bg = SINGLE ? blockIdx.x : blockIdx.x / p.n_split;
-  if (SINGLE && BN_DECODE_SINGLE_XCD && (gridDim.x & 7) == 0)
+  if (SINGLE && (gridDim.x & 7) == 0)
     bg = (blockIdx.x & 7) * (gridDim.x >> 3) + (blockIdx.x >> 3);
   const int units = SINGLE ? p.n_heads : p.n_kv_heads;
   const int b = bg / units;
@@ -276,18 +273,10 @@ typedef float df32x4_t __attribute__((ext_vector_type(4)));
 constexpr int TK = 32;   // keys per wave tile
 constexpr int VTP = 36;  // V^T LDS pitch (elements): conflict-free writes and b64 reads
 
-#ifndef BN_DECODE_G_FASTEST
-#define BN_DECODE_G_FASTEST 0
-#endif
-#ifndef BN_DECODE_NBUF
-#define BN_DECODE_NBUF 2
-#endif
-constexpr int NBUF = BN_DECODE_NBUF;
-#ifndef BN_DECODE_WAVES_PER_EU
-#define BN_DECODE_WAVES_PER_EU 3
-#endif
+constexpr int NBUF = 2;  // register tile buffers in turn
+// register budget for 3 waves per SIMD
 template <int G>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(BN_DECODE_WAVES_PER_EU)))
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
 void decode_bf16_mfma_kernel(DecodeParams p) {
   // per-wave V^T tile; after the wave's last tile the same bytes hold its
   // (acc) merge values, so the workgroup needs no second LDS array
@@ -297,17 +286,9 @@ void decode_bf16_mfma_kernel(DecodeParams p) {
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int l16 = lane & 15, grp = lane >> 4;
-#if BN_DECODE_G_FASTEST
-  // the n_kv_heads workgroups of one (sequence, chunk) are dispatched together:
-  // together they stream whole 512-byte cache rows
-  const int g = blockIdx.x % p.n_kv_heads;
-  const int bs = blockIdx.x / p.n_kv_heads;
-  const int b = bs / p.n_split, split = bs % p.n_split;
-#else
   const int split = blockIdx.x % p.n_split;
   const int bg = blockIdx.x / p.n_split;
   const int b = bg / p.n_kv_heads, g = bg % p.n_kv_heads;
-#endif
 
   int len = p.lens[b];
   len = len < 0 ? 0 : (len > p.max_len ? p.max_len : len);
@@ -479,9 +460,6 @@ void decode_bf16_mfma_kernel(DecodeParams p) {
 // K fragments come from LDS with ds_read_b128, V^T fragments with the gfx950
 // transpose read ds_read_b64_tr_b16, and the wave writes its own partials.
 typedef short ds4_t __attribute__((ext_vector_type(4)));
-#ifndef BN_DECODE_ROWS_WAVES
-#define BN_DECODE_ROWS_WAVES 2
-#endif
 constexpr int RKP = 4 * HD + 8;   // K tile row pitch (elements): 528 B, 16 rows hit 64 distinct banks
 constexpr int RVP = 4 * HD + 16;  // V tile row pitch: 544 B, 4 rows x 32 B transpose reads conflict-free
 constexpr int RCH = TK * 4 * HD * 2 / 16 / 256;  // 16-byte chunks per thread per array per tile
@@ -493,7 +471,8 @@ __device__ __forceinline__ dbf16x4_t lds_read_tr16(const bf16_t *p) {
 }
 
 template <int G>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(BN_DECODE_ROWS_WAVES))) void decode_bf16_rows_kernel(DecodeParams p) {
+// register budget for 2 waves per SIMD (two register tiles ahead)
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void decode_bf16_rows_kernel(DecodeParams p) {
   // two tile buffers: one barrier per tile orders the LDS writes and reads
   __shared__ __attribute__((aligned(16))) bf16_t KL[2][TK * RKP];
   __shared__ __attribute__((aligned(16))) bf16_t VL[2][TK * RVP];
@@ -542,17 +521,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(BN_DECODE_R
     const int64_t o1 = (int64_t)min(kb + crow + 8, last) * kv_rs + ccol;
     const int64_t o2 = (int64_t)min(kb + crow + 16, last) * kv_rs + ccol;
     const int64_t o3 = (int64_t)min(kb + crow + 24, last) * kv_rs + ccol;
-#if BN_DECODE_NT  // streamed once: non-temporal loads
+    // streamed once: non-temporal loads
     r.k0 = __builtin_nontemporal_load((const u32x4 *)(Kr + o0)); r.v0 = __builtin_nontemporal_load((const u32x4 *)(Vr + o0));
     r.k1 = __builtin_nontemporal_load((const u32x4 *)(Kr + o1)); r.v1 = __builtin_nontemporal_load((const u32x4 *)(Vr + o1));
     r.k2 = __builtin_nontemporal_load((const u32x4 *)(Kr + o2)); r.v2 = __builtin_nontemporal_load((const u32x4 *)(Vr + o2));
     r.k3 = __builtin_nontemporal_load((const u32x4 *)(Kr + o3)); r.v3 = __builtin_nontemporal_load((const u32x4 *)(Vr + o3));
-#else
-    r.k0 = *(const u32x4 *)(Kr + o0); r.v0 = *(const u32x4 *)(Vr + o0);
-    r.k1 = *(const u32x4 *)(Kr + o1); r.v1 = *(const u32x4 *)(Vr + o1);
-    r.k2 = *(const u32x4 *)(Kr + o2); r.v2 = *(const u32x4 *)(Vr + o2);
-    r.k3 = *(const u32x4 *)(Kr + o3); r.v3 = *(const u32x4 *)(Vr + o3);
-#endif
   };
   auto lstore = [&](const RegTile &r, int buf) __attribute__((always_inline)) {
     bf16_t *kd = KL[buf], *vd = VL[buf];
@@ -669,10 +642,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(BN_DECODE_R
 // v_mfma_f32_16x16x32_bf16 as in the whole-row kernel.  The waves'
 // (m, l, acc) are merged through LDS at the end and the workgroup writes the
 // G output rows.
-#ifndef BN_DECODE_WHOLE_WAVES
-#define BN_DECODE_WHOLE_WAVES 4
-#endif
-constexpr int WWV = BN_DECODE_WHOLE_WAVES;
+constexpr int WWV = 4;  // waves per workgroup (8 measured 8% slower on config 3, 2 3% slower)
 constexpr int WKP = HD + 8;  // tile row pitch, 144 B: b128 K reads of 16 rows and tr16 V
                              // reads of 4 rows x 32 B hit distinct banks
 
@@ -730,17 +700,11 @@ __global__ __launch_bounds__(64 * WWV) void decode_bf16_whole_kernel(DecodeParam
     const int64_t o1 = (int64_t)min(kb + crow + 8, last) * kv_rs + ccol;
     const int64_t o2 = (int64_t)min(kb + crow + 16, last) * kv_rs + ccol;
     const int64_t o3 = (int64_t)min(kb + crow + 24, last) * kv_rs + ccol;
-#if BN_DECODE_NT  // streamed once: non-temporal loads
+    // streamed once: non-temporal loads
     r.k0 = __builtin_nontemporal_load((const u32x4 *)(Kr + o0)); r.v0 = __builtin_nontemporal_load((const u32x4 *)(Vr + o0));
     r.k1 = __builtin_nontemporal_load((const u32x4 *)(Kr + o1)); r.v1 = __builtin_nontemporal_load((const u32x4 *)(Vr + o1));
     r.k2 = __builtin_nontemporal_load((const u32x4 *)(Kr + o2)); r.v2 = __builtin_nontemporal_load((const u32x4 *)(Vr + o2));
     r.k3 = __builtin_nontemporal_load((const u32x4 *)(Kr + o3)); r.v3 = __builtin_nontemporal_load((const u32x4 *)(Vr + o3));
-#else
-    r.k0 = *(const u32x4 *)(Kr + o0); r.v0 = *(const u32x4 *)(Vr + o0);
-    r.k1 = *(const u32x4 *)(Kr + o1); r.v1 = *(const u32x4 *)(Vr + o1);
-    r.k2 = *(const u32x4 *)(Kr + o2); r.v2 = *(const u32x4 *)(Vr + o2);
-    r.k3 = *(const u32x4 *)(Kr + o3); r.v3 = *(const u32x4 *)(Vr + o3);
-#endif
   };
   bf16_t *const kt = KT[wave], *const vt = VT[wave];
   auto lstore = [&](const RegTile &r) __attribute__((always_inline)) {
@@ -809,11 +773,6 @@ __global__ __launch_bounds__(64 * WWV) void decode_bf16_whole_kernel(DecodeParam
     }
   };
 
-  // Tile ti is register tile ta (even) / tb (odd), loaded two tiles ahead,
-  // and goes through the wave's single LDS tile.  LDS instructions of one
-  // wave execute in order, so the tile's writes follow the previous tile's
-  // reads (already consumed) and precede its own reads without a barrier;
-  // wave_barrier keeps the compiler from moving LDS accesses across.
   // The wave's tile ti goes through one register tile (loaded one tile ahead)
   // and the wave's LDS tile.  LDS instructions of one wave execute in order,
   // so a tile's writes follow the previous tile's reads (already consumed) and
@@ -932,12 +891,9 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeParams p) {
   for (int e = 0; e < 4; ++e) Elem<T>::store(out + e, A[e] * inv);
 }
 
-#ifndef BN_DECODE_MIN_WG
-#define BN_DECODE_MIN_WG 2048
-#endif
-#ifndef BN_DECODE_ROWS_MIN_WG
-#define BN_DECODE_ROWS_MIN_WG 512
-#endif
+// split-K workgroup targets: per-head kernels / whole-row kernel (4 KV heads
+// per workgroup)
+constexpr int kMinWg = 2048, kRowsMinWg = 512;
 int choose_chunk(int batch, int max_len, int units, int min_wg) {
   // enough workgroups to cover the 256 CUs several times over (a partial last
   // round of resident workgroups costs a whole round), chunks >= 128 keys
@@ -961,9 +917,6 @@ void launch_split(const DecodeParams &p, dim3 grid, hipStream_t s) {
 
 bool rows_path(const DecodeParams &p, bool bf16) { return bf16 && p.n_kv_heads % 4 == 0; }
 
-#ifndef BN_DECODE_SINGLE_WV
-#define BN_DECODE_SINGLE_WV 16
-#endif
 // fp32 caches of at most this many keys with at most this many (sequence,
 // query head) pairs take the single-pass kernel
 constexpr int kSingleMaxLen = 1024, kSingleMaxUnits = 256;
@@ -972,7 +925,7 @@ bool single_path(int dtype, int batch, int max_len, int n_heads) {
 }
 
 void launch_single(const DecodeParams &p, hipStream_t s) {
-  constexpr int WV = BN_DECODE_SINGLE_WV;
+  constexpr int WV = 16;  // waves per workgroup (16 measured faster than 8)
   hipLaunchKernelGGL((decode_split_kernel<float, 1, WV, true>), dim3((unsigned)(p.batch * p.n_heads)),
                      dim3(64 * WV), 0, s, p);
 }
@@ -1094,10 +1047,7 @@ int gqa_decode_impl(int dtype, const void *q, const void *k_cache, const void *v
     BN_LAUNCH_CHECK();
     return BN_OK;
   }
-#ifndef BN_DECODE_WHOLE
-#define BN_DECODE_WHOLE 1
-#endif
-  if (BN_DECODE_WHOLE && dtype == BN_BF16) {  // one workgroup per (sequence, KV head) when that fills the CUs
+  if (dtype == BN_BF16) {  // one workgroup per (sequence, KV head) when that fills the CUs
     int st = ensure_device();
     if (st) return st;
     const int cus = device_cu_count();
@@ -1120,8 +1070,8 @@ int gqa_decode_impl(int dtype, const void *q, const void *k_cache, const void *v
   }
   // the whole-row kernel gives each workgroup 4 KV heads: 1/4 of the workgroups per chunk
   p.chunk = rows_path(p, dtype == BN_BF16)
-                ? choose_chunk(batch, max_len, n_kv_heads / 4, BN_DECODE_ROWS_MIN_WG)
-                : choose_chunk(batch, max_len, n_kv_heads, BN_DECODE_MIN_WG);
+                ? choose_chunk(batch, max_len, n_kv_heads / 4, kRowsMinWg)
+                : choose_chunk(batch, max_len, n_kv_heads, kMinWg);
   p.n_split = (max_len + p.chunk - 1) / p.chunk;
   p.c = scale * 1.4426950408889634f;
   const size_t need = (size_t)batch * n_heads * p.n_split * (HD + 2) * sizeof(float);

@@ -32,21 +32,15 @@ template <typename T>
 struct LinCfg;
 // k per LDS stage (measured: doubling it to 64 / 128 loses 8% (fp32) and 17%
 // (bf16, 2048 rows) -- half the workgroups fit a compute unit)
-#ifndef BN_LIN_KT32
-#define BN_LIN_KT32 32
-#endif
-#ifndef BN_LIN_KT16
-#define BN_LIN_KT16 64
-#endif
 template <>
 struct LinCfg<float> {
-  static constexpr int KT = BN_LIN_KT32;  // k per LDS stage
+  static constexpr int KT = 32;  // k per LDS stage
   static constexpr int WP = TN + 4;       // Ws[k][n] pitch, elements
   static constexpr int XP = KT + 4;       // Xs[m][k] pitch
 };
 template <>
 struct LinCfg<bf16_t> {
-  static constexpr int KT = BN_LIN_KT16;
+  static constexpr int KT = 64;
   static constexpr int WP = TN + 8;  // 144 B rows: conflict-free transposed 16-bit reads
   static constexpr int XP = KT + 8;
 };
@@ -306,15 +300,13 @@ __global__ __launch_bounds__(256) void linear_small_kernel(LinParams p) {
   }
 }
 
-// slabs of the few-rows path: about BN_SMALL_WG workgroups, slabs of
+// slabs of the few-rows path: about kSmallWg workgroups, slabs of
 // 32..SK_MAX rows in multiples of 32
-#ifndef BN_SMALL_WG
-#define BN_SMALL_WG 512
-#endif
+constexpr int kSmallWg = 512;
 void plan_small(int dtype, int n, int k, int *nsplit, int *kchunk) {
   const int cols = 64 * (dtype == BN_BF16 ? 8 : 4);
   const int strips = (n + cols - 1) / cols;
-  const int want = std::max(1, BN_SMALL_WG / strips);
+  const int want = std::max(1, kSmallWg / strips);
   int kc = (k + want - 1) / want;
   kc = std::min(std::max((kc + 31) / 32 * 32, 32), SK_MAX);
   *kchunk = kc;
@@ -322,17 +314,15 @@ void plan_small(int dtype, int n, int k, int *nsplit, int *kchunk) {
 }
 
 // k slabs: as many as still fit the grid in one round of resident
-// workgroups (BN_LIN_SLOTS: 4 per compute unit of an MI355X -- 36 KB of LDS
+// workgroups (kLinSlots: 4 per compute unit of an MI355X -- 36 KB of LDS
 // each), each slab at least two stages deep.  A fixed device size keeps the
 // plan, and so the workspace size, independent of the device queried.
-#ifndef BN_LIN_SLOTS
-#define BN_LIN_SLOTS 1024
-#endif
+constexpr int64_t kLinSlots = 1024;
 void plan_split(int dtype, int m, int n, int k, int *nsplit, int *kchunk) {
   const int KT = dtype == BN_BF16 ? LinCfg<bf16_t>::KT : LinCfg<float>::KT;
   const int64_t tiles = (int64_t)((n + TN - 1) / TN) * ((m + TM - 1) / TM);
   const int stages = (k + KT - 1) / KT;
-  int ns = (int)std::min<int64_t>(BN_LIN_SLOTS / tiles, std::max(1, stages / 2));
+  int ns = (int)std::min<int64_t>(kLinSlots / tiles, std::max(1, stages / 2));
   ns = std::max(ns, 1);
   const int per = (stages + ns - 1) / ns;
   *kchunk = std::max(per, 1) * KT;

@@ -29,25 +29,11 @@ __device__ __forceinline__ raw16_t load_raw(const void *p) { return *reinterpret
 // loads +7% on SwiGLU but -14% on RMSNorm+RoPE, whose 67 MB input stays in
 // the 256 MB MALL, and -5% on the residual add with the stores also
 // non-temporal.
-#ifndef BN_NORM_NT_LOAD
-#define BN_NORM_NT_LOAD 1
-#endif
-#ifndef BN_NORM_NT_STORE
-#define BN_NORM_NT_STORE 1
-#endif
 __device__ __forceinline__ raw16_t load_stream(const void *p) {
-#if BN_NORM_NT_LOAD
   return __builtin_nontemporal_load(reinterpret_cast<const raw16_t *>(p));
-#else
-  return *reinterpret_cast<const raw16_t *>(p);
-#endif
 }
 __device__ __forceinline__ void store_stream(void *p, raw16_t v) {
-#if BN_NORM_NT_STORE
   __builtin_nontemporal_store(v, reinterpret_cast<raw16_t *>(p));
-#else
-  *reinterpret_cast<raw16_t *>(p) = v;
-#endif
 }
 
 template <> struct Chunk<float> {

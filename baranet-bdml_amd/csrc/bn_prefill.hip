@@ -212,21 +212,11 @@ __device__ __forceinline__ Work decode_work_packed(const PrefillParams &p) {
 // V_{j+1} (register-staged one iteration earlier) into the buffers of K_j and
 // V_{j-1}, last read in iteration j-1: one barrier per block orders them.
 constexpr float kSumLimit = 65536.f;
-#ifndef BN_PIPE_OCC1
-#define BN_PIPE_OCC1 2  // workgroups per CU the register budget is sized for (RT = 1)
-#endif
-#ifndef BN_PIPE_OCC2
-#define BN_PIPE_OCC2 2  // (RT = 2)
-#endif
-#ifndef BN_PIPE_SCHED
-#define BN_PIPE_SCHED 1
-#endif
-#ifndef BN_PIPE_V0
-#define BN_PIPE_V0 4  // VALU instructions ahead of the first MFMA of a step
-#endif
-#ifndef BN_PIPE_V1
-#define BN_PIPE_V1 5  // VALU instructions after each MFMA
-#endif
+constexpr int kOcc = 2;  // workgroups per CU the register budget is sized for
+// step interleave: VALU instructions ahead of the first MFMA, then after each
+// MFMA (re-swept on the head-packed kernel: 3-5 ahead, 4-6 after, 2/6; this
+// is best or tied on configs 2 and 5)
+constexpr int kSchedV0 = 4, kSchedV1 = 5;
 
 template <int RT, int OCC, bool HP>
 __global__ __launch_bounds__(256, OCC) void prefill_bf16_kernel(PrefillParams p) {
@@ -454,16 +444,14 @@ __global__ __launch_bounds__(256, OCC) void prefill_bf16_kernel(PrefillParams p)
       exps(sc[rt], mcv[rt], pc[rt], rs[rt]);  // m = -inf: inf/NaN -> fixup
       bad = bad || !(rs[rt] <= kSumLimit);
     }
-#if BN_PIPE_SCHED
     // LDS reads first, then one MFMA every few VALU instructions
     __builtin_amdgcn_sched_group_barrier(0x100, 12, 0);
-    __builtin_amdgcn_sched_group_barrier(0x002, BN_PIPE_V0, 0);
+    __builtin_amdgcn_sched_group_barrier(0x002, kSchedV0, 0);
 #pragma unroll
     for (int i = 0; i < 8 * RT; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x002, BN_PIPE_V1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, kSchedV1, 0);
     }
-#endif
     finish(bad, sc, pc, rs);
   };
 
@@ -558,7 +546,9 @@ __global__ __launch_bounds__(256, 2) void prefill_f32_kernel(PrefillParams p) {
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int r32 = lane & 31, hf = lane >> 5;
-  const Work w = decode_work(p);
+  // a (batch, KV head) group's heads and row tiles on one XCD: its K/V is
+  // read from HBM once, then from that XCD's L2
+  const Work w = decode_work_xcd(p);
   const float *Q = (const float *)p.q + w.b * p.q_bs + (int64_t)w.h * HD;
   const float *K = (const float *)p.k + w.b * p.kv_bs + (int64_t)w.g * HD;
   const float *V = (const float *)p.v + w.b * p.kv_bs + (int64_t)w.g * HD;
@@ -723,17 +713,12 @@ static int prefill_impl(int dtype, const void *q, const void *k, const void *v, 
   // small problems keep enough workgroups in flight (measured with settled
   // clocks: RT = 2 gains 3% on config 2 and 3-7% from S = 4096 on, and loses
   // 10-30% at 512 workgroups or fewer)
-#ifndef BN_RT2_MIN_WG
-#define BN_RT2_MIN_WG 1024
-#endif
-  const int rt16 = ((int64_t)batch * n_heads * ((seq_q + 255) / 256) >= BN_RT2_MIN_WG) ? 2 : 1;
+  constexpr int64_t kRt2MinWg = 1024;
+  const int rt16 = ((int64_t)batch * n_heads * ((seq_q + 255) / 256) >= kRt2MinWg) ? 2 : 1;
   // bf16 with 4 or 8 query heads per KV head: head-packed work items (all of
-  // a group's heads over 32 rows per workgroup) when BN_PACKED is set
-#ifndef BN_PACKED
-#define BN_PACKED 1
-#endif
+  // a group's heads over 32 rows per workgroup; config 2 +6%, config 5 +3%)
   const int group = n_heads / n_kv_heads;
-  const bool packed = BN_PACKED && dtype == BN_BF16 && (group == 8 || group == 4);
+  const bool packed = dtype == BN_BF16 && (group == 8 || group == 4);
   const int rows_per_wg = packed ? 32 : dtype == BN_BF16 ? 4 * 32 * rt16 : BM;
   const int n_mt = (seq_q + rows_per_wg - 1) / rows_per_wg;
   const int64_t n_wg = (int64_t)batch * (packed ? n_kv_heads : n_heads) * n_mt;
@@ -754,13 +739,13 @@ static int prefill_impl(int dtype, const void *q, const void *k, const void *v, 
   hipStream_t s = as_stream(stream);
   if (dtype == BN_BF16) {
     if (packed && group == 8)
-      hipLaunchKernelGGL((prefill_bf16_kernel<2, BN_PIPE_OCC2, true>), dim3((unsigned)n_wg), dim3(256), 0, s, p);
+      hipLaunchKernelGGL((prefill_bf16_kernel<2, kOcc, true>), dim3((unsigned)n_wg), dim3(256), 0, s, p);
     else if (packed)
-      hipLaunchKernelGGL((prefill_bf16_kernel<1, BN_PIPE_OCC1, true>), dim3((unsigned)n_wg), dim3(256), 0, s, p);
+      hipLaunchKernelGGL((prefill_bf16_kernel<1, kOcc, true>), dim3((unsigned)n_wg), dim3(256), 0, s, p);
     else if (rt16 == 2)
-      hipLaunchKernelGGL((prefill_bf16_kernel<2, BN_PIPE_OCC2, false>), dim3((unsigned)n_wg), dim3(256), 0, s, p);
+      hipLaunchKernelGGL((prefill_bf16_kernel<2, kOcc, false>), dim3((unsigned)n_wg), dim3(256), 0, s, p);
     else
-      hipLaunchKernelGGL((prefill_bf16_kernel<1, BN_PIPE_OCC1, false>), dim3((unsigned)n_wg), dim3(256), 0, s, p);
+      hipLaunchKernelGGL((prefill_bf16_kernel<1, kOcc, false>), dim3((unsigned)n_wg), dim3(256), 0, s, p);
   } else
     hipLaunchKernelGGL(prefill_f32_kernel, dim3((unsigned)n_wg), dim3(256), 0, s, p);
   BN_LAUNCH_CHECK();

@@ -198,6 +198,33 @@ def test_decode_bf16_one_workgroup_per_kv_head(L, H, Hkv):
         assert_close(got[b:b + 1], ref, BF16_TOL, f"b={b} len={Lb}")
 
 
+@pytest.mark.parametrize("lens_kind", ["skewed", "two_groups"])
+def test_decode_bf16_whole_cache_skewed_lengths(lens_kind):
+    """The one-workgroup-per-(sequence, KV head) kernel on batches whose
+    lengths differ by far: a few long caches among short ones (skewed) or
+    two length classes (two_groups); every sequence matches the oracle."""
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    H, Hkv, L = 32, 4, 4096
+    Bn = -(-cus // Hkv)
+    r = np.random.default_rng(71)
+    if lens_kind == "skewed":
+        lens = np.full(Bn, 64, np.int32)
+        lens[:4] = [4096, 4095, 3000, 2049]
+    else:
+        lens = np.where(np.arange(Bn) % 2 == 0, 1000, 3000).astype(np.int32)
+    q = bf16_round(r.standard_normal((Bn, H, 64)).astype(np.float32))
+    kc = bf16_round(r.standard_normal((Bn, L, Hkv, 64)).astype(np.float32))
+    vc = bf16_round(r.standard_normal((Bn, L, Hkv, 64)).astype(np.float32))
+    got = host(B.gqa_decode(dev(q, torch.bfloat16), dev(kc, torch.bfloat16),
+                            dev(vc, torch.bfloat16), torch.from_numpy(lens).cuda(), scale=0.125))
+    assert np.all(np.isfinite(got))
+    for b in [0, 1, 2, 3, 4, 5, Bn - 1]:
+        Lb = int(lens[b])
+        ref = O.gqa_decode(q[b:b + 1], kc[b:b + 1, :Lb], vc[b:b + 1, :Lb],
+                           np.array([Lb], np.int32), 0.125)
+        assert_close(got[b:b + 1], ref, BF16_TOL, f"{lens_kind} b={b} len={Lb}")
+
+
 @pytest.mark.parametrize("dtype,Bn,L,H,Hkv", [("f32", 1, 640, 32, 4), ("f32", 3, 300, 8, 2),
                                               ("bf16", 2, 300, 32, 4), ("bf16", 80, 200, 16, 4)])
 def test_decode_ignores_cache_rows_past_len(dtype, Bn, L, H, Hkv):
