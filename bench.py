@@ -128,6 +128,32 @@ def roofline(bound, achieved, peak, unit, traffic=None):
             "frac": round(achieved / peak, 4), "traffic": traffic}
 
 
+def cpu_meta():
+    """Host the CPU baselines ran on: logical CPUs of the machine, CPUs this
+    process may run on, and the CPU model from /proc/cpuinfo."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        allowed = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        allowed = os.cpu_count()
+    return {"nproc": os.cpu_count(), "cpus_allowed": allowed, "cpu_model": model}
+
+
+def cpu_result(value, unit, sample, cores=1):
+    """A cpu_baseline object: the single-threaded C oracle (kind "port": a
+    restatement of the reference kernels' loops) on a bounded sample."""
+    return dict({"value": value, "unit": unit, "cores": cores, "kind": "port", "sample": sample},
+                **cpu_meta())
+
+
 def bench_prefill(B_, S, H, Hkv, dtype, steps, warmup, seed=0):
     import torch
     import bnhip
@@ -144,8 +170,10 @@ def bench_prefill(B_, S, H, Hkv, dtype, steps, warmup, seed=0):
     return {"value": round(tflops, 3), "unit": "TFLOP/s", "ms_per_launch": round(ms, 5),
             "flops_per_launch": fl,
             "roofline": roofline("mfma", tflops, peak, "TFLOP/s",
-                                 measured_traffic("prefill_bf16") if (dtype == "bf16" and S == 2048)
-                                 else None)}
+                                 measured_traffic({("bf16", 2048): "prefill_bf16",
+                                                   ("fp32", 2048): "prefill_fp32",
+                                                   ("bf16", 16384): "prefill_long"}.get((dtype, S),
+                                                                                        "")))}
 
 
 def bench_backward(steps, warmup, seed=5):
@@ -266,15 +294,18 @@ def bench_rmsnorm_rope(steps, warmup):
     import bnhip
     rows, w = 16384, 2048
     g = torch.Generator(device="cuda").manual_seed(5)
-    xs = [torch.randn((rows, w), generator=g, device="cuda").bfloat16() for _ in range(2)]
-    ys = [torch.empty_like(xs[0]) for _ in range(2)]
+    # 4 input/output sets of 67 MB each (537 MB) rotated per launch: the input
+    # of a launch was last touched 3 launches ago, past the 256 MB MALL
+    NS = 4
+    xs = [torch.randn((rows, w), generator=g, device="cuda").bfloat16() for _ in range(NS)]
+    ys = [torch.empty_like(xs[0]) for _ in range(NS)]
     wt = torch.ones((1, w), device="cuda", dtype=torch.bfloat16)
     wv = bnhip.view(wt)
     views = [(bnhip.view(x), bnhip.view(y)) for x, y in zip(xs, ys)]
     st = bnhip.stream_of()
 
     def run(i):
-        xv, yv = views[i % 2]
+        xv, yv = views[i % NS]
         bnhip.call("bn_rmsnorm_rope", C.byref(xv), C.byref(wv), C.byref(yv), 1e-5, 0, 64,
                    1e4, st)
 
@@ -387,9 +418,9 @@ def cpu_baseline_block(x, ws):
     xn = O.rmsnorm(x, np.ones((1, x.shape[1]), np.float32), 1e-5)
     O.gqa_layer(xn, *ws, 32, 4, 10000.0, 0, per_head=False)
     el = time.perf_counter() - t0
-    return {"value": round(el * 1e3, 2), "unit": "ms per block", "cores": 1, "kind": "port",
-            "sample": "the whole config-1 block once (RMSNorm + projections + fused-head "
-                      "attention + output projection), fp32 oracle"}
+    return cpu_result(round(el * 1e3, 2), "ms per block",
+                      "the whole config-1 block once (RMSNorm + projections + fused-head "
+                      "attention + output projection), fp32 oracle")
 
 
 def bench_tinyllama(prompt=512, new_tokens=128, cpu=True, warmup_tokens=2):
@@ -410,10 +441,19 @@ def bench_tinyllama(prompt=512, new_tokens=128, cpu=True, warmup_tokens=2):
             L["v_cache"].zero_()
         m.length = 0
     torch.cuda.synchronize()
+    m.path_log = []
     t0 = time.perf_counter()
     toks, path_ms = m.generate(ids, new_tokens, time_path=True)
     wall = time.perf_counter() - t0
+    log, m.path_log = m.path_log, None
+    by_kind = path_replay_ms(log)
     res = {"prompt": prompt, "new_tokens": new_tokens, "wall_s": round(wall, 3),
+           "path_device_ms": round(sum(by_kind.values()), 3),
+           "path_device_ms_by_kind": {k: round(v, 3) for k, v in by_kind.items()},
+           "path_device_note": "each kind's launches of the generate (prompt + 128 steps) "
+                               "captured into one graph in launch order and replayed; ms per "
+                               "replay, no host gaps; qkv_rope = the decode steps' fused QKV "
+                               "projection + RoPE (their RoPE), so it includes the projection",
            "path_ms": round(path_ms, 3),
            "path_kernels": "RMSNorm (plain and fused with the residual add), RoPE (prompt: "
                            "bn_rope; decode steps: fused into the QKV projection kernel), GQA "
@@ -440,6 +480,23 @@ def bench_tinyllama(prompt=512, new_tokens=128, cpu=True, warmup_tokens=2):
     return res
 
 
+def path_replay_ms(log, steps=5):
+    """Device time (ms) of logged launches by kind: each kind's launches are
+    captured into one graph, in launch order, and the graph is replayed."""
+    import torch
+    out = {}
+    for kind in sorted({k for k, _ in log}):
+        fns = [fn for k, fn in log if k == kind]
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for fn in fns:
+                fn()
+        out[kind] = time_launches(lambda i: g.replay(), steps, 1)
+        del g
+    return out
+
+
 def cpu_baseline_tinyllama(m, ids):
     """Oracle on the layer-0 prefill path inputs of the GPU model (teacher-forced),
     single thread, extrapolated x22 layers (labelled).  The projections that feed
@@ -462,12 +519,11 @@ def cpu_baseline_tinyllama(m, ids):
                   0.125, True, 0)
     t_attn = time.perf_counter() - t0
     layer_s = 2 * t_norm + t_attn  # two RMSNorms per decoder layer
-    return {"value": round(layer_s * cfg.num_hidden_layers * 1e3, 1),
-            "unit": "ms (prefill path kernels, 22 layers, extrapolated from layer 0)",
-            "cores": 1, "kind": "port",
-            "sample": f"layer 0 of the prefill: 2 RMSNorm + RoPE(q, k) + per-head causal GQA "
+    return cpu_result(round(layer_s * cfg.num_hidden_layers * 1e3, 1),
+                      "ms (prefill path kernels, 22 layers, extrapolated from layer 0)",
+                      f"layer 0 of the prefill: 2 RMSNorm + RoPE(q, k) + per-head causal GQA "
                       f"over {S} tokens on the GPU run's inputs, fp32 oracle, "
-                      f"{layer_s:.2f} s; decode steps not included"}
+                      f"{layer_s:.2f} s; decode steps not included")
 
 
 def cpu_baseline_prefill(budget_s=12.0):
@@ -485,29 +541,116 @@ def cpu_baseline_prefill(budget_s=12.0):
         done += 1
         fl += prefill_flops(1, S, 1, D)
     el = time.perf_counter() - t0
-    return {"value": round(fl / el / 1e12, 6), "unit": "TFLOP/s", "cores": 1, "kind": "port",
-            "sample": f"{done} of 128 (batch, head) pairs of config 2 (S=2048, D=64, causal), "
+    return cpu_result(round(fl / el / 1e12, 6), "TFLOP/s",
+                      f"{done} of 128 (batch, head) pairs of config 2 (S=2048, D=64, causal), "
                       f"fp32 oracle, {el:.1f} s; the oracle computes full S x S scores as the "
-                      f"reference chain does, so only the causal half is counted as work"}
+                      f"reference chain does, so only the causal half is counted as work")
 
 
-def cpu_baseline_decode(budget_s=6.0):
+def cpu_baseline_decode(ragged=False, budget_s=6.0, seed=2):
+    """The oracle's decode (single thread) on whole sequences of config 3 (the
+    bench's own lengths when ragged); bytes counted at bf16 size."""
     import numpy as np
     from oracle import oracle as O
     L, H, Hkv, D = 4096, 32, 4, 64
-    r = np.random.default_rng(2)
+    r = np.random.default_rng(seed)
+    lens = r.integers(512, 4097, 64).astype(np.int32) if ragged else np.full(64, L, np.int32)
     done, nb, t0 = 0, 0, time.perf_counter()
     while done < 64 and (time.perf_counter() - t0) < budget_s:
+        Lb = int(lens[done])
         q = r.standard_normal((1, H, D)).astype(np.float32)
-        kc = r.standard_normal((1, L, Hkv, D)).astype(np.float32)
-        vc = r.standard_normal((1, L, Hkv, D)).astype(np.float32)
-        O.gqa_decode(q, kc, vc, np.array([L], np.int32), 0.125)
+        kc = r.standard_normal((1, Lb, Hkv, D)).astype(np.float32)
+        vc = r.standard_normal((1, Lb, Hkv, D)).astype(np.float32)
+        O.gqa_decode(q, kc, vc, np.array([Lb], np.int32), 0.125)
         done += 1
-        nb += decode_bytes([L], Hkv, D, 1, H, 2)
+        nb += decode_bytes([Lb], Hkv, D, 1, H, 2)
     el = time.perf_counter() - t0
-    return {"value": round(nb / el / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": f"{done} of 64 sequences of config 3 (L=4096), fp32 oracle, {el:.1f} s, "
-                      f"bytes counted at bf16 size"}
+    what = "ragged lengths U[512,4096]" if ragged else "L=4096"
+    return cpu_result(round(nb / el / 1e9, 4), "GB/s",
+                      f"{done} of 64 sequences of config 3 ({what}), fp32 oracle, {el:.1f} s, "
+                      f"bytes counted at bf16 size")
+
+
+def cpu_baseline_rows(kind, rows=512, w=2048, reps_s=3.0):
+    """The oracle's RMSNorm+RoPE / residual add + RMSNorm / SwiGLU (single
+    thread) on `rows` rows of the GPU workload's width; GB/s at bf16 size."""
+    import numpy as np
+    from oracle import oracle as O
+    r = np.random.default_rng(9)
+    x = r.standard_normal((rows, w)).astype(np.float32)
+    d = r.standard_normal((rows, w)).astype(np.float32)
+    wt = np.ones((1, w), np.float32)
+    fn = {"rmsnorm_rope": lambda: O.rmsnorm_rope(x, wt, 1e-5, 0, 64, 1e4),
+          "add_rmsnorm": lambda: O.add_rmsnorm(x, d, wt, 1e-5),
+          "silu_mul": lambda: O.silu_mul(x, d)}[kind]
+    per_row = {"rmsnorm_rope": 2, "add_rmsnorm": 4, "silu_mul": 3}[kind] * w * 2
+    n, t0 = 0, time.perf_counter()
+    while n == 0 or time.perf_counter() - t0 < reps_s:
+        fn()
+        n += 1
+    el = (time.perf_counter() - t0) / n
+    return cpu_result(round(rows * per_row / el / 1e9, 4), "GB/s",
+                      f"{rows} rows x {w} of the GPU workload's shape, fp32 oracle "
+                      f"(silu_mul: numpy fp32, the op has no loop of its own to restate), "
+                      f"{n} repetitions, bytes counted at bf16 size")
+
+
+def cpu_baseline_prefill_long(rows=32):
+    """Config 5's prefill on the oracle: the last `rows` query rows of S=16384
+    (all 32 heads, every key they see), extrapolated to the whole causal
+    triangle by flop count (labelled)."""
+    import numpy as np
+    from oracle import oracle as O
+    S, H, Hkv, D = 16384, 32, 4, 64
+    r = np.random.default_rng(4)
+    q = r.standard_normal((1, rows, H, D)).astype(np.float32)
+    k = r.standard_normal((1, S, Hkv, D)).astype(np.float32)
+    v = r.standard_normal((1, S, Hkv, D)).astype(np.float32)
+    t0 = time.perf_counter()
+    O.gqa_prefill(q, k, v, 0.125, True, S - rows)
+    el = time.perf_counter() - t0
+    fl = 4 * H * D * sum(S - rows + i + 1 for i in range(rows))
+    return cpu_result(round(fl / el / 1e12, 6), "TFLOP/s",
+                      f"last {rows} query rows of S=16384, all heads, fp32 oracle, {el:.1f} s "
+                      f"(rate extrapolated to the full causal prefill)")
+
+
+def cpu_baseline_linear(m_rows=8):
+    """The QKV projection + RoPE on the oracle: op_mm's sequential-k fp32 loop
+    (or_matmul) then op_rope, on `m_rows` rows of [2048] x [2048, 2560]."""
+    import numpy as np
+    from oracle import oracle as O
+    r = np.random.default_rng(6)
+    x = r.standard_normal((m_rows, 2048)).astype(np.float32)
+    w = (r.standard_normal((2048, 2560)) / 45.0).astype(np.float32)
+    t0 = time.perf_counter()
+    y = O.matmul(x, w)
+    O.rope(np.ascontiguousarray(y[:, :2304]), 7, 64, 1e4)
+    el = time.perf_counter() - t0
+    return cpu_result(round(2 * m_rows * 2048 * 2560 / el / 1e12, 6), "TFLOP/s",
+                      f"{m_rows} rows, op_mm restated (sequential k, fp32) + op_rope, {el:.2f} s")
+
+
+def cpu_baseline_backward(S=2048, H=8):
+    """The oracle's attention backward (the reference chain's backward
+    primitives composed in numpy fp64, BLAS held to one thread) on one KV
+    group of config 2: B=1, S=2048, 8 query heads, 1 KV head."""
+    import numpy as np
+    from threadpoolctl import threadpool_limits
+    from oracle import oracle as O
+    r = np.random.default_rng(5)
+    q = r.standard_normal((1, S, H, 64)).astype(np.float32)
+    k = r.standard_normal((1, S, 1, 64)).astype(np.float32)
+    v = r.standard_normal((1, S, 1, 64)).astype(np.float32)
+    do = r.standard_normal((1, S, H, 64)).astype(np.float32)
+    with threadpool_limits(1):
+        t0 = time.perf_counter()
+        O.gqa_prefill_backward(q, k, v, do, 0.125, True, 0)
+        el = time.perf_counter() - t0
+    fl = 5 * prefill_flops(1, S, H, 64) // 2
+    return cpu_result(round(fl / el / 1e12, 6), "TFLOP/s",
+                      f"one KV group of config 2 (S={S}, {H} query heads), oracle backward "
+                      f"in numpy fp64 on one BLAS thread, {el:.1f} s")
 
 
 def main():
@@ -593,8 +736,20 @@ def main():
         print(f"copy: {out['copy']['value']} GB/s", file=sys.stderr, flush=True)
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline_prefill()
-        if "decode" in out:
-            out["decode"]["cpu_baseline"] = cpu_baseline_decode()
+        cpu = {"decode": lambda: cpu_baseline_decode(False),
+               "decode_ragged": lambda: cpu_baseline_decode(True),
+               # the oracle computes in fp32 whatever the GPU dtype: the same sample
+               "prefill_fp32": lambda: dict(out["cpu_baseline"],
+                                            note="same oracle run as the headline's (fp32)"),
+               "rmsnorm_rope": lambda: cpu_baseline_rows("rmsnorm_rope"),
+               "prefill_long": cpu_baseline_prefill_long,
+               "add_rmsnorm": lambda: cpu_baseline_rows("add_rmsnorm"),
+               "silu_mul": lambda: cpu_baseline_rows("silu_mul", w=5632),
+               "linear_rope": cpu_baseline_linear,
+               "prefill_backward": cpu_baseline_backward}
+        for key, fn in cpu.items():
+            if key in out:
+                out[key]["cpu_baseline"] = fn()
     print(json.dumps(out), flush=True)
 
 
