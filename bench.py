@@ -200,7 +200,9 @@ def bench_backward(steps, warmup, seed=5):
     tflops = fl / (ms * 1e-3) / 1e12
     return {"value": round(tflops, 3), "unit": "TFLOP/s", "ms_per_launch": round(ms, 5),
             "flops_per_launch": fl, "config": "config 2 backward, bf16",
-            "roofline": roofline("mfma", tflops, PEAK_BF16_TFLOPS, "TFLOP/s")}
+            "roofline": roofline("mfma", tflops, PEAK_BF16_TFLOPS, "TFLOP/s",
+                                 measured_traffic("prefill_backward")),
+            "traffic_kernel": "dK/dV kernel (the longest of the three launches)"}
 
 
 def bench_linear(steps, warmup, seed=6):
@@ -247,12 +249,14 @@ def bench_linear(steps, warmup, seed=6):
             v = fl / (ms * 1e-3) / 1e12
             out["prompt"] = {"value": round(v, 3), "unit": "TFLOP/s", "ms_per_launch": round(ms, 5),
                              "m": M, "unfused_ms": round(ms_ref, 5),
-                             "roofline": roofline("mfma", v, PEAK_FP32_TFLOPS, "TFLOP/s")}
+                             "roofline": roofline("mfma", v, PEAK_FP32_TFLOPS, "TFLOP/s",
+                                                  measured_traffic("linear_rope_prompt"))}
         else:
             v = byt / (ms * 1e-3) / 1e9
             out["decode_step"] = {"value": round(v, 1), "unit": "GB/s", "ms_per_launch": round(ms, 5),
                                   "m": M, "unfused_ms": round(ms_ref, 5),
-                                  "roofline": roofline("hbm", v, PEAK_HBM_GBS, "GB/s")}
+                                  "roofline": roofline("hbm", v, PEAK_HBM_GBS, "GB/s",
+                                                       measured_traffic("linear_rope_decode"))}
     out["config"] = "config 4 QKV projection + RoPE, fp32, K=2048, N=2560, rope_cols=2304"
     return out
 
