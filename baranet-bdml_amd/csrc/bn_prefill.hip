@@ -198,8 +198,8 @@ __device__ __forceinline__ Work decode_work_packed(const PrefillParams &p) {
 //     reference max m that is NOT recomputed per tile: one fma, one
 //     transcendental, half a bf16 pack and half a dot2 (row sum) per score;
 //   * m moves only in a rare exact fixup, taken when a tile's row sum exceeds
-//     2^16 (some p > 2^16, which includes inf and the NaN of the first tile,
-//     where m = -inf), and then only when it grew by more than 2^8;
+//     2^16 (some p > 2^16, which includes inf and NaN), and then only when it
+//     grew by more than 2^8; the first tile (m = -inf) runs the fixup alone;
 //   * software pipeline over 32-key tiles: step t issues O += V_{t-1}^T P_{t-1}
 //     and the scores of tile t+1 on the matrix cores, interleaved with the
 //     softmax of tile t on the VALU -- three independent pieces of work in
@@ -475,14 +475,15 @@ __global__ __launch_bounds__(256, OCC) void prefill_bf16_kernel(PrefillParams p)
     kfrags(kring + 32 * KP16, ka);
     scores(ka, sb);
     mask(0, sa);
-    float rs[RT];
-    bool bad = false;
+    // first tile: the reference max starts at -inf, so the fast path always
+    // ends in the fixup of every row tile; run the fixup directly (true max
+    // first, one pass of exponentials instead of two) -- the same state
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
-      exps(sa[rt], mcv[rt], pa[rt], rs[rt]);  // m = -inf: inf/NaN -> fixup
-      bad = bad || !(rs[rt] <= kSumLimit);
+      float rs;
+      fixup(rt, sa[rt], pa[rt], rs);
+      l[rt] += rs;
     }
-    finish(bad, sa, pa, rs);
   }
   // iteration j: steps 2j+1 (P of tile 2j, scores of 2j+2, softmax of 2j+1)
   // and 2j+2 (P of 2j+1, scores of 2j+3, softmax of 2j+2).  The leading
