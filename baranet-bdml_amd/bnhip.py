@@ -92,6 +92,7 @@ def lib():
         "bn_add_rmsnorm": ([V, V, V, V, V, f, vp], i), "bn_silu_mul": ([V, V, V, vp], i),
         "bn_softmax": ([V, V, i, i, vp], i), "bn_softmax_backward": ([V, V, V, vp], i),
         "bn_matmul": ([V, V, V, vp], i), "bn_repeat_kv": ([V, V, i, i, vp], i),
+        "bn_fused_head_attention": ([V, V, V, V, i, i, i, f, i, i, vp], i),
         "bn_binary": ([i, V, V, V, vp], i), "bn_unary": ([i, V, f, V, vp], i),
         "bn_unary_backward": ([i, V, V, V, vp], i), "bn_fill": ([V, C.c_double, vp], i),
         "bn_sum": ([V, V, i, vp], i), "bn_argmax": ([V, V, vp], i), "bn_copy": ([V, V, vp], i),
@@ -172,6 +173,20 @@ def gqa_prefill(q, k, v, o=None, scale=None, causal=True, seq_offset=0, stream=N
     call("bn_gqa_prefill", _torch_dtype_code(q), q.data_ptr(), k.data_ptr(), v.data_ptr(),
          o.data_ptr(), B, Sq, Skv, H, Hkv, D, q.stride(0), q.stride(1), k.stride(0),
          k.stride(1), o.stride(0), o.stride(1), sc, int(causal), seq_offset, stream_of(stream))
+    return o
+
+
+def fused_head_attention(q, k, v, n_heads, n_kv_heads, head_dim=64, o=None, scale=None,
+                         causal=True, seq_offset=0, stream=None):
+    """The fused-head chain in one launch: q [Sq, H*D], k/v [Sk, Hkv*D] fp32
+    torch 2-D views -> o [Sq, H*D]."""
+    if o is None:
+        import torch
+        o = torch.empty((q.shape[0], n_heads * head_dim), device=q.device, dtype=q.dtype)
+    sc = 1.0 / math.sqrt(head_dim) if scale is None else scale
+    call("bn_fused_head_attention", C.byref(view(q)), C.byref(view(k)), C.byref(view(v)),
+         C.byref(view(o)), n_heads, n_kv_heads, head_dim, sc, int(causal), seq_offset,
+         stream_of(stream))
     return o
 
 

@@ -10,7 +10,7 @@
 //   (:256-310), randgen_seed (bindings.cu:16-18), LLaMAConfig and
 //   LLaMAModelCpp (llama_bindings.hpp:31-122).
 // Additions (new names only): TensorBF16, Tensor*.rmsnorm_rope, gqa_prefill,
-// gqa_prefill_lse, gqa_prefill_backward,
+// gqa_prefill_lse, gqa_prefill_backward, fused_head_attention,
 // gqa_decode, repeat_kv, add_rmsnorm, silu_mul, pool_stats / pool_trim / pool_set_limit,
 // synchronize, set_stream / get_stream.
 //
@@ -442,6 +442,19 @@ PyTensor<DT> gqa_prefill(const PyTensor<DT> &q, const PyTensor<DT> &k, const PyT
   return out;
 }
 
+// The fused-head chain of llama_layers.hpp:83-109 (repeat_kv, q @ k_rep^T,
+// * scale, causal softmax, @ v_rep) in one launch: q [seq_q, n_heads*head_dim],
+// k/v [seq_kv, n_kv_heads*head_dim], fp32; returns [seq_q, n_heads*head_dim]
+TF fused_head_attention(const TF &q, const TF &k, const TF &v, int n_heads, int n_kv_heads,
+                        int head_dim, py::object scale, bool causal, int seq_offset) {
+  float sc = scale.is_none() ? (float)(1.0 / std::sqrt((double)head_dim)) : scale.cast<float>();
+  TF out(q.h, q.w, q.on_device);
+  bn_view qv = q.view(), kv = k.view(), vv = v.view(), ov = out.view();
+  check(bn_fused_head_attention(&qv, &kv, &vv, &ov, n_heads, n_kv_heads, head_dim, sc,
+                                causal ? 1 : 0, seq_offset, g_stream));
+  return out;
+}
+
 // gqa_prefill that also returns lse, TensorF [batch*n_heads, seq_q]: the
 // natural-log row log-sum-exp the backward recomputes the probabilities from
 template <int DT>
@@ -629,9 +642,10 @@ void fill_uniform(TF &t, float lo, float hi, uint64_t seed) {
 //     [hidden, 2I]) so each is one GEMM; weights() returns the reference's
 //     per-projection tensors as column views of them (loading through those
 //     views writes the model's weights).
-//   * attention = "fused_head" (default) computes the reference's chain as it
-//     is (llama_layers.hpp:96-109: Q K_rep^T over all heads at once, scale,
-//     causal softmax, @ V_rep); "per_head" runs per-head GQA on bn_gqa_prefill.
+//   * attention = "fused_head" (default) computes the reference's chain
+//     (llama_layers.hpp:96-109: Q K_rep^T over all heads at once, scale,
+//     causal softmax, @ V_rep) with bn_fused_head_attention, one launch;
+//     "per_head" runs per-head GQA on bn_gqa_prefill.
 //   * Embedding gathers on the device (bn_embedding) instead of copying the
 //     whole table to the host and back (llama_model.hpp:161-198).
 class LlamaModelCpp {
@@ -801,11 +815,17 @@ class LlamaModelCpp {
         attn = gqa_prefill<BN_F32>(q, k, v, 1, cfg_.num_attention_heads, cfg_.num_key_value_heads,
                                    D, py::none(), true, 0);
       } else {
-        TF krep = G > 1 ? repeat_kv<BN_F32>(k, G, D) : k;
-        TF vrep = G > 1 ? repeat_kv<BN_F32>(v, G, D) : v;
-        TF scores = matmul(q, krep.transpose());
-        TF scaled = unary(BN_MUL_SCALAR, scores, (float)(1.0 / std::sqrt((double)D)));
-        attn = matmul(softmax<BN_F32>(scaled, true, 0), vrep);
+        if (kv <= 512 && kv % 16 == 0 && D % 4 == 0) {
+          // repeat_kv, q @ k_rep^T, * scale, causal softmax, @ v_rep: one launch
+          attn = fused_head_attention(q, k, v, cfg_.num_attention_heads,
+                                      cfg_.num_key_value_heads, D, py::none(), true, 0);
+        } else {  // KV widths past the fused kernel's LDS budget: the chain op by op
+          TF krep = G > 1 ? repeat_kv<BN_F32>(k, G, D) : k;
+          TF vrep = G > 1 ? repeat_kv<BN_F32>(v, G, D) : v;
+          TF scores = matmul(q, krep.transpose());
+          TF scaled = unary(BN_MUL_SCALAR, scores, (float)(1.0 / std::sqrt((double)D)));
+          attn = matmul(softmax<BN_F32>(scaled, true, 0), vrep);
+        }
       }
       TF o = matmul(attn, L.wo);
       TF x2 = hdn.like();
@@ -917,6 +937,10 @@ PYBIND11_MODULE(bten, m) {
   });
 
   // ----------------------------------------------------- fused attention
+  m.def("fused_head_attention", &fused_head_attention, py::arg("query"), py::arg("key"),
+        py::arg("value"), py::arg("n_heads") = 32, py::arg("n_kv_heads") = 4,
+        py::arg("head_dim") = 64, py::arg("scale") = py::none(), py::arg("causal") = true,
+        py::arg("seq_offset") = 0);
   m.def("gqa_prefill", &gqa_prefill<BN_F32>, py::arg("q"), py::arg("k"), py::arg("v"),
         py::arg("batch") = 1, py::arg("n_heads") = 32, py::arg("n_kv_heads") = 4,
         py::arg("head_dim") = 64, py::arg("scale") = py::none(), py::arg("causal") = true,

@@ -8,12 +8,15 @@ reference layers runs on this build:
 * ``RotaryEmbedding.__call__``  -> ``x.rope(offset, head_dim, theta)``   (:40-42)
 * ``GroupedQueryAttention``     -> the sequence of :154-186.
 
-``GroupedQueryAttention`` has two modes:
+``GroupedQueryAttention`` has three modes:
 
-``"fused_head"`` (default) reproduces the reference exactly: one causal
+``"fused_head"`` (default) computes the reference's attention: one causal
 softmax over the full hidden width, ``softmax(0.125 * Q_rope @ K_rep^T) @ V_rep``
-(every head shares one probability matrix), with ``repeat_kv`` done on the
-device instead of the reference's host round trip (:105-138).
+(every head shares one probability matrix), in one launch
+(``bten.fused_head_attention``: no K_rep / V_rep and no S x S matrices).
+``"fused_head_ops"`` runs the same chain op by op as the reference does
+(``repeat_kv`` on the device instead of the reference's host round trip,
+:105-138; then matmul, scale, softmax, matmul).
 
 ``"per_head"`` is grouped-query attention with one softmax per query head
 (query head h reads KV head h // (H/Hkv)), computed by the fused
@@ -73,8 +76,8 @@ class GroupedQueryAttention:
 
     def __init__(self, config, is_cuda: bool = True, mode: str = "fused_head",
                  seed: int | None = None, init_std: float | None = None):
-        if mode not in ("fused_head", "per_head"):
-            raise ValueError("mode must be 'fused_head' or 'per_head'")
+        if mode not in ("fused_head", "fused_head_ops", "per_head"):
+            raise ValueError("mode must be 'fused_head', 'fused_head_ops' or 'per_head'")
         self.config = config
         self.is_cuda = is_cuda
         self.mode = mode
@@ -111,6 +114,10 @@ class GroupedQueryAttention:
             attn_output = bten.gqa_prefill(query, key, value, 1, self.num_heads,
                                            self.num_kv_heads, self.head_dim, self.scale,
                                            use_causal_mask, position_offset)
+        elif self.mode == "fused_head":
+            attn_output = bten.fused_head_attention(query, key, value, self.num_heads,
+                                                    self.num_kv_heads, self.head_dim, self.scale,
+                                                    use_causal_mask, position_offset)
         else:
             n_rep = self.num_heads // self.num_kv_heads
             if n_rep > 1:

@@ -403,15 +403,63 @@ def bench_block(steps, warmup):
     xt = bten.TensorF(S, hid)
     xt.copy_from_numpy(x)
     out = {}
-    for mode in ("fused_head", "per_head"):
+    for mode in ("fused_head", "fused_head_ops", "per_head"):
         norm = RMSNorm(hid, eps=1e-5)
         attn = GroupedQueryAttention(bten.LLaMAConfig(), mode=mode)
         attn.load_weights(*ws)
         ms = time_launches(lambda i: attn(norm(xt)), steps, warmup)
         out[mode] = {"ms_per_block": round(ms, 4)}
     out["note"] = ("bten launches on the legacy default stream, timed with events on the same "
-                   "stream; includes the per-op pool allocations of the op surface")
+                   "stream; includes the per-op pool allocations of the op surface. fused_head = "
+                   "the chain's attention in one launch (bn_fused_head_attention); "
+                   "fused_head_ops = the same chain op by op (repeat_kv x2, QK^T GEMM, scale, "
+                   "softmax, PV GEMM)")
+    out["fused_head_kernel"] = bench_fused_head_kernel(steps, warmup)
     return out, (x, ws)
+
+
+def bench_fused_head_kernel(steps, warmup, S=128):
+    """The attention of config 1 alone through the C ABI: bn_fused_head_attention
+    against the op-by-op chain it replaces, on the same torch buffers (q
+    [128, 2048], k/v [128, 256], fp32).  Device time from graph replays of 20
+    back-to-back launches (no host gaps); the chain eagerly (its GEMMs are
+    library calls)."""
+    import ctypes as C
+    import torch
+    import bnhip
+    g = torch.Generator(device="cuda").manual_seed(0)
+    q = torch.randn((S, 2048), generator=g, device="cuda")
+    k = torch.randn((S, 256), generator=g, device="cuda")
+    v = torch.randn((S, 256), generator=g, device="cuda")
+    o = torch.empty((S, 2048), device="cuda")
+    fused = lambda i: bnhip.fused_head_attention(q, k, v, 32, 4, 64, o=o, scale=0.125)
+    graph_ms = time_graph(fused, 20, max(steps, 20), warmup, check=o)
+    eager_ms = time_launches(fused, max(steps, 20), warmup)
+    kr, vr = torch.empty((S, 2048), device="cuda"), torch.empty((S, 2048), device="cuda")
+    sc, p, oc = (torch.empty((S, S), device="cuda"), torch.empty((S, S), device="cuda"),
+                 torch.empty((S, 2048), device="cuda"))
+    V = lambda t: C.byref(bnhip.view(t))
+    st = bnhip.stream_of()
+    krt = kr.t()
+
+    def chain(i):
+        bnhip.call("bn_repeat_kv", V(k), V(kr), 64, 8, st)
+        bnhip.call("bn_repeat_kv", V(v), V(vr), 64, 8, st)
+        bnhip.call("bn_matmul", V(q), V(krt), V(sc), st)
+        bnhip.call("bn_unary", bnhip.BN_MUL_SCALAR, V(sc), 0.125, V(sc), st)
+        bnhip.call("bn_softmax", V(sc), V(p), 1, 0, st)
+        bnhip.call("bn_matmul", V(p), V(vr), V(oc), st)
+    chain_ms = time_launches(chain, max(steps, 20), warmup)
+    torch.cuda.synchronize()
+    diff = float(((o - oc).abs().max() / oc.abs().max()).item())
+    flop = 2 * 2 * 2048 * (S * (S + 1) // 2)   # the chain's causal QK^T and PV, 2048 wide
+    return {"config": "Sq = Sk = 128, 32/4 heads, head_dim 64, fp32, causal",
+            "device_us": round(graph_ms * 1e3, 2), "eager_us_per_launch": round(eager_ms * 1e3, 2),
+            "chain_eager_us": round(chain_ms * 1e3, 2),
+            "chain_flop_causal": flop, "max_rel_diff_vs_chain": diff,
+            "algorithmic_bytes": 4 * (2 * S * 2048 + 2 * S * 256),
+            "note": "device_us from graph replays; the chain = repeat_kv x2, bn_matmul (library "
+                    "GEMM), scale, softmax, bn_matmul, launched eagerly"}
 
 
 def cpu_baseline_block(x, ws):

@@ -158,6 +158,24 @@ int bn_linear_rope(const bn_view *x, const bn_view *w, const bn_view *y,
  * out column block kv_h*n_rep + r = kv column block kv_h, on the device. */
 int bn_repeat_kv(const bn_view *kv, const bn_view *out, int head_dim, int n_rep,
                  void *stream);
+/* The fused-head attention chain of src/llama/llama_layers.hpp:83-109 in one
+ * launch: with n_rep = n_heads / n_kv_heads and K_rep / V_rep = repeat_kv(k /
+ * v, n_rep) (head h reads KV head h / n_rep),
+ *   o = softmax((q @ K_rep^T) * scale, causal, seq_offset) @ V_rep
+ * -- ONE probability matrix over the full n_heads*head_dim-wide rows, as the
+ * reference's op_mm / op_multiply / op_softmax / op_mm chain computes it --
+ * without forming K_rep, V_rep or the seq_q x seq_kv matrices.
+ * q, o: [seq_q, n_heads*head_dim]; k, v: [seq_kv, n_kv_heads*head_dim]; fp32
+ * views whose columns are contiguous and whose rows start on 16-byte
+ * boundaries.  Causal mask as op_softmax.cuh:89-99 (key j is visible to row i
+ * iff j <= i + seq_offset); a row with no visible key is written as zeros, as
+ * the chain's all-zero probability row gives.  Needs head_dim % 4 == 0 and
+ * n_kv_heads*head_dim a multiple of 16, at most 512.  Results agree with the
+ * chain to fp32 rounding (the sums associate differently). */
+int bn_fused_head_attention(const bn_view *q, const bn_view *k, const bn_view *v,
+                            const bn_view *o, int n_heads, int n_kv_heads,
+                            int head_dim, float scale, int causal, int seq_offset,
+                            void *stream);
 
 /* Elementwise surface used by the layers (src/ops/op_elemwise.cuh:326-507,
  * op_silu.cuh, op_reduction.cuh).  Binary ops broadcast b along a unit

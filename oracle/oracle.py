@@ -200,6 +200,18 @@ def repeat_kv(kv, head_dim, n_rep):
     return out
 
 
+def fused_head_attention(q, k, v, head_dim, n_rep, scale_c, causal=True, seq_offset=0):
+    """The reference's fused-head chain (llama_layers.hpp:87-109) on the
+    oracle's own ops: repeat_kv (:87-89), q @ k_rep^T (:96-98), * scale (:101),
+    softmax(causal, seq_offset) (:105), @ v_rep (:108-109).  q [Sq, H*D],
+    k/v [Sk, Hkv*D] float32 -> [Sq, H*D]."""
+    k, v = _f32(k), _f32(v)
+    kr = repeat_kv(k, head_dim, n_rep) if n_rep > 1 else k
+    vr = repeat_kv(v, head_dim, n_rep) if n_rep > 1 else v
+    s = scale(matmul(q, np.ascontiguousarray(kr.T)), scale_c)
+    return matmul(softmax(s, causal, seq_offset), vr)
+
+
 def gqa_prefill(q, k, v, scale, causal=True, seq_offset=0):
     """q [B,Sq,H,D], k/v [B,Skv,Hkv,D] float32 -> o [B,Sq,H,D]."""
     q, k, v = _f32(q), _f32(k), _f32(v)

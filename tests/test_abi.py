@@ -315,3 +315,26 @@ def test_llama_decode_validation():
     s, m = st("bn_llama_decode", C.byref(c), fake, fake, fake, full, 0, 0, 1, fake,
               C.c_void_p(fake + 16), n, None)
     assert s == B.BN_ERR_UNSUPPORTED and "256-byte" in m
+
+
+@pytest.mark.parametrize("kw,status,msg", [
+    (dict(Hkv=3), B.BN_ERR_SHAPE, "multiple of n_kv_heads"),
+    (dict(qw=1024), B.BN_ERR_SHAPE, "query and output"),
+    (dict(kh=9), B.BN_ERR_SHAPE, "key and value"),
+    (dict(H=32, Hkv=16, kw_=1024), B.BN_ERR_UNSUPPORTED, "<= 512"),
+    (dict(D=6, qw=192, kw_=24, H=32, Hkv=4), B.BN_ERR_UNSUPPORTED, "head_dim % 4"),
+    (dict(dt=B.BN_BF16), B.BN_ERR_UNSUPPORTED, "unsupported dtype"),
+    (dict(), B.BN_ERR_NOT_DEVICE, "only GPU implementation available"),
+])
+def test_fused_head_attention_validation(kw, status, msg):
+    """Shape, limit and dtype checks come before the device check (host
+    views, never dereferenced: no GPU needed)."""
+    a = dict(S=8, qw=2048, kh=8, kw_=256, H=32, Hkv=4, D=64, dt=B.BN_F32)
+    a.update(kw)
+    q = V(a["S"], a["qw"], dtype=a["dt"])
+    k = V(a["kh"], a["kw_"])
+    v = V(8, a["kw_"])
+    o = V(a["S"], a["qw"])
+    s, m = st("bn_fused_head_attention", q, k, v, o, a["H"], a["Hkv"], a["D"], 0.125, 1, 0, None)
+    assert s == status, m
+    assert m.startswith("Fused-head attention:") and msg in m, m

@@ -33,7 +33,7 @@ def config1_inputs(S=128, hidden=2048, H=32, Hkv=4):
     return x, ws
 
 
-@pytest.mark.parametrize("mode", ["fused_head", "per_head"])
+@pytest.mark.parametrize("mode", ["fused_head", "fused_head_ops", "per_head"])
 def test_config1_attention_block(mode):
     """RMSNorm(eps 1e-5) -> Q/K/V -> RoPE -> causal softmax(QK^T/8) V -> O, fp32."""
     x, (wq, wk, wv, wo) = config1_inputs()
@@ -47,6 +47,19 @@ def test_config1_attention_block(mode):
     xn = O.rmsnorm(x, np.ones((1, 2048), np.float32), 1e-5)
     ref = O.gqa_layer(xn, wq, wk, wv, wo, 32, 4, 10000.0, 0, per_head=(mode == "per_head"))
     assert_close(out, ref, FP32_TOL, f"config 1 {mode}")
+
+
+def test_config1_fused_head_kernel_equals_op_chain():
+    """bten.fused_head_attention against the same chain op by op on the device
+    (repeat_kv, QK^T, scale, softmax, PV) on config 1's shapes."""
+    r = np.random.default_rng(4)
+    q, k, v = (bten.TensorF(128, w) for w in (2048, 256, 256))
+    for t in (q, k, v):
+        t.copy_from_numpy(r.standard_normal(t.shape).astype(np.float32))
+    one = bten.fused_head_attention(q, k, v, 32, 4, 64, 0.125, True, 0).to_numpy()
+    kr, vr = bten.repeat_kv(k, 8, 64), bten.repeat_kv(v, 8, 64)
+    chain = ((q @ kr.T) * 0.125).softmax(True, 0) @ vr
+    assert_close(one, chain.to_numpy(), FP32_TOL, "fused kernel vs op chain")
 
 
 def test_config1_offset_and_views():

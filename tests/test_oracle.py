@@ -412,6 +412,70 @@ def test_gqa_layer_chain(per_head):
     assert relerr(out, other) > 1e-3   # fused-head and per-head really differ
 
 
+def fused_head_torch64(q, k, v, D, n_rep, sc, causal, off):
+    """The fused-head chain in torch fp64: heads expanded with
+    repeat_interleave on a [S, Hkv, D] view, one masked softmax over the full
+    width; rows with no visible key are zero (the chain's all-zero P row)."""
+    q, k, v = (torch.from_numpy(np.asarray(a, np.float64)) for a in (q, k, v))
+    Sq, Sk = q.shape[0], k.shape[0]
+    kr = k.view(Sk, -1, D).repeat_interleave(n_rep, dim=1).reshape(Sk, -1)
+    vr = v.view(Sk, -1, D).repeat_interleave(n_rep, dim=1).reshape(Sk, -1)
+    s = (q @ kr.T) * sc
+    if causal:
+        i = torch.arange(Sq).unsqueeze(1)
+        j = torch.arange(Sk).unsqueeze(0)
+        s = s.masked_fill(j > i + off, float("-inf"))
+    p = torch.nan_to_num(torch.softmax(s, dim=1), nan=0.0)
+    return (p @ vr).numpy()
+
+
+@pytest.mark.parametrize("Sq,Sk,H,Hkv,D,causal,off", [
+    (12, 12, 8, 2, 16, True, 0), (9, 20, 4, 4, 8, True, 11), (7, 7, 6, 2, 4, False, 0),
+    (5, 5, 4, 1, 8, True, -2)])
+def test_fused_head_attention_vs_torch(Sq, Sk, H, Hkv, D, causal, off):
+    r = rng(17)
+    q = r.standard_normal((Sq, H * D)).astype(np.float32)
+    k = r.standard_normal((Sk, Hkv * D)).astype(np.float32)
+    v = r.standard_normal((Sk, Hkv * D)).astype(np.float32)
+    sc = 1.0 / math.sqrt(D)
+    out = O.fused_head_attention(q, k, v, D, H // Hkv, sc, causal, off)
+    ref = fused_head_torch64(q, k, v, D, H // Hkv, sc, causal, off)
+    assert relerr(out, ref) < 1e-5
+    if off < 0:   # rows 0 and 1 see no key: exact zeros
+        assert not out[:-off].any()
+
+
+def test_fused_head_attention_uniform_keys_closed_form():
+    # identical keys: every visible key gets the same weight, so row i of head
+    # h is the mean of the visible rows of V's KV head h // n_rep
+    r = rng(18)
+    S, H, Hkv, D, off = 10, 8, 2, 4, 3
+    q = r.standard_normal((S, H * D)).astype(np.float32)
+    k = np.tile(r.standard_normal((1, Hkv * D)).astype(np.float32), (S, 1))
+    v = r.standard_normal((S, Hkv * D)).astype(np.float32)
+    out = O.fused_head_attention(q, k, v, D, H // Hkv, 0.5, True, off)
+    for i in range(S):
+        mean = v[:min(S, i + off + 1)].astype(np.float64).mean(0)
+        for h in range(H):
+            g = h // (H // Hkv)
+            np.testing.assert_allclose(out[i, h * D:(h + 1) * D], mean[g * D:(g + 1) * D],
+                                       rtol=1e-5, atol=1e-6)
+
+
+def test_fused_head_check_catches_planted_group_slip():
+    # head h reading KV head h % Hkv instead of h // n_rep fails the torch pin
+    r = rng(19)
+    S, H, Hkv, D = 8, 8, 2, 8
+    q = r.standard_normal((S, H * D)).astype(np.float32)
+    k = r.standard_normal((S, Hkv * D)).astype(np.float32)
+    v = r.standard_normal((S, Hkv * D)).astype(np.float32)
+    kt, vt = np.tile(k, (1, H // Hkv)), np.tile(v, (1, H // Hkv))   # the slip
+    s = O.scale(O.matmul(q, np.ascontiguousarray(kt.T)), 0.25)
+    slipped = O.matmul(O.softmax(s, True, 0), vt)
+    ref = fused_head_torch64(q, k, v, D, H // Hkv, 0.25, True, 0)
+    assert relerr(slipped, ref) > 1e-2
+
+
 # ---------------------------------------------------------------- backward
 def test_rmsnorm_backward_vs_torch():
     r = rng(17)
