@@ -47,6 +47,21 @@ int decode_scratch_setup(int device);
 // ensure_device().
 int device_cu_count();
 
+// bn_linear_rope with the split-k reduction's epilogue chosen by the caller
+// (bn_linear.hip): kLinEpiPlain is bn_linear_rope's own (the rotation of the
+// first rope_cols columns; with k_dst, columns [app_col, app_col + app_w) of
+// row r are also stored to k_dst + r*app_rs and the next app_w columns to
+// v_dst + r*app_rs: a QKV projection's K and V appended to the caches);
+// kLinEpiSilu reads the output as [gate | up] halves and writes
+// y = silu(gate) * up, y [m, n/2].  The slabs are summed in one order for
+// every epilogue, so a fused epilogue gives the bits of the unfused ops.
+// The epilogues need the split-k path (always taken for m <= 8).
+constexpr int kLinEpiPlain = 0, kLinEpiSilu = 1;
+int linear_run(const bn_view *x, const bn_view *w, const bn_view *y, int rope_cols,
+               int position_offset, int head_dim, float theta, void *workspace,
+               size_t workspace_bytes, int epi, float *k_dst, float *v_dst, int app_col, int app_w,
+               int64_t app_rs, void *stream);
+
 // ------------------------------------------------------------ validation
 inline size_t dtype_size(int dt) { return dt == BN_BF16 ? 2 : 4; }
 

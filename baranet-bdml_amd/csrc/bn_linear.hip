@@ -52,7 +52,19 @@ struct LinParams {
   int64_t x_rs, w_rs, y_rs;
   int m, n, k, kchunk;  // kchunk: k per slab, a multiple of the stage depth
   int rope_cols, head_dim, pos0;
+  // epilogue extras of the split-k reduction (decode steps, fp32): columns
+  // [app_col, app_col + app_w) of row r also go to k_dst + r*app_rs and
+  // [app_col + app_w, app_col + 2*app_w) to v_dst + r*app_rs (the K and V
+  // rows of a QKV projection appended to the caches); null: none
+  float *k_dst, *v_dst;
+  int app_col, app_w;
+  int64_t app_rs;
 };
+
+// reduction epilogues: EPI_PLAIN writes y (rotated in the first rope_cols
+// columns); EPI_SILU reads the slabs as gate | up halves and writes
+// y = silu(gate) * up, the width of one half
+constexpr int EPI_PLAIN = kLinEpiPlain, EPI_SILU = kLinEpiSilu;
 
 __device__ __forceinline__ bf16x4_t tr16(const bf16_t *lds) {
   const s16x4_t r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
@@ -186,32 +198,67 @@ __global__ __launch_bounds__(256, 2) void linear_kernel(LinParams p, RopeFreqs f
   }
 }
 
-// y = sum of the slabs' partial sums (slab 0 first), then the rotation: one
-// thread per four consecutive columns of one row
-template <typename T>
+// Split-k slab sums, in one order for every caller and epilogue: wave w of
+// a 256-thread workgroup adds slabs w, w+4, w+8, ... in increasing order
+// (loads 8 deep), and the four wave sums meet in LDS as ((s0 + s1) + s2) + s3.
+// Lane l owns columns 4l..4l+3 of the workgroup's 256-column strip; grid y
+// is the row.  Four waves per strip spread the slab reads of a few-row
+// projection over 4x the threads of a one-thread-per-column sum.
+__device__ __forceinline__ float4 add4(float4 a, float4 b) {
+  return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
+}
+__device__ __forceinline__ float4 slab_sum_wave(const float *src, int nsplit, int64_t stride, int w) {
+  constexpr int B = 8;
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int s0 = w; s0 < nsplit; s0 += 4 * B) {
+    float4 a[B];
+#pragma unroll
+    for (int j = 0; j < B; ++j)
+      a[j] = *(const float4 *)(src + (int64_t)min(s0 + 4 * j, nsplit - 1) * stride);
+#pragma unroll
+    for (int j = 0; j < B; ++j)
+      if (s0 + 4 * j < nsplit) acc = add4(acc, a[j]);
+  }
+  return acc;
+}
+
+template <typename T, int EPI>
 __global__ __launch_bounds__(256) void linear_reduce_kernel(LinParams p, RopeFreqs fr, int nsplit) {
-  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  const int q = p.n >> 2;
-  if (idx >= (int64_t)p.m * q) return;
-  const int gm = (int)(idx / q), gn = (int)(idx % q) * 4;
+  __shared__ float4 red[EPI == EPI_SILU ? 2 : 1][3][64];
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int gm = blockIdx.y;
+  const int width = EPI == EPI_SILU ? p.n / 2 : p.n;  // output columns
+  const int gn = blockIdx.x * 256 + lane * 4;
+  const int gc = min(gn, width - 4);  // clamped: loads stay in the row
   const int64_t mn = (int64_t)p.m * p.n;
-  const float *src = p.part + (int64_t)gm * p.n + gn;
-  float v[4] = {0.f, 0.f, 0.f, 0.f};
-  // groups of 16 slabs: all loads of a group in flight, then added in slab order
-  constexpr int G = 16;
-  for (int z0 = 0; z0 < nsplit; z0 += G) {
-    float4 a[G];
+  const float *src = p.part + (int64_t)gm * p.n + gc;
+  float4 a = slab_sum_wave(src, nsplit, mn, w);
+  float4 b = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (EPI == EPI_SILU) b = slab_sum_wave(src + width, nsplit, mn, w);
+  if (w > 0) {
+    red[0][w - 1][lane] = a;
+    if constexpr (EPI == EPI_SILU) red[1][w - 1][lane] = b;
+  }
+  __syncthreads();
+  if (w > 0 || gn >= width) return;
+  a = add4(add4(add4(a, red[0][0][lane]), red[0][1][lane]), red[0][2][lane]);
+  float v[4] = {a.x, a.y, a.z, a.w};
+  if constexpr (EPI == EPI_SILU) {
+    b = add4(add4(add4(b, red[1][0][lane]), red[1][1][lane]), red[1][2][lane]);
+    const float u[4] = {b.x, b.y, b.z, b.w};
 #pragma unroll
-    for (int j = 0; j < G; ++j)
-      a[j] = z0 + j < nsplit ? *(const float4 *)(src + (z0 + j) * mn) : make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-    for (int j = 0; j < G; ++j) {
-      if (z0 + j < nsplit) {
-        v[0] += a[j].x; v[1] += a[j].y; v[2] += a[j].z; v[3] += a[j].w;
+    for (int j = 0; j < 4; ++j) v[j] = v[j] / (1.0f + expf(-v[j])) * u[j];  // as silu_mul_rows_kernel
+  } else {
+    rope4(v, gm, gn, p, fr);
+    if (p.k_dst) {  // K | V columns appended to the caches (fp32)
+      const int c = gn - p.app_col;
+      if (c >= 0 && c < 2 * p.app_w) {
+        float *dst = (c < p.app_w ? p.k_dst + c : p.v_dst + (c - p.app_w)) + gm * p.app_rs;
+        *(float4 *)dst = make_float4(v[0], v[1], v[2], v[3]);
       }
     }
   }
-  rope4(v, gm, gn, p, fr);
   store4<T>((T *)p.y + gm * p.y_rs + gn, v);
 }
 
@@ -352,10 +399,16 @@ extern "C" size_t bn_linear_rope_workspace_size(int dtype, int m, int n, int k) 
   return (small || ns > 1) ? (size_t)ns * m * n * sizeof(float) : 0;
 }
 
-extern "C" int bn_linear_rope(const bn_view *x, const bn_view *w, const bn_view *y, int rope_cols,
-                              int position_offset, int head_dim, float theta, void *workspace,
-                              size_t workspace_bytes, void *stream) {
-  const char *op = "Linear";
+namespace bn {
+
+// bn_linear_rope with a reduction epilogue (EPI_SILU: y is [m, n/2]) and
+// optional K/V appends (LinParams::k_dst); the epilogues exist only on the
+// split-k paths, which the few-rows projections always take.
+int linear_run(const bn_view *x, const bn_view *w, const bn_view *y, int rope_cols,
+               int position_offset, int head_dim, float theta, void *workspace,
+               size_t workspace_bytes, int epi, float *k_dst, float *v_dst, int app_col, int app_w,
+               int64_t app_rs, void *stream) {
+  const char *op = epi == EPI_SILU ? "Linear+SwiGLU" : "Linear";
   const unsigned mask = (1u << BN_F32) | (1u << BN_BF16);
   int st;
   if ((st = check_view(x, op, "x", mask))) return st;
@@ -363,7 +416,8 @@ extern "C" int bn_linear_rope(const bn_view *x, const bn_view *w, const bn_view 
   if ((st = check_view(y, op, "y", mask))) return st;
   if (x->dtype != w->dtype || x->dtype != y->dtype)
     return fail(BN_ERR_UNSUPPORTED, std::string(op) + ": x, w and y must share one dtype");
-  if (x->w != w->h || y->h != x->h || y->w != w->w)
+  const int64_t y_cols = epi == EPI_SILU ? (int64_t)w->w / 2 : w->w;
+  if (x->w != w->h || y->h != x->h || y->w != y_cols || (epi == EPI_SILU && w->w % 8))
     return fail(BN_ERR_SHAPE, std::string(op) + ": shape mismatch x:(" + std::to_string(x->h) +
                                   ", " + std::to_string(x->w) + "), w:(" + std::to_string(w->h) +
                                   ", " + std::to_string(w->w) + "), y:(" + std::to_string(y->h) +
@@ -392,10 +446,14 @@ extern "C" int bn_linear_rope(const bn_view *x, const bn_view *w, const bn_view 
                                         ": rows must start 16-byte aligned and widths be multiples of 16 bytes");
   if ((st = require_device(op, {x, w, y}))) return st;
   if (y->h == 0 || y->w == 0) return BN_OK;
-  const int m = y->h, n = y->w, k = x->w;
+  const int m = y->h, n = w->w, k = x->w;
   int nsplit, kchunk;
   bool small;
   plan(dt, m, n, k, &small, &nsplit, &kchunk);
+  if ((epi != EPI_PLAIN || k_dst) && !(small || nsplit > 1))
+    return fail(BN_ERR_UNSUPPORTED, std::string(op) + ": the fused epilogue needs the split-k path");
+  if (k_dst && (dt != BN_F32 || app_col < 0 || app_col % 4 || app_w % 4 || app_col + 2 * app_w > n))
+    return fail(BN_ERR_UNSUPPORTED, std::string(op) + ": bad K/V append columns");
   const size_t need = (small || nsplit > 1) ? (size_t)nsplit * m * n * sizeof(float) : 0;
   if (workspace && workspace_bytes < need)
     return fail(BN_ERR_INVALID_ARG, std::string(op) + ": workspace of " +
@@ -404,7 +462,7 @@ extern "C" int bn_linear_rope(const bn_view *x, const bn_view *w, const bn_view 
   if (workspace && (reinterpret_cast<uintptr_t>(workspace) & 15u))
     return fail(BN_ERR_UNSUPPORTED, std::string(op) + ": workspace must be 16-byte aligned");
   // grid limits: row tiles on grid y (at most 65535), reduction threads
-  if ((!small && (m + TM - 1) / TM > 65535) || (int64_t)m * (n / 4) / 256 >= 0x7fffffff)
+  if ((!small && (m + TM - 1) / TM > 65535) || ((small || nsplit > 1) && m > 65535))
     return fail(BN_ERR_UNSUPPORTED, std::string(op) + ": problem too large");
   if ((st = ensure_device())) return st;
   hipStream_t s = as_stream(stream);
@@ -422,6 +480,7 @@ extern "C" int bn_linear_rope(const bn_view *x, const bn_view *w, const bn_view 
   p.x_rs = x->stride_h; p.w_rs = w->stride_h; p.y_rs = y->stride_h;
   p.m = m; p.n = n; p.k = k; p.kchunk = kchunk;
   p.rope_cols = rope_cols; p.head_dim = rope_cols ? head_dim : 2; p.pos0 = position_offset;
+  p.k_dst = k_dst; p.v_dst = v_dst; p.app_col = app_col; p.app_w = app_w; p.app_rs = app_rs;
   if (small) {
     const int cols = 64 * (dt == BN_BF16 ? 8 : 4);
     dim3 grid((unsigned)((n + cols - 1) / cols), (unsigned)nsplit);
@@ -447,12 +506,18 @@ extern "C" int bn_linear_rope(const bn_view *x, const bn_view *w, const bn_view 
   }
   hipError_t e = hipGetLastError();
   if (e == hipSuccess && need) {
-    const int64_t th = (int64_t)m * (n / 4);
-    const dim3 rg((unsigned)((th + 255) / 256));
-    if (dt == BN_F32)
-      hipLaunchKernelGGL(linear_reduce_kernel<float>, rg, dim3(256), 0, s, p, fr, nsplit);
-    else
-      hipLaunchKernelGGL(linear_reduce_kernel<bf16_t>, rg, dim3(256), 0, s, p, fr, nsplit);
+    const dim3 rg((unsigned)((y->w + 255) / 256), (unsigned)m);
+    if (epi == EPI_SILU) {
+      if (dt == BN_F32)
+        hipLaunchKernelGGL((linear_reduce_kernel<float, EPI_SILU>), rg, dim3(256), 0, s, p, fr, nsplit);
+      else
+        hipLaunchKernelGGL((linear_reduce_kernel<bf16_t, EPI_SILU>), rg, dim3(256), 0, s, p, fr, nsplit);
+    } else {
+      if (dt == BN_F32)
+        hipLaunchKernelGGL((linear_reduce_kernel<float, EPI_PLAIN>), rg, dim3(256), 0, s, p, fr, nsplit);
+      else
+        hipLaunchKernelGGL((linear_reduce_kernel<bf16_t, EPI_PLAIN>), rg, dim3(256), 0, s, p, fr, nsplit);
+    }
     e = hipGetLastError();
   }
   st = e == hipSuccess ? BN_OK : hip_fail(e, __FILE__, __LINE__);
@@ -461,4 +526,13 @@ extern "C" int bn_linear_rope(const bn_view *x, const bn_view *w, const bn_view 
     if (st == BN_OK) st = st2;
   }
   return st;
+}
+
+}  // namespace bn
+
+extern "C" int bn_linear_rope(const bn_view *x, const bn_view *w, const bn_view *y, int rope_cols,
+                              int position_offset, int head_dim, float theta, void *workspace,
+                              size_t workspace_bytes, void *stream) {
+  return linear_run(x, w, y, rope_cols, position_offset, head_dim, theta, workspace, workspace_bytes,
+                    EPI_PLAIN, nullptr, nullptr, 0, 0, 0, stream);
 }

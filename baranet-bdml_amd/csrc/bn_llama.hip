@@ -5,8 +5,11 @@
 // The reference has no KV cache and reruns the whole prefix for every token
 // (llama_model.py:135-141, llama_model.hpp:161-198); its decoder layer is
 // llama_layers.hpp:241-272.  Every step is the path's own kernels:
-// bn_linear_rope (projections, the QKV rotation in its epilogue),
-// bn_gqa_decode, bn_add_rmsnorm, bn_silu_mul, bn_rmsnorm and bn_argmax.
+// bn_linear_rope's projections (the QKV rotation and the K/V cache append in
+// its split-k reduction; the SwiGLU product in the gate|up reduction),
+// bn_gqa_decode, bn_add_rmsnorm, bn_rmsnorm and bn_argmax.  The fused
+// reductions sum the slabs in the same order as the unfused ones, so the
+// tokens and caches are those of the op-by-op step loop.
 #include <algorithm>
 
 #include "bn_common.hpp"
@@ -60,7 +63,7 @@ size_t a256(size_t n) { return (n + 255) & ~(size_t)255; }
 
 // workspace regions, in bytes from the start
 struct Plan {
-  size_t hdn, xn, qkv, o, attn, gu, act, mlp, logits, tok, lens, lin, dec, total;
+  size_t hdn, xn, qkv, o, attn, act, mlp, logits, tok, lens, lin, dec, total;
   size_t lin_bytes, dec_bytes;
 };
 
@@ -79,7 +82,6 @@ Plan plan_of(const bn_llama_config *c) {
   p.qkv = take(4 * (size_t)(c->hidden + 2 * kv));
   p.o = take(4 * (size_t)c->hidden);
   p.attn = take(4 * (size_t)c->hidden);
-  p.gu = take(4 * (size_t)2 * c->intermediate);
   p.act = take(4 * (size_t)c->intermediate);
   p.mlp = take(4 * (size_t)c->hidden);
   p.logits = take(4 * (size_t)c->vocab);
@@ -152,7 +154,7 @@ extern "C" int bn_llama_decode(const bn_llama_config *c, const float *embed, con
   }
   char *W = (char *)ws;
   float *hdn = (float *)(W + pl.hdn), *xn = (float *)(W + pl.xn), *qkv = (float *)(W + pl.qkv);
-  float *o = (float *)(W + pl.o), *attn = (float *)(W + pl.attn), *gu = (float *)(W + pl.gu);
+  float *o = (float *)(W + pl.o), *attn = (float *)(W + pl.attn);
   float *act = (float *)(W + pl.act), *mlp = (float *)(W + pl.mlp), *logits = (float *)(W + pl.logits);
   int32_t *lens = (int32_t *)(W + pl.lens);
   void *lin_ws = W + pl.lin, *dec_ws = pl.dec_bytes ? W + pl.dec : nullptr;
@@ -162,8 +164,6 @@ extern "C" int bn_llama_decode(const bn_llama_config *c, const float *embed, con
   const bn_view v_hdn = fview(hdn, 1, hid, hid), v_xn = fview(xn, 1, hid, hid);
   const bn_view v_qkv = fview(qkv, 1, hid + 2 * kv, hid + 2 * kv);
   const bn_view v_o = fview(o, 1, hid, hid), v_attn = fview(attn, 1, hid, hid);
-  const bn_view v_gu = fview(gu, 1, 2 * I, 2 * I);
-  bn_view v_gate = fview(gu, 1, I, 2 * I), v_up = fview(gu + I, 1, I, 2 * I);
   const bn_view v_act = fview(act, 1, I, I), v_mlp = fview(mlp, 1, hid, hid);
   const bn_view v_logits = fview(logits, 1, c->vocab, c->vocab);
   const bn_view v_lnf = fview(ln_f, 1, hid, hid), v_lm = fview(lm_head, hid, c->vocab, c->vocab);
@@ -189,23 +189,22 @@ extern "C" int bn_llama_decode(const bn_llama_config *c, const float *embed, con
       const bn_view wo = fview(L.wo, hid, hid, hid), wgu = fview(L.wgu, hid, 2 * I, 2 * I);
       const bn_view wd = fview(L.wd, I, hid, hid), ln2 = fview(L.ln2, 1, hid, hid);
       const bn_view nxt = l + 1 < c->n_layers ? fview(layers[l + 1].ln1, 1, hid, hid) : v_lnf;
-      // Q, K and V (Q and K rotated at position pos), K and V appended to the caches
-      if ((st = bn_linear_rope(&v_xn, &wqkv, &v_qkv, hid + kv, pos, hd, c->rope_theta, lin_ws,
-                               pl.lin_bytes, stream)))
+      // Q, K and V (Q and K rotated at position pos); the reduction also
+      // appends K and V to the caches at row pos
+      if ((st = linear_run(&v_xn, &wqkv, &v_qkv, hid + kv, pos, hd, c->rope_theta, lin_ws,
+                           pl.lin_bytes, kLinEpiPlain, L.k_cache + (int64_t)pos * kv,
+                           L.v_cache + (int64_t)pos * kv, hid, kv, 0, stream)))
         break;
-      const bn_view kq = fview(qkv + hid, 1, kv, kv), vq = fview(qkv + hid + kv, 1, kv, kv);
-      const bn_view kc = fview(L.k_cache + (int64_t)pos * kv, 1, kv, kv);
-      const bn_view vc = fview(L.v_cache + (int64_t)pos * kv, 1, kv, kv);
-      if ((st = bn_copy(&kq, &kc, stream)) || (st = bn_copy(&vq, &vc, stream))) break;
       if ((st = bn_gqa_decode(BN_F32, qkv, L.k_cache, L.v_cache, lens + t, o, 1, c->max_len, c->n_heads,
                               c->n_kv_heads, hd, scale, dec_ws, pl.dec_bytes, stream)))
         break;
       if ((st = bn_linear_rope(&v_o, &wo, &v_attn, 0, 0, hd, c->rope_theta, lin_ws, pl.lin_bytes, stream)))
         break;
       if ((st = bn_add_rmsnorm(&v_hdn, &v_attn, &ln2, &v_hdn, &v_xn, c->rms_eps, stream))) break;
-      if ((st = bn_linear_rope(&v_xn, &wgu, &v_gu, 0, 0, hd, c->rope_theta, lin_ws, pl.lin_bytes, stream)))
+      // gate | up projection; its reduction writes silu(gate) * up
+      if ((st = linear_run(&v_xn, &wgu, &v_act, 0, 0, hd, c->rope_theta, lin_ws, pl.lin_bytes,
+                           kLinEpiSilu, nullptr, nullptr, 0, 0, 0, stream)))
         break;
-      if ((st = bn_silu_mul(&v_gate, &v_up, &v_act, stream))) break;
       if ((st = bn_linear_rope(&v_act, &wd, &v_mlp, 0, 0, hd, c->rope_theta, lin_ws, pl.lin_bytes, stream)))
         break;
       if ((st = bn_add_rmsnorm(&v_hdn, &v_mlp, &nxt, &v_hdn, &v_xn, c->rms_eps, stream))) break;

@@ -128,9 +128,11 @@ def test_tinyllama_cache_matches_recompute():
 @pytest.mark.parametrize("prompt,new", [(40, 12), (7, 1), (1, 30)])
 def test_native_decode_matches_generate(prompt, new):
     """bn_llama_decode runs the decode loop natively (gather, layers, lm_head,
-    argmax, next token fed on the device).  It launches the same kernels in
-    the same order as the Python step loop, so the generated tokens and every
-    layer's KV cache are bit-identical to generate()."""
+    argmax, next token fed on the device).  Its QKV reduction also appends K
+    and V to the caches and its gate|up reduction writes silu(gate) * up; the
+    slabs are summed in the order of the unfused reduction, so the generated
+    tokens and every layer's KV cache are bit-identical to generate(), which
+    runs the ops one by one."""
     ids = torch.from_numpy(np.random.default_rng(7 + prompt).integers(0, 512, prompt)).cuda()
     a, b = small_llama(), small_llama()
     ref, _ = a.generate(ids, new)
