@@ -210,7 +210,8 @@ __device__ __forceinline__ Work decode_work_packed(const PrefillParams &p) {
 // LDS: 2-deep K and V rings of 64-key blocks.  Block iteration j runs steps
 // 2j+1 and 2j+2, which read only V_j and K_{j+1}; it stores K_{j+2} and
 // V_{j+1} (register-staged one iteration earlier) into the buffers of K_j and
-// V_{j-1}, last read in iteration j-1: one barrier per block orders them.
+// V_{j-1}, last read in iteration j-1 (K_0: in step 0): one barrier per block
+// orders them.
 constexpr float kSumLimit = 65536.f;
 constexpr int kOcc = 2;  // workgroups per CU the register budget is sized for
 // step interleave: VALU instructions ahead of the first MFMA, then after each
@@ -485,6 +486,9 @@ __global__ __launch_bounds__(256, OCC) void prefill_bf16_kernel(PrefillParams p)
       l[rt] += rs;
     }
   }
+  // iteration 0 stores K_2 into K_0's buffer, which step 0 reads: every wave
+  // must be past those reads first
+  __syncthreads();
   // iteration j: steps 2j+1 (P of tile 2j, scores of 2j+2, softmax of 2j+1)
   // and 2j+2 (P of 2j+1, scores of 2j+3, softmax of 2j+2).  The leading
   // iterations whose tiles every wave sees whole (no causal or tail mask)
