@@ -164,6 +164,10 @@ __global__ __launch_bounds__(64 * WV) void decode_split_kernel(DecodeParams p) {
       DecVec<T>::load(Kb + (int64_t)key * kv_rs, kk[t]);
       DecVec<T>::load(Vb + (int64_t)key * kv_rs, vv[t]);
     }
+    // single pass: every load of the round is issued before any is consumed.
+    // Left alone, the scheduler trades them for registers (load, wait, use,
+    // next: ten round trips); 116 VGPRs still fit 16 waves per workgroup.
+    if constexpr (SINGLE) __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
       const int key = base + t * KPI + grp;
