@@ -121,6 +121,23 @@ __global__ __launch_bounds__(256) void rmsnorm_rows_kernel(
   const float pos = (float)(row + pos_off);
   int cached_p0 = -1;
   float cs[VEC / 2], sn[VEC / 2];
+  // A row has head_dim/2 distinct angles.  When every chunk of a lane starts
+  // at the same offset within its head (64*VEC a multiple of head_dim), lane
+  // l evaluates angle l % (head_dim/2) once and each lane collects its VEC/2
+  // angles from the lanes that hold them: one sincosf per lane instead of
+  // VEC/2, the same values.
+  if (ROPE && head_dim <= 128 && (64 * VEC) % head_dim == 0) {
+    const int half = head_dim >> 1;
+    float s1, c1;
+    sincosf(pos * freqs.f[lane % half], &s1, &c1);  // op_rope.cuh:83
+    const int p0 = ((lane * VEC) % head_dim) >> 1;
+#pragma unroll
+    for (int j = 0; j < VEC / 2; ++j) {
+      sn[j] = __shfl(s1, p0 + j, 64);
+      cs[j] = __shfl(c1, p0 + j, 64);
+    }
+    cached_p0 = p0;
+  }
 #pragma unroll
   for (int i = 0; i < NCH; ++i) {
     int c = lane + 64 * i;

@@ -152,11 +152,16 @@ def test_rope_transposed_view():
     assert_close(host(yd), O.rope(np.ascontiguousarray(x.T), 3, 64, 1e4), FP32_TOL)
 
 
-@pytest.mark.parametrize("rows,w,off,dtype", [(32, 2048, 0, "f32"), (9, 2048, 77, "f32"),
-                                              (64, 2048, 1000, "bf16"), (5, 512, 3, "bf16"),
-                                              (3, 320, 0, "f32"), (8194, 512, 5, "bf16"),
-                                              (8198, 2048, 0, "f32")])
-def test_rmsnorm_rope(rows, w, off, dtype):
+@pytest.mark.parametrize("rows,w,off,dtype,hd", [(32, 2048, 0, "f32", 64), (9, 2048, 77, "f32", 64),
+                                                 (64, 2048, 1000, "bf16", 64), (5, 512, 3, "bf16", 64),
+                                                 (3, 320, 0, "f32", 64), (8194, 512, 5, "bf16", 64),
+                                                 (8198, 2048, 0, "f32", 64),
+                                                 # one angle per lane, shared (head_dim 32 / 128) and
+                                                 # the per-chunk path (48: chunks start at varying
+                                                 # offsets within their heads)
+                                                 (7, 2048, 9, "bf16", 128), (7, 1024, 9, "f32", 32),
+                                                 (5, 960, 3, "bf16", 48), (5, 960, 3, "f32", 48)])
+def test_rmsnorm_rope(rows, w, off, dtype, hd):
     r = rng(5)
     x = r.standard_normal((rows, w)).astype(np.float32)
     wt = (1 + 0.1 * r.standard_normal((1, w))).astype(np.float32)
@@ -165,8 +170,8 @@ def test_rmsnorm_rope(rows, w, off, dtype):
         x, wt = bf16_round(x), bf16_round(wt)
     xd, wd = dev(x, td), dev(wt, td)
     yd = torch.empty_like(xd)
-    B.call("bn_rmsnorm_rope", V(xd), V(wd), V(yd), 1e-5, off, 64, 1e4, S0)
-    assert_close(host(yd), O.rmsnorm_rope(x, wt, 1e-5, off, 64, 1e4),
+    B.call("bn_rmsnorm_rope", V(xd), V(wd), V(yd), 1e-5, off, hd, 1e4, S0)
+    assert_close(host(yd), O.rmsnorm_rope(x, wt, 1e-5, off, hd, 1e4),
                  BF16_TOL if dtype == "bf16" else FP32_TOL, "rmsnorm_rope")
 
 
