@@ -248,7 +248,7 @@ __global__ __launch_bounds__(256) void linear_reduce_kernel(LinParams p, RopeFre
     b = add4(add4(add4(b, red[1][0][lane]), red[1][1][lane]), red[1][2][lane]);
     const float u[4] = {b.x, b.y, b.z, b.w};
 #pragma unroll
-    for (int j = 0; j < 4; ++j) v[j] = v[j] / (1.0f + expf(-v[j])) * u[j];  // as silu_mul_rows_kernel
+    for (int j = 0; j < 4; ++j) v[j] = swiglu_silu(v[j]) * u[j];  // as silu_mul_rows_kernel
   } else {
     rope4(v, gm, gn, p, fr);
     if (p.k_dst) {  // K | V columns appended to the caches (fp32)

@@ -254,7 +254,7 @@ __global__ __launch_bounds__(256) void silu_mul_rows_kernel(const T *__restrict_
     Chunk<T>::cvt(graw[k], gv);
     Chunk<T>::cvt(uraw[k], uv);
 #pragma unroll
-    for (int j = 0; j < VEC; ++j) ov[j] = gv[j] / (1.0f + expf(-gv[j])) * uv[j];
+    for (int j = 0; j < VEC; ++j) ov[j] = swiglu_silu(gv[j]) * uv[j];
     Chunk<T>::store(o + ooff[k], ov);
   }
 }
@@ -267,7 +267,7 @@ __global__ __launch_bounds__(256) void silu_mul_strided_kernel(DView<const T> g,
        idx += (int64_t)gridDim.x * 256) {
     const int r = (int)(idx / o.w), c = (int)(idx - (int64_t)r * o.w);
     const float gv = Elem<T>::load(&g.at(r, c));
-    Elem<T>::store(&o.at(r, c), gv / (1.0f + expf(-gv)) * Elem<T>::load(&u.at(r, c)));
+    Elem<T>::store(&o.at(r, c), swiglu_silu(gv) * Elem<T>::load(&u.at(r, c)));
   }
 }
 
