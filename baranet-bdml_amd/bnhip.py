@@ -40,7 +40,7 @@ class BnPoolStats(C.Structure):
 class BnLlamaConfig(C.Structure):
     _fields_ = [(n, C.c_int) for n in ("n_layers", "hidden", "n_heads", "n_kv_heads",
                                        "intermediate", "vocab", "max_len")] + \
-               [("rms_eps", C.c_float), ("rope_theta", C.c_float)]
+               [("rms_eps", C.c_float), ("rope_theta", C.c_float), ("weights_out_major", C.c_int)]
 
 
 class BnLlamaLayer(C.Structure):

@@ -347,6 +347,189 @@ __global__ __launch_bounds__(256) void linear_small_kernel(LinParams p) {
   }
 }
 
+// Few rows against an output-major weight: w viewed [k, n] with stride_h 1,
+// so the k weights of each output are contiguous (a row of the [n, k]
+// matrix the view transposes).  Every output then streams as one contiguous
+// row and needs no k split, no partials and no second launch.  A wave owns
+// two outputs -- a rotation pair (2p, 2p+1), or for EPI_SILU the gate column
+// j and the up column j + n/2 -- and reads their weight rows 16 bytes per
+// lane through buffer descriptors whose range ends at k (loads past it
+// return zeros and move no data), GV_ROUND loads per row and lane per round.
+// The first round is requested before x is staged (the two round trips
+// overlap).  Each lane sums its k positions in increasing order, a
+// wave sum gives the dot product, and the wave applies the epilogue (the
+// rotation and the K/V cache append, or silu(gate) * up) and stores.  x is
+// staged in LDS once per workgroup as fp32.
+constexpr int GV_M = 4;        // rows of x, at most
+constexpr int GV_ROUND = 8;    // 16-byte loads per weight row and lane in a round
+constexpr int GV_XMAX = 16384; // fp32 elements of x in LDS (64 KB)
+
+template <typename T, int MR, int EPI>
+__global__ __launch_bounds__(256) void linear_gemv_t_kernel(LinParams p, RopeFreqs fr) {
+  extern __shared__ __attribute__((aligned(16))) float gxs[];  // [MR][kp], zeros past k
+  constexpr int VE = 16 / (int)sizeof(T);  // k per 16-byte load
+  constexpr int SPAN = 64 * VE;            // k per wave-wide load
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int kp = (p.k + SPAN - 1) / SPAN * SPAN;
+  const int nl = kp / SPAN;  // wave-wide loads per weight row
+
+  // this wave's outputs and weight rows (clamped: a wave past the last
+  // output loads a valid row and exits after the staging barrier)
+  const int width = EPI == EPI_SILU ? p.n / 2 : p.n;  // output columns
+  const int j0 = EPI == EPI_SILU ? blockIdx.x * 4 + wave : (blockIdx.x * 4 + wave) * 2;
+  const bool active = j0 < width;  // wave-uniform
+  const int jc = active ? j0 : 0;
+  const int r0 = jc, r1 = EPI == EPI_SILU ? jc + width : jc + 1;
+  // w_rs: elements between consecutive outputs' rows
+  auto rsrc = [&](int row) __attribute__((always_inline)) {
+    const uint64_t a = (uint64_t)((const T *)p.w + (int64_t)row * p.w_rs);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
+    return __builtin_amdgcn_make_buffer_rsrc((void *)(((uint64_t)hi << 32) | lo), (short)0,
+                                             p.k * (int)sizeof(T), 0x00020000);
+  };
+  const __amdgpu_buffer_rsrc_t ra = rsrc(r0), rb = rsrc(r1);
+  auto issue = [&](u32x4_t (&a)[GV_ROUND], u32x4_t (&b)[GV_ROUND], int l0) __attribute__((always_inline)) {
+#pragma unroll
+    for (int u = 0; u < GV_ROUND; ++u) {
+      const int off = ((l0 + u) * SPAN + lane * VE) * (int)sizeof(T);  // past k: zeros
+      // each weight byte is read once per call: non-temporal
+      a[u] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(ra, off, 0, 2));
+      b[u] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rb, off, 0, 2));
+    }
+  };
+  float acc[2][MR];
+#pragma unroll
+  for (int r = 0; r < MR; ++r) acc[0][r] = acc[1][r] = 0.f;
+  auto consume = [&](const u32x4_t (&a)[GV_ROUND], const u32x4_t (&b)[GV_ROUND], int l0)
+      __attribute__((always_inline)) {
+#pragma unroll
+    for (int u = 0; u < GV_ROUND; ++u) {
+      // slots past the padded row carry zero weights; their x reads stay in range
+      const int xo = min((l0 + u) * SPAN, kp - SPAN) + lane * VE;
+      float wa[VE], wb[VE];
+      if constexpr (sizeof(T) == 4) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) { wa[e] = __uint_as_float(a[u][e]); wb[e] = __uint_as_float(b[u][e]); }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          wa[2 * e] = __uint_as_float(a[u][e] << 16);
+          wa[2 * e + 1] = __uint_as_float(a[u][e] & 0xffff0000u);
+          wb[2 * e] = __uint_as_float(b[u][e] << 16);
+          wb[2 * e + 1] = __uint_as_float(b[u][e] & 0xffff0000u);
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < MR; ++r) {
+        const float *xr = gxs + r * kp + xo;
+#pragma unroll
+        for (int e = 0; e < VE; e += 4) {
+          const float4 x4 = *(const float4 *)(xr + e);
+          acc[0][r] = fmaf(wa[e], x4.x, acc[0][r]);
+          acc[0][r] = fmaf(wa[e + 1], x4.y, acc[0][r]);
+          acc[0][r] = fmaf(wa[e + 2], x4.z, acc[0][r]);
+          acc[0][r] = fmaf(wa[e + 3], x4.w, acc[0][r]);
+          acc[1][r] = fmaf(wb[e], x4.x, acc[1][r]);
+          acc[1][r] = fmaf(wb[e + 1], x4.y, acc[1][r]);
+          acc[1][r] = fmaf(wb[e + 2], x4.z, acc[1][r]);
+          acc[1][r] = fmaf(wb[e + 3], x4.w, acc[1][r]);
+        }
+      }
+    }
+  };
+
+  u32x4_t a0[GV_ROUND], b0[GV_ROUND];
+  issue(a0, b0, 0);
+  {
+    // x rows in 16-byte chunks: thread tid takes chunks tid + 256u of every
+    // row, XB per row requested before any is stored (clamped addresses,
+    // zeros selected afterwards: no branch around a load).  One pass covers
+    // 256*XB chunks per row; longer rows loop.
+    constexpr int XB = 8 / MR;
+    const T *X = (const T *)p.x;
+    const int cpr = kp / VE;  // chunks per row
+    auto stage = [&](int cb) __attribute__((always_inline)) {
+      u32x4_t v[MR][XB];
+#pragma unroll
+      for (int r = 0; r < MR; ++r)
+#pragma unroll
+        for (int u = 0; u < XB; ++u) {
+          const int kk = min((cb + u * 256 + tid) * VE, p.k - VE);
+          v[r][u] = *(const u32x4_t *)(X + min(r, p.m - 1) * p.x_rs + kk);
+        }
+#pragma unroll
+      for (int r = 0; r < MR; ++r)
+#pragma unroll
+        for (int u = 0; u < XB; ++u) {
+          const int c = cb + u * 256 + tid, kk = c * VE;
+          if (c < cpr) {
+            const bool ok = r < p.m && kk < p.k;
+            float *d = gxs + r * kp + kk;
+            if constexpr (sizeof(T) == 4) {
+              *(float4 *)d = ok ? make_float4(__uint_as_float(v[r][u][0]), __uint_as_float(v[r][u][1]),
+                                              __uint_as_float(v[r][u][2]), __uint_as_float(v[r][u][3]))
+                                : make_float4(0.f, 0.f, 0.f, 0.f);
+            } else {
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                d[2 * e] = ok ? __uint_as_float(v[r][u][e] << 16) : 0.f;
+                d[2 * e + 1] = ok ? __uint_as_float(v[r][u][e] & 0xffff0000u) : 0.f;
+              }
+            }
+          }
+        }
+    };
+    stage(0);
+    for (int cb = 256 * XB; cb < cpr; cb += 256 * XB) stage(cb);
+  }
+  __syncthreads();
+  if (!active) return;  // a whole wave; no barrier follows
+  // longer rows: one round after the other (keeping the next round in flight
+  // while one is consumed measured slower on config 4's down projection)
+  for (int l0 = 0; l0 < nl; l0 += GV_ROUND) {
+    if (l0 > 0) issue(a0, b0, l0);
+    __builtin_amdgcn_sched_barrier(0);
+    consume(a0, b0, l0);
+  }
+#pragma unroll
+  for (int r = 0; r < MR; ++r) {
+    acc[0][r] = wave_sum(acc[0][r]);
+    acc[1][r] = wave_sum(acc[1][r]);
+  }
+  // lane r stores row r's outputs
+  float v0 = acc[0][0], v1 = acc[1][0];
+#pragma unroll
+  for (int r = 1; r < MR; ++r)
+    if (lane == r) { v0 = acc[0][r]; v1 = acc[1][r]; }
+  if (lane >= p.m) return;
+  const int gm = lane;
+  T *yrow = (T *)p.y + gm * p.y_rs;
+  if constexpr (EPI == EPI_SILU) {
+    Elem<T>::store(yrow + j0, swiglu_silu(v0) * v1);  // as silu_mul_rows_kernel
+  } else {
+    if (j0 < p.rope_cols) {  // op_rope.cuh:79-98: fp32 angle position*freq
+      const float ang = (float)(p.pos0 + gm) * fr.f[(j0 % p.head_dim) >> 1];
+      float sn, cs;
+      sincosf(ang, &sn, &cs);
+      const float x0 = v0, x1 = v1;
+      v0 = x0 * cs - x1 * sn;
+      v1 = x0 * sn + x1 * cs;
+    }
+    if (p.k_dst) {  // K | V columns appended to the caches (fp32)
+      const int c = j0 - p.app_col;
+      if (c >= 0 && c < 2 * p.app_w) {
+        float *dst = (c < p.app_w ? p.k_dst + c : p.v_dst + (c - p.app_w)) + gm * p.app_rs;
+        dst[0] = v0;
+        dst[1] = v1;
+      }
+    }
+    Elem<T>::store(yrow + j0, v0);
+    Elem<T>::store(yrow + j0 + 1, v1);
+  }
+}
+
 // slabs of the few-rows path: about kSmallWg workgroups, slabs of
 // 32..SK_MAX rows in multiples of 32
 constexpr int kSmallWg = 512;
@@ -401,9 +584,77 @@ extern "C" size_t bn_linear_rope_workspace_size(int dtype, int m, int n, int k) 
 
 namespace bn {
 
+namespace {
+// output-major w (linear_gemv_t_kernel): shapes and the rotation table are
+// checked by linear_run; this checks the layout the kernel reads
+int gemv_t_run(const bn_view *x, const bn_view *w, const bn_view *y, int rope_cols,
+               int position_offset, int head_dim, const RopeFreqs &fr, int epi, float *k_dst,
+               float *v_dst, int app_col, int app_w, int64_t app_rs, const char *op, void *stream) {
+  const int dt = x->dtype;
+  const int64_t ve = dt == BN_BF16 ? 8 : 4;  // elements per 16 bytes
+  const size_t es = dtype_size(dt);
+  const int m = x->h, n = w->w, k = x->w;
+  const int64_t kp = (k + 64 * ve - 1) / (64 * ve) * (64 * ve);
+  auto base_ok = [&](const bn_view *v) {
+    return ((reinterpret_cast<uintptr_t>(v->data) + (uintptr_t)(v->offset * (int64_t)es)) & 15u) == 0;
+  };
+  auto rows_ok = [&](const bn_view *v) {
+    return (int64_t)v->h * v->w == 0 || (v->stride_w == 1 && v->stride_h % ve == 0 && base_ok(v));
+  };
+  if (!rows_ok(x) || !rows_ok(y) || !base_ok(w) || w->stride_w % ve || k % ve || y->w % 2)
+    return fail(BN_ERR_UNSUPPORTED,
+                std::string(op) + ": an output-major w needs 16-byte aligned rows of x, y and w, k a "
+                                  "multiple of 16 bytes and an even output width");
+  if (m > GV_M || (int64_t)m * kp > GV_XMAX)
+    return fail(BN_ERR_UNSUPPORTED, std::string(op) + ": an output-major w takes at most " +
+                                        std::to_string(GV_M) + " rows of x and " +
+                                        std::to_string(GV_XMAX) + " staged x elements");
+  if (k_dst && (dt != BN_F32 || app_col < 0 || app_col % 4 || app_w % 4 || app_col + 2 * app_w > n))
+    return fail(BN_ERR_UNSUPPORTED, std::string(op) + ": bad K/V append columns");
+  int st;
+  if ((st = require_device(op, {x, w, y}))) return st;
+  if (y->h == 0 || y->w == 0) return BN_OK;
+  if ((st = ensure_device())) return st;
+  LinParams p = {};
+  p.x = (const char *)x->data + x->offset * (int64_t)es;
+  p.w = (const char *)w->data + w->offset * (int64_t)es;
+  p.y = (char *)y->data + y->offset * (int64_t)es;
+  p.x_rs = x->stride_h; p.w_rs = w->stride_w; p.y_rs = y->stride_h;
+  p.m = m; p.n = n; p.k = k;
+  p.rope_cols = rope_cols; p.head_dim = rope_cols ? head_dim : 2; p.pos0 = position_offset;
+  p.k_dst = k_dst; p.v_dst = v_dst; p.app_col = app_col; p.app_w = app_w; p.app_rs = app_rs;
+  const int mr = m <= 1 ? 1 : (m <= 2 ? 2 : 4);
+  const size_t lds = (size_t)mr * kp * sizeof(float);
+  // four waves per workgroup, two weight rows (one output pair, or one
+  // gate | up output) per wave
+  const int waves = n / 2;
+  const dim3 grid((unsigned)((waves + 3) / 4)), block(256);
+  hipStream_t s = as_stream(stream);
+#define BN_GV(T, MR, E) hipLaunchKernelGGL((linear_gemv_t_kernel<T, MR, E>), grid, block, lds, s, p, fr)
+#define BN_GV_M(T, E)                 \
+  do {                                \
+    if (mr == 1) BN_GV(T, 1, E);      \
+    else if (mr == 2) BN_GV(T, 2, E); \
+    else BN_GV(T, 4, E);              \
+  } while (0)
+  if (dt == BN_F32) {
+    if (epi == EPI_SILU) BN_GV_M(float, EPI_SILU);
+    else BN_GV_M(float, EPI_PLAIN);
+  } else {
+    if (epi == EPI_SILU) BN_GV_M(bf16_t, EPI_SILU);
+    else BN_GV_M(bf16_t, EPI_PLAIN);
+  }
+#undef BN_GV_M
+#undef BN_GV
+  BN_LAUNCH_CHECK();
+  return BN_OK;
+}
+}  // namespace
+
 // bn_linear_rope with a reduction epilogue (EPI_SILU: y is [m, n/2]) and
-// optional K/V appends (LinParams::k_dst); the epilogues exist only on the
-// split-k paths, which the few-rows projections always take.
+// optional K/V appends (LinParams::k_dst); the epilogues exist on the
+// split-k paths, which the few-rows projections always take, and on the
+// output-major few-rows kernel.
 int linear_run(const bn_view *x, const bn_view *w, const bn_view *y, int rope_cols,
                int position_offset, int head_dim, float theta, void *workspace,
                size_t workspace_bytes, int epi, float *k_dst, float *v_dst, int app_col, int app_w,
@@ -439,6 +690,11 @@ int linear_run(const bn_view *x, const bn_view *w, const bn_view *y, int rope_co
            ((reinterpret_cast<uintptr_t>(v->data) + (uintptr_t)(v->offset * (int64_t)es)) & 15u) == 0;
   };
   auto unit = [](const bn_view *v) { return (int64_t)v->h * v->w == 0 || v->stride_w == 1; };
+  // an output-major w (stride_h == 1: each output's k weights contiguous) takes
+  // the few-rows streaming kernel without a k split
+  if ((int64_t)w->h * w->w > 0 && w->stride_h == 1 && w->stride_w != 1)
+    return gemv_t_run(x, w, y, rope_cols, position_offset, head_dim, fr, epi, k_dst, v_dst, app_col,
+                      app_w, app_rs, op, stream);
   if (!unit(x) || !unit(w) || !unit(y))
     return fail(BN_ERR_UNSUPPORTED, std::string(op) + ": rows must be contiguous (stride_w == 1)");
   if (!ok(x) || !ok(w) || !ok(y) || x->w % ve || y->w % ve)

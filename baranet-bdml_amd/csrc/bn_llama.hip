@@ -6,10 +6,11 @@
 // (llama_model.py:135-141, llama_model.hpp:161-198); its decoder layer is
 // llama_layers.hpp:241-272.  Every step is the path's own kernels:
 // bn_linear_rope's projections (the QKV rotation and the K/V cache append in
-// its split-k reduction; the SwiGLU product in the gate|up reduction),
+// their epilogue; the SwiGLU product in the gate|up projection's),
 // bn_gqa_decode, bn_add_rmsnorm, bn_rmsnorm and bn_argmax.  The fused
-// reductions sum the slabs in the same order as the unfused ones, so the
-// tokens and caches are those of the op-by-op step loop.
+// epilogues see the sums the unfused projection writes (the split-k slabs in
+// one order; with output-major weights each output's own dot product), so
+// the tokens and caches are those of the op-by-op step loop.
 #include <algorithm>
 
 #include "bn_common.hpp"
@@ -56,6 +57,17 @@ bn_view fview(const void *p, int h, int w, int stride_h) {
   v.stride_w = 1;
   v.dtype = BN_F32;
   v.on_device = 1;
+  return v;
+}
+
+// the [in, out] view of a projection weight: row-major, or the transposed
+// view of an output-major [out, in] matrix
+bn_view wview(const void *p, int in, int out, bool out_major) {
+  bn_view v = fview(p, in, out, out);
+  if (out_major) {
+    v.stride_h = 1;
+    v.stride_w = in;
+  }
   return v;
 }
 
@@ -166,7 +178,8 @@ extern "C" int bn_llama_decode(const bn_llama_config *c, const float *embed, con
   const bn_view v_o = fview(o, 1, hid, hid), v_attn = fview(attn, 1, hid, hid);
   const bn_view v_act = fview(act, 1, I, I), v_mlp = fview(mlp, 1, hid, hid);
   const bn_view v_logits = fview(logits, 1, c->vocab, c->vocab);
-  const bn_view v_lnf = fview(ln_f, 1, hid, hid), v_lm = fview(lm_head, hid, c->vocab, c->vocab);
+  const bool om = c->weights_out_major != 0;
+  const bn_view v_lnf = fview(ln_f, 1, hid, hid), v_lm = wview(lm_head, hid, c->vocab, om);
 
   hipLaunchKernelGGL(fill_lens_kernel, dim3((unsigned)((n_tokens + 255) / 256)), dim3(256), 0, s, lens,
                      position, n_tokens);
@@ -185,9 +198,9 @@ extern "C" int bn_llama_decode(const bn_llama_config *c, const float *embed, con
     if ((st = bn_rmsnorm(&v_hdn, &ln10, &v_xn, c->rms_eps, stream))) break;
     for (int l = 0; l < c->n_layers && st == BN_OK; ++l) {
       const bn_llama_layer_weights &L = layers[l];
-      const bn_view wqkv = fview(L.wqkv, hid, hid + 2 * kv, hid + 2 * kv);
-      const bn_view wo = fview(L.wo, hid, hid, hid), wgu = fview(L.wgu, hid, 2 * I, 2 * I);
-      const bn_view wd = fview(L.wd, I, hid, hid), ln2 = fview(L.ln2, 1, hid, hid);
+      const bn_view wqkv = wview(L.wqkv, hid, hid + 2 * kv, om);
+      const bn_view wo = wview(L.wo, hid, hid, om), wgu = wview(L.wgu, hid, 2 * I, om);
+      const bn_view wd = wview(L.wd, I, hid, om), ln2 = fview(L.ln2, 1, hid, hid);
       const bn_view nxt = l + 1 < c->n_layers ? fview(layers[l + 1].ln1, 1, hid, hid) : v_lnf;
       // Q, K and V (Q and K rotated at position pos); the reduction also
       // appends K and V to the caches at row pos

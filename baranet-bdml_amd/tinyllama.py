@@ -17,11 +17,14 @@ RMSNorm (plain and fused with the residual add), RoPE, prefill attention,
 decode attention and the SwiGLU activation run on the HIP kernels through the
 C ABI (bnhip).  The Q, K and V projections are one GEMM against the
 concatenated weight [hidden, (H + 2*Hkv)*64]; attention reads Q, K and V as
-column slices of its output.  Decode steps (rows <= SMALL_ROWS) run every
-projection -- QKV, O, the concatenated gate/up, down and lm_head -- on
-bn_linear_rope's few-rows kernel, with the Q/K rotation fused into the QKV
-projection; the prompt runs the library GEMM (torch) and rotates the Q and K
-columns in place in one bn_rope launch.  The embedding gather is a torch GPU
+column slices of its output.  Projection weights are stored output-major
+([out, in] row-major, so each output's weights are contiguous); the model
+holds them as the transposed [in, out] views, so x @ W reads as in the
+reference.  Decode steps (rows <= SMALL_ROWS) run every projection -- QKV, O,
+the concatenated gate/up, down and lm_head -- on bn_linear_rope's
+output-major few-rows kernel (one pass over each weight, no k split), with
+the Q/K rotation fused into the QKV projection; the prompt runs the library
+GEMM (torch) and rotates the Q and K columns in place in one bn_rope launch.  The embedding gather is a torch GPU
 operation.  The config's metric times the attention, RoPE (standalone or
 fused into the decode QKV projection) and RMSNorm kernels.  ``path_ms`` accumulates hip-event time around those
 kernel launches (an upper bound on their device time; the rocprofv3 kernel
@@ -55,12 +58,12 @@ class TinyLlamaConfig:
 
 
 class TinyLlama:
-    # Rows up to which the projections run on bn_linear_rope's few-rows kernel
-    # (one pass over the weights, the QKV rotation fused into its reduction).
-    # Longer prompts take the library GEMM and a separate RoPE launch: at 512
-    # rows hipBLASLt's fp32 GEMM plus bn_rope (45 + 4 us) beats the hand-written
-    # tiled kernel (66 us).
-    SMALL_ROWS = 8
+    # Rows up to which the projections run on bn_linear_rope's output-major
+    # few-rows kernel (one pass over the weights, the QKV rotation in its
+    # epilogue; it takes up to 4 rows).  Longer prompts take the library GEMM
+    # and a separate RoPE launch: at 512 rows hipBLASLt's fp32 GEMM plus
+    # bn_rope (45 + 4 us) beats the hand-written tiled kernel (66 us).
+    SMALL_ROWS = 4
 
     def __init__(self, cfg: TinyLlamaConfig, max_len: int, seed: int = 1, std: float = 0.02,
                  dtype=torch.float32):
@@ -74,6 +77,10 @@ class TinyLlama:
         def w(*shape):
             return torch.randn(shape, generator=g, device="cuda") * std
 
+        def out_major(m):
+            # [in, out] values stored [out, in]; the model keeps the [in, out] view
+            return m.t().contiguous().t()
+
         self.embed = w(cfg.vocab_size, h)
         self.layers = []
         for _ in range(cfg.num_hidden_layers):
@@ -81,19 +88,16 @@ class TinyLlama:
             wo = w(h, h)
             wg, wu = w(h, inter), w(h, inter)
             self.layers.append(dict(
-                ln1=torch.ones((1, h), device="cuda"), wqkv=torch.cat([wq, wk, wv], dim=1),
-                wo=wo, ln2=torch.ones((1, h), device="cuda"), wgu=torch.cat([wg, wu], dim=1),
-                wd=w(inter, h),
+                ln1=torch.ones((1, h), device="cuda"),
+                wqkv=out_major(torch.cat([wq, wk, wv], dim=1)), wo=out_major(wo),
+                ln2=torch.ones((1, h), device="cuda"), wgu=out_major(torch.cat([wg, wu], dim=1)),
+                wd=out_major(w(inter, h)),
                 k_cache=torch.zeros((1, max_len, cfg.num_key_value_heads, cfg.head_dim), device="cuda"),
                 v_cache=torch.zeros((1, max_len, cfg.num_key_value_heads, cfg.head_dim), device="cuda")))
         self.ln_f = torch.ones((1, h), device="cuda")
-        self.lm_head = w(h, cfg.vocab_size)
+        self.lm_head = out_major(w(h, cfg.vocab_size))
         self.length = 0
         self.ws = bnhip.decode_workspace(1, max_len, cfg.num_attention_heads, cfg.head_dim)
-        # few-rows projections (decode steps): split-k partial sums of the largest one
-        shapes = [(h, h + 2 * kv), (h, h), (h, 2 * inter), (inter, h), (h, cfg.vocab_size)]
-        n_ws = max(bnhip.lib().bn_linear_rope_workspace_size(0, self.SMALL_ROWS, n, k) for k, n in shapes)
-        self.lin_ws = torch.empty(max(n_ws // 4, 1), device="cuda")
         self.path_ms = 0.0
         self.timing = False
         self.trace = None  # list of (kernel, inputs, output, kw) when set
@@ -179,8 +183,7 @@ class TinyLlama:
 
         def run():
             bnhip.linear_rope(x, w, y, rope_cols=rope_cols, position_offset=pos0,
-                              head_dim=self.cfg.head_dim, theta=self.cfg.rope_theta,
-                              workspace=self.lin_ws)
+                              head_dim=self.cfg.head_dim, theta=self.cfg.rope_theta)
         if rope_cols:
             self._timed(run, "qkv_rope")  # carries the RoPE of the step
             self._record("linear_rope", [x, w], y, rope_cols=rope_cols, offset=pos0,
@@ -287,7 +290,7 @@ class TinyLlama:
         cfg = self.cfg
         return bnhip.BnLlamaConfig(cfg.num_hidden_layers, cfg.hidden_size, cfg.num_attention_heads,
                                    cfg.num_key_value_heads, cfg.intermediate_size, cfg.vocab_size,
-                                   self.max_len, cfg.rms_norm_eps, cfg.rope_theta)
+                                   self.max_len, cfg.rms_norm_eps, cfg.rope_theta, 1)
 
     def generate_native(self, ids: torch.Tensor, new_tokens: int):
         """Greedy decode with the decode loop in native code: the prompt runs

@@ -149,7 +149,12 @@ int bn_matmul(const bn_view *a, const bn_view *b, const bn_view *c, void *stream
  * op_mm for the output projection (:112, rope_cols = 0).  fp32 accumulation;
  * y must not overlap x or w.  Split-k partial sums take
  * bn_linear_rope_workspace_size(dtype, M, N, K) bytes of workspace (16-byte
- * aligned; NULL: the pool supplies them). */
+ * aligned; NULL: the pool supplies them).  w may also be output-major -- the
+ * transposed view of an [N, K] matrix (stride_h 1, stride_w a multiple of 16
+ * bytes, the view's element (0, 0) 16-byte aligned): for M <= 4 and
+ * M*ceil(K / (64*elements per 16 bytes))*64*elements per 16 bytes <= 16384
+ * this streams each output's contiguous weights once with no k split (no
+ * workspace; N even); other M are BN_ERR_UNSUPPORTED for that layout. */
 size_t bn_linear_rope_workspace_size(int dtype, int m, int n, int k);
 int bn_linear_rope(const bn_view *x, const bn_view *w, const bn_view *y,
                    int rope_cols, int position_offset, int head_dim, float theta,
@@ -290,11 +295,15 @@ int bn_gqa_prefill_backward(int dtype, const void *q, const void *k,
  * deterministic limit (top_k = 1, argmax) and runs all n steps.  Weight layouts are x @ W: wqkv [hidden, (H + 2*Hkv)*64]
  * (Q | K | V), wo [hidden, hidden], wgu [hidden, 2*intermediate] (gate | up),
  * wd [intermediate, hidden], embed [vocab, hidden], lm_head [hidden, vocab];
- * norm weights [hidden].  workspace (256-byte aligned,
+ * norm weights [hidden].  With weights_out_major set, wqkv, wo, wgu, wd and
+ * lm_head are stored transposed ([out, in] row-major: each output's weights
+ * contiguous), and every projection streams them without a k split (see
+ * bn_linear_rope).  workspace (256-byte aligned,
  * bn_llama_decode_workspace_size bytes) may be NULL: the pool supplies it. */
 typedef struct bn_llama_config {
   int n_layers, hidden, n_heads, n_kv_heads, intermediate, vocab, max_len;
   float rms_eps, rope_theta;
+  int weights_out_major;  /* 0: [in, out] row-major (x @ W); 1: [out, in] row-major */
 } bn_llama_config;
 typedef struct bn_llama_layer_weights {
   const float *ln1, *wqkv, *wo, *ln2, *wgu, *wd;

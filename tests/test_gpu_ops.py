@@ -371,6 +371,56 @@ def test_linear_rope_strided_views_and_workspace(dtype):
     assert torch.equal(y2, y)
 
 
+@pytest.mark.parametrize("case", [(1, 2048, 2560, 2304, 511), (1, 5632, 2048, 0, 0), (2, 2048, 512, 256, 7),
+                                  (3, 520, 320, 192, 40), (4, 1024, 256, 0, 0), (1, 68, 64, 64, 16383),
+                                  (1, 8200, 128, 64, 3)])
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_linear_rope_output_major_weight(case, dtype):
+    """w given as the transposed view of an [N, K] matrix (each output's
+    weights contiguous): the few-rows kernel without a k split.  Config 4's
+    decode shapes, k not a multiple of a wave-wide load, 1-4 rows, positions
+    up to 16383; against the oracle and, bit for bit where the sums are the
+    same, across the row-major path's rows."""
+    M, K, N, rc, off = case
+    if dtype == "bf16" and K % 8:
+        pytest.skip("bf16 rows of 16 bytes need K % 8 == 0")
+    r = rng(62)
+    x = r.standard_normal((M, K)).astype(np.float32)
+    wt = (r.standard_normal((N, K)) / np.sqrt(K)).astype(np.float32)  # [N, K] storage
+    if dtype == "bf16":
+        x, wt = bf16_round(x), bf16_round(wt)
+    td = torch.float32 if dtype == "f32" else torch.bfloat16
+    wd = dev(wt, td)
+    y = B.linear_rope(dev(x, td), wd.t(), rope_cols=rc, position_offset=off)
+    ref = O.linear_rope(x, np.ascontiguousarray(wt.T), rc, off, 64, 1e4)
+    assert_close(host(y), ref, FP32_TOL if dtype == "f32" else BF16_TOL, f"out-major {case} {dtype}")
+    # each output depends only on its own row of w and x: one row of x alone
+    # gives the same bits as that row inside the batch
+    if M > 1:
+        y1 = B.linear_rope(dev(x[1:2], td), wd.t(), rope_cols=rc, position_offset=off + 1)
+        assert torch.equal(y1[0], y[1])
+
+
+def test_linear_rope_output_major_strided_and_limits():
+    # w the transposed view of the first 320 rows and 256 columns of a wider
+    # [400, 264] buffer (stride between outputs 264), y a column slice
+    r = rng(63)
+    xb = r.standard_normal((2, 256)).astype(np.float32)
+    wb = (r.standard_normal((400, 264)) / 16).astype(np.float32)
+    w = dev(wb)[:320, :256].t()
+    yb = torch.full((2, 400), 7.0, device="cuda")
+    B.linear_rope(dev(xb), w, yb[:, 40:360], rope_cols=128, position_offset=9)
+    got = host(yb)
+    ref = O.linear_rope(xb, np.ascontiguousarray(wb[:320, :256].T), 128, 9, 64, 1e4)
+    assert_close(got[:, 40:360], ref, FP32_TOL, "out-major strided")
+    assert np.all(got[:, :40] == 7.0) and np.all(got[:, 360:] == 7.0)
+    # more than 4 rows, or an odd output width, is refused for this layout
+    with pytest.raises(B.BnError, match="at most 4 rows"):
+        B.linear_rope(torch.randn((5, 256), device="cuda"), w)
+    with pytest.raises(B.BnError, match="even output width"):
+        B.linear_rope(dev(xb), dev(wb)[:319, :256].t())
+
+
 def test_linear_rope_empty_k_gives_zeros():
     x = torch.empty((5, 0), device="cuda")
     w = torch.empty((0, 64), device="cuda")
