@@ -208,10 +208,12 @@ def bench_backward(steps, warmup, seed=5):
 def bench_linear(steps, warmup, seed=6):
     """Config 4's fused QKV projection with RoPE on its Q/K columns, fp32:
     x [M, 2048] @ w [2048, 2560], rope_cols 2304, for the prompt (M = 512,
-    MFMA-bound, flops 2*M*K*N) and a decode step (M = 1, HBM-bound on w,
-    bytes K*N*4 + x + y; timed from a replayed graph of 16 launches).  Beside
-    it, the unfused path it replaces: torch's library GEMM (x @ w) followed by
-    bn_rope on the Q/K columns."""
+    MFMA-bound, flops 2*M*K*N, row-major w) and a decode step (M = 1,
+    HBM-bound on w, bytes K*N*4 + x + y; timed from a replayed graph of 16
+    launches; w output-major, as the TinyLLaMA driver stores it, with the
+    row-major split-k path beside it).  Beside each, the unfused path it
+    replaces: torch's library GEMM (x @ w) followed by bn_rope on the Q/K
+    columns."""
     import torch
     import bnhip
     g = torch.Generator(device="cuda").manual_seed(seed)
@@ -226,12 +228,15 @@ def bench_linear(steps, warmup, seed=6):
         y = torch.empty((M, N), device="cuda")
         ws = torch.empty(max(bnhip.lib().bn_linear_rope_workspace_size(0, M, N, K) // 4, 1),
                          device="cuda")
-        fused = lambda i: bnhip.linear_rope(x, ws_all[i % 16], y, rope_cols=RC, position_offset=7,
+        # the decode step reads the weights output-major ([N, K] storage, the
+        # [K, N] view transposed): the few-rows kernel without a k split
+        wts = ws_all if M > 1 else [w.t().contiguous().t() for w in ws_all]
+        fused = lambda i: bnhip.linear_rope(x, wts[i % 16], y, rope_cols=RC, position_offset=7,
                                              workspace=ws)
         yt = torch.empty((M, N), device="cuda")
 
         def unfused(i):
-            torch.matmul(x, ws_all[i % 16], out=yt)
+            torch.matmul(x, wts[i % 16], out=yt)
             q = yt[:, :RC]
             bnhip.call("bn_rope", bnhip.C.byref(bnhip.view(q)), bnhip.C.byref(bnhip.view(q)), 7, 64,
                        1e4, bnhip.stream_of())
@@ -243,6 +248,10 @@ def bench_linear(steps, warmup, seed=6):
             # launches (one per weight copy) replayed from a captured graph
             ms = time_graph(fused, 16, steps, warmup, check=y)
             ms_ref = time_graph(unfused, 16, steps, warmup, check=yt)
+            ms_rm = time_graph(lambda i: bnhip.linear_rope(x, ws_all[i % 16], y, rope_cols=RC,
+                                                           position_offset=7, workspace=ws),
+                               16, steps, warmup, check=y)
+            del wts
         fl = 2 * M * K * N
         byt = 4 * (K * N + M * K + M * N)
         if M > 1:
@@ -255,6 +264,8 @@ def bench_linear(steps, warmup, seed=6):
             v = byt / (ms * 1e-3) / 1e9
             out["decode_step"] = {"value": round(v, 1), "unit": "GB/s", "ms_per_launch": round(ms, 5),
                                   "m": M, "unfused_ms": round(ms_ref, 5),
+                                  "weights": "output-major ([N, K] storage)",
+                                  "row_major_split_k_ms": round(ms_rm, 5),
                                   "roofline": roofline("hbm", v, PEAK_HBM_GBS, "GB/s",
                                                        measured_traffic("linear_rope_decode"))}
     out["config"] = "config 4 QKV projection + RoPE, fp32, K=2048, N=2560, rope_cols=2304"
