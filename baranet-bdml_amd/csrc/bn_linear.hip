@@ -13,6 +13,10 @@
 // ds_read_b64_tr_b16 and the x fragments in the same k order.  Small grids
 // split k: each slab writes fp32 partial sums and linear_reduce_kernel adds
 // them in slab order and applies the rotation (deterministic, no atomics).
+// A few rows (decode steps) stream w instead: row-major w through
+// linear_small_kernel's k slabs (and the same reduction), an output-major w
+// (the transposed view of an [n, k] matrix) through linear_gemv_t_kernel,
+// one launch with the epilogue and no partials.
 #include <algorithm>
 
 #include "bn_common.hpp"
@@ -52,7 +56,8 @@ struct LinParams {
   int64_t x_rs, w_rs, y_rs;
   int m, n, k, kchunk;  // kchunk: k per slab, a multiple of the stage depth
   int rope_cols, head_dim, pos0;
-  // epilogue extras of the split-k reduction (decode steps, fp32): columns
+  // epilogue extras of the split-k reduction and of the output-major
+  // few-rows kernel (decode steps, fp32): columns
   // [app_col, app_col + app_w) of row r also go to k_dst + r*app_rs and
   // [app_col + app_w, app_col + 2*app_w) to v_dst + r*app_rs (the K and V
   // rows of a QKV projection appended to the caches); null: none
@@ -61,9 +66,9 @@ struct LinParams {
   int64_t app_rs;
 };
 
-// reduction epilogues: EPI_PLAIN writes y (rotated in the first rope_cols
-// columns); EPI_SILU reads the slabs as gate | up halves and writes
-// y = silu(gate) * up, the width of one half
+// epilogues: EPI_PLAIN writes y (rotated in the first rope_cols columns);
+// EPI_SILU takes the sums as gate | up halves and writes y = silu(gate) * up,
+// the width of one half
 constexpr int EPI_PLAIN = kLinEpiPlain, EPI_SILU = kLinEpiSilu;
 
 __device__ __forceinline__ bf16x4_t tr16(const bf16_t *lds) {
