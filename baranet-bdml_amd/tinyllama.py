@@ -66,20 +66,24 @@ class TinyLlama:
     SMALL_ROWS = 4
 
     def __init__(self, cfg: TinyLlamaConfig, max_len: int, seed: int = 1, std: float = 0.02,
-                 dtype=torch.float32):
+                 dtype=torch.float32, out_major: bool = True):
+        """out_major: projection weights stored [out, in] (default; decode steps
+        take the output-major few-rows kernel) or [in, out] row-major (the
+        split-k few-rows kernel); the same values either way."""
         if dtype != torch.float32:
             raise ValueError("config 4 is fp32")
         self.cfg = cfg
         self.max_len = max_len
+        self.out_major = out_major
         g = torch.Generator(device="cuda").manual_seed(seed)
         h, kv, inter = cfg.hidden_size, cfg.num_key_value_heads * cfg.head_dim, cfg.intermediate_size
 
         def w(*shape):
             return torch.randn(shape, generator=g, device="cuda") * std
 
-        def out_major(m):
-            # [in, out] values stored [out, in]; the model keeps the [in, out] view
-            return m.t().contiguous().t()
+        def laid_out(m):
+            # [in, out] values stored [out, in] (out_major); the model keeps the [in, out] view
+            return m.t().contiguous().t() if out_major else m
 
         self.embed = w(cfg.vocab_size, h)
         self.layers = []
@@ -89,15 +93,20 @@ class TinyLlama:
             wg, wu = w(h, inter), w(h, inter)
             self.layers.append(dict(
                 ln1=torch.ones((1, h), device="cuda"),
-                wqkv=out_major(torch.cat([wq, wk, wv], dim=1)), wo=out_major(wo),
-                ln2=torch.ones((1, h), device="cuda"), wgu=out_major(torch.cat([wg, wu], dim=1)),
-                wd=out_major(w(inter, h)),
+                wqkv=laid_out(torch.cat([wq, wk, wv], dim=1)), wo=laid_out(wo),
+                ln2=torch.ones((1, h), device="cuda"), wgu=laid_out(torch.cat([wg, wu], dim=1)),
+                wd=laid_out(w(inter, h)),
                 k_cache=torch.zeros((1, max_len, cfg.num_key_value_heads, cfg.head_dim), device="cuda"),
                 v_cache=torch.zeros((1, max_len, cfg.num_key_value_heads, cfg.head_dim), device="cuda")))
         self.ln_f = torch.ones((1, h), device="cuda")
-        self.lm_head = out_major(w(h, cfg.vocab_size))
+        self.lm_head = laid_out(w(h, cfg.vocab_size))
         self.length = 0
         self.ws = bnhip.decode_workspace(1, max_len, cfg.num_attention_heads, cfg.head_dim)
+        # row-major few-rows projections: split-k partial sums of the largest one
+        shapes = [(h, h + 2 * kv), (h, h), (h, 2 * inter), (inter, h), (h, cfg.vocab_size)]
+        n_ws = 0 if out_major else max(bnhip.lib().bn_linear_rope_workspace_size(0, self.SMALL_ROWS, n, k)
+                                       for k, n in shapes)
+        self.lin_ws = torch.empty(max(n_ws // 4, 1), device="cuda") if n_ws else None
         self.path_ms = 0.0
         self.timing = False
         self.trace = None  # list of (kernel, inputs, output, kw) when set
@@ -183,7 +192,8 @@ class TinyLlama:
 
         def run():
             bnhip.linear_rope(x, w, y, rope_cols=rope_cols, position_offset=pos0,
-                              head_dim=self.cfg.head_dim, theta=self.cfg.rope_theta)
+                              head_dim=self.cfg.head_dim, theta=self.cfg.rope_theta,
+                              workspace=self.lin_ws)
         if rope_cols:
             self._timed(run, "qkv_rope")  # carries the RoPE of the step
             self._record("linear_rope", [x, w], y, rope_cols=rope_cols, offset=pos0,
@@ -290,7 +300,8 @@ class TinyLlama:
         cfg = self.cfg
         return bnhip.BnLlamaConfig(cfg.num_hidden_layers, cfg.hidden_size, cfg.num_attention_heads,
                                    cfg.num_key_value_heads, cfg.intermediate_size, cfg.vocab_size,
-                                   self.max_len, cfg.rms_norm_eps, cfg.rope_theta, 1)
+                                   self.max_len, cfg.rms_norm_eps, cfg.rope_theta,
+                                   int(self.out_major))
 
     def generate_native(self, ids: torch.Tensor, new_tokens: int):
         """Greedy decode with the decode loop in native code: the prompt runs

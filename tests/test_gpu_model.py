@@ -76,9 +76,9 @@ def test_config1_offset_and_views():
     assert_close(out, ref, FP32_TOL, "offset 5")
 
 
-def small_llama(layers=2, vocab=512, max_len=96):
+def small_llama(layers=2, vocab=512, max_len=96, out_major=True):
     cfg = TinyLlamaConfig(vocab_size=vocab, num_hidden_layers=layers)
-    return TinyLlama(cfg, max_len=max_len, seed=1)
+    return TinyLlama(cfg, max_len=max_len, seed=1, out_major=out_major)
 
 
 def test_tinyllama_kernels_teacher_forced():
@@ -125,16 +125,18 @@ def test_tinyllama_cache_matches_recompute():
     assert float(np.max(np.abs(a - b)) / np.max(np.abs(b))) < 1e-4
 
 
+@pytest.mark.parametrize("out_major", [True, False])
 @pytest.mark.parametrize("prompt,new", [(40, 12), (7, 1), (1, 30)])
-def test_native_decode_matches_generate(prompt, new):
+def test_native_decode_matches_generate(prompt, new, out_major):
     """bn_llama_decode runs the decode loop natively (gather, layers, lm_head,
-    argmax, next token fed on the device).  Its QKV reduction also appends K
-    and V to the caches and its gate|up reduction writes silu(gate) * up; the
-    slabs are summed in the order of the unfused reduction, so the generated
-    tokens and every layer's KV cache are bit-identical to generate(), which
-    runs the ops one by one."""
+    argmax, next token fed on the device).  Its QKV projection also appends K
+    and V to the caches and its gate|up projection writes silu(gate) * up --
+    in the output-major kernel's epilogue (out_major) or in the split-k
+    reduction, whose slabs are summed in the order of the unfused one -- so
+    the generated tokens and every layer's KV cache are bit-identical to
+    generate(), which runs the ops one by one."""
     ids = torch.from_numpy(np.random.default_rng(7 + prompt).integers(0, 512, prompt)).cuda()
-    a, b = small_llama(), small_llama()
+    a, b = small_llama(out_major=out_major), small_llama(out_major=out_major)
     ref, _ = a.generate(ids, new)
     got = b.generate_native(ids, new)
     torch.cuda.synchronize()
