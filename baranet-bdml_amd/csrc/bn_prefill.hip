@@ -546,8 +546,9 @@ constexpr int KP32 = HD + 4;  // 272 B pitch
 constexpr int VP32 = BN + 4;
 
 __global__ __launch_bounds__(256, 2) void prefill_f32_kernel(PrefillParams p) {
-  __shared__ __attribute__((aligned(16))) float Ks[BN * KP32];
-  __shared__ __attribute__((aligned(16))) float Vt[HD * VP32];
+  // double-buffered K and V^T blocks: one barrier per block
+  __shared__ __attribute__((aligned(16))) float Ks2[2][BN * KP32];
+  __shared__ __attribute__((aligned(16))) float Vt2[2][HD * VP32];
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int r32 = lane & 31, hf = lane >> 5;
@@ -594,7 +595,8 @@ __global__ __launch_bounds__(256, 2) void prefill_f32_kernel(PrefillParams p) {
       }
     }
   };
-  auto lstore = [&]() {
+  auto lstore = [&](int buf) {
+    float *Ks = Ks2[buf], *Vt = Vt2[buf];
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       const int idx = tid + 256 * c, key = idx >> 4, dc = idx & 15;
@@ -609,15 +611,19 @@ __global__ __launch_bounds__(256, 2) void prefill_f32_kernel(PrefillParams p) {
   float m = -INFINITY, l = 0.f;
   f32x16_t o[2] = {f32x16_t{}, f32x16_t{}};
 
-  if (nblk > 0) gload(0);
+  // block blk is computed from buffer blk & 1 while block blk + 1 (loaded
+  // one block earlier) is stored into the other buffer, whose last reads were
+  // in block blk - 1, before the previous barrier
+  if (nblk > 0) {
+    gload(0);
+    lstore(0);
+  }
+  __syncthreads();
+  if (nblk > 1) gload(BN);
   for (int blk = 0; blk < nblk; ++blk) {
-    const int kb = blk * BN;
-    __syncthreads();
-    lstore();
-    __syncthreads();
-    if (blk + 1 < nblk) gload(kb + BN);
-    if (kb >= wave_kend) continue;
-
+    const int kb = blk * BN, buf = blk & 1;
+    if (kb < wave_kend) {  // wave-uniform
+      const float *Ks = Ks2[buf], *Vt = Vt2[buf];
     f32x16_t s[2];
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt) {
@@ -651,6 +657,12 @@ __global__ __launch_bounds__(256, 2) void prefill_f32_kernel(PrefillParams p) {
           o[dt] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.w, s[kt][4 * gi + 3], o[dt], 0, 0, 0);
         }
       }
+    }
+    if (blk + 1 < nblk) {
+      lstore(buf ^ 1);
+      if (blk + 2 < nblk) gload(kb + 2 * BN);
+    }
+    __syncthreads();
   }
 
   const float lt = l + __shfl_xor(l, 32, 64);
