@@ -255,6 +255,22 @@ def test_linear_rope_validation():
     assert s == B.BN_ERR_NOT_DEVICE and m == "Linear: only GPU implementation available"
 
 
+def test_linear_rope_output_major_validation():
+    # w viewed [k, n] with stride_h 1: the output-major few-rows kernel; its
+    # limits are checked before the device
+    wt = lambda k, n, sw=None: V(k, n, stride_h=1, stride_w=k if sw is None else sw)
+    s, m = st("bn_linear_rope", V(5, 256), wt(256, 128), V(5, 128), 0, 0, 64, 1e4, None, 0, None)
+    assert s == B.BN_ERR_UNSUPPORTED and "at most 4 rows" in m
+    s, m = st("bn_linear_rope", V(1, 256), wt(256, 126), V(1, 126), 0, 0, 64, 1e4, None, 0, None)
+    assert s == B.BN_ERR_UNSUPPORTED and "even output width" in m
+    s, m = st("bn_linear_rope", V(1, 256), wt(256, 128, 258), V(1, 128), 0, 0, 64, 1e4, None, 0, None)
+    assert s == B.BN_ERR_UNSUPPORTED  # stride between outputs not a multiple of 16 bytes
+    s, m = st("bn_linear_rope", V(2, 16384), wt(16384, 64), V(2, 64), 0, 0, 64, 1e4, None, 0, None)
+    assert s == B.BN_ERR_UNSUPPORTED and "staged x elements" in m
+    s, m = st("bn_linear_rope", V(4, 256), wt(256, 128), V(4, 128), 64, 3, 64, 1e4, None, 0, None)
+    assert s == B.BN_ERR_NOT_DEVICE and m == "Linear: only GPU implementation available"
+
+
 def test_linear_rope_workspace_size():
     L = B.lib()
     # config 4 decode step (few rows): 10 strips of 256 columns x 32 slabs of 64 rows
