@@ -357,17 +357,18 @@ __global__ __launch_bounds__(256, OCC) void prefill_bf16_kernel(PrefillParams p)
   // p = exp2(s * c - mc) as bf16 MFMA operands and the row sum of those bf16 values
   auto exps = [&](const f32x16_t &s, float mc, bf16x8_t (&pb)[2], float &rs)
       __attribute__((always_inline)) {
-    float r2[2] = {0.f, 0.f};  // two chains: the sum is needed early by the check
+    // one chain of eight dot2s, the first from an inline zero (no register
+    // to clear, no second chain to add)
+    float r = 0.f;
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
 #pragma unroll
       for (int j = 0; j < 8; ++j) pb[u][j] = (__bf16)__builtin_amdgcn_exp2f(fmaf(s[8 * u + j], c, -mc));
 #pragma unroll
       for (int j = 0; j < 4; ++j)
-        r2[u] = __builtin_amdgcn_fdot2_f32_bf16(bf16x2_t{pb[u][2 * j], pb[u][2 * j + 1]}, ones,
-                                                r2[u], false);
+        r = __builtin_amdgcn_fdot2_f32_bf16(bf16x2_t{pb[u][2 * j], pb[u][2 * j + 1]}, ones, r, false);
     }
-    rs = r2[0] + r2[1];
+    rs = r;
   };
   // causal / tail mask of tile t (keys kb..kb+31) in place
   auto mask = [&](int t, f32x16_t (&sc)[RT]) __attribute__((always_inline)) {
