@@ -57,10 +57,25 @@ int device_cu_count();
 // every epilogue, so a fused epilogue gives the bits of the unfused ops.
 // The epilogues need the split-k path (always taken for m <= 8).
 constexpr int kLinEpiPlain = 0, kLinEpiSilu = 1;
+// fp32 row width up to which bn_rmsnorm / bn_add_rmsnorm run their one-wave
+// row kernels (64 lanes x 8 chunks of 4; wider rows take a strided kernel
+// with another summation order)
+constexpr int kNormRowF32 = 2048;
+// A normalised input for an output-major projection of one fp32 row (a
+// decode step; k <= kNormRowF32): the kernel reads x as the residual stream
+// h and projects rmsnorm(h + d) * w instead (d null: rmsnorm(h) * w), formed as
+// add_rmsnorm / rmsnorm form it, so the product has the bits of the norm
+// kernel followed by the projection; h_out (not null) receives h + d.  h_out
+// must not alias h or d (other workgroups still read them).
+struct LinNorm {
+  const float *d, *w;
+  float *h_out;
+  float eps;
+};
 int linear_run(const bn_view *x, const bn_view *w, const bn_view *y, int rope_cols,
                int position_offset, int head_dim, float theta, void *workspace,
                size_t workspace_bytes, int epi, float *k_dst, float *v_dst, int app_col, int app_w,
-               int64_t app_rs, void *stream);
+               int64_t app_rs, void *stream, const LinNorm *nrm = nullptr);
 
 // ------------------------------------------------------------ validation
 inline size_t dtype_size(int dt) { return dt == BN_BF16 ? 2 : 4; }

@@ -64,6 +64,10 @@ struct LinParams {
   float *k_dst, *v_dst;
   int app_col, app_w;
   int64_t app_rs;
+  // normalised input of the output-major kernel (LinNorm): x is h
+  const float *nd, *nw;
+  float *nh_out;
+  float neps;
 };
 
 // epilogues: EPI_PLAIN writes y (rotated in the first rope_cols columns);
@@ -369,9 +373,12 @@ constexpr int GV_M = 4;        // rows of x, at most
 constexpr int GV_ROUND = 8;    // 16-byte loads per weight row and lane in a round
 constexpr int GV_XMAX = 16384; // fp32 elements of x in LDS (64 KB)
 
-template <typename T, int MR, int EPI>
+// NRM: x = rmsnorm(h + d) * w formed in the staging (one fp32 row of at
+// most kNormRowF32 elements: two 16-byte chunks per thread)
+template <typename T, int MR, int EPI, bool NRM = false>
 __global__ __launch_bounds__(256) void linear_gemv_t_kernel(LinParams p, RopeFreqs fr) {
-  extern __shared__ __attribute__((aligned(16))) float gxs[];  // [MR][kp], zeros past k
+  // [MR][kp], zeros past k; NRM: then h + d [kp]
+  extern __shared__ __attribute__((aligned(16))) float gxs[];
   constexpr int VE = 16 / (int)sizeof(T);  // k per 16-byte load
   constexpr int SPAN = 64 * VE;            // k per wave-wide load
   const int tid = threadIdx.x, lane = tid & 63;
@@ -446,8 +453,79 @@ __global__ __launch_bounds__(256) void linear_gemv_t_kernel(LinParams p, RopeFre
   };
 
   u32x4_t a0[GV_ROUND], b0[GV_ROUND];
-  issue(a0, b0, 0);
-  {
+  if constexpr (NRM) {
+    // x = rmsnorm(h + d) * nw (one fp32 row, k <= kNormRowF32: one pass), each
+    // element formed as add_rmsnorm_rows_kernel (d given) or
+    // rmsnorm_rows_kernel form it: h + d, the sum of squares in their order
+    // (lane l of one wave over chunks l, l + 64, ... in turn as one fma
+    // chain, then the wave sum), 1 / sqrtf(ss / k + eps), (v * inv) * w.
+    // Every wave of every workgroup forms the same sum from h + d staged in
+    // LDS; workgroup 0 also stores h + d to nh_out (the next residual).  The
+    // h, d and norm-weight loads go out before the first weight round, so
+    // they return first (in order) and the norm is formed while the weights
+    // are on their way; no loop or branch sits between them and their use.
+    static_assert(MR == 1 && sizeof(T) == 4, "the normalised input is one fp32 row");
+    constexpr int XB = kNormRowF32 / 1024;  // 16-byte chunks per thread
+    constexpr int CPL = kNormRowF32 / 256;  // 16-byte chunks per lane of one wave
+    const float *H = (const float *)p.x;
+    const float *D = p.nd ? p.nd : H;  // no d: a second read of h, not used
+    const int cpr = kp / 4, nch = p.k / 4;
+    float *raw = gxs + kp;
+    u32x4_t hr[XB], dr[XB], wr[XB];
+#pragma unroll
+    for (int u = 0; u < XB; ++u) {
+      const int kk = min((u * 256 + tid) * 4, p.k - 4);
+      hr[u] = *(const u32x4_t *)(H + kk);
+      dr[u] = *(const u32x4_t *)(D + kk);
+      wr[u] = *(const u32x4_t *)(p.nw + kk);
+    }
+    __builtin_amdgcn_sched_barrier(0);  // keep them ahead of the weight loads
+    issue(a0, b0, 0);
+    float v[XB][4];
+#pragma unroll
+    for (int u = 0; u < XB; ++u) {
+      const int c = u * 256 + tid, kk = c * 4;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float h = __uint_as_float(hr[u][e]);
+        v[u][e] = p.nd ? h + __uint_as_float(dr[u][e]) : h;
+      }
+      if (c < cpr) {
+        const bool ok = kk < p.k;
+        const float4 hv = ok ? make_float4(v[u][0], v[u][1], v[u][2], v[u][3]) : make_float4(0.f, 0.f, 0.f, 0.f);
+        *(float4 *)(raw + kk) = hv;
+        if (ok && p.nh_out && blockIdx.x == 0) *(float4 *)(p.nh_out + kk) = hv;
+      }
+    }
+    __syncthreads();
+    // chunks past the row add exact zeros (fma(0, 0, ss) = ss)
+    float4 h4[CPL];
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) h4[i] = *(const float4 *)(raw + min(lane + 64 * i, nch - 1) * 4);
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      const bool in = lane + 64 * i < nch;
+      const float4 z = in ? h4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+      ss = fmaf(z.x, z.x, ss);
+      ss = fmaf(z.y, z.y, ss);
+      ss = fmaf(z.z, z.z, ss);
+      ss = fmaf(z.w, z.w, ss);
+    }
+    ss = wave_sum(ss);
+    const float inv = 1.0f / sqrtf(ss / (float)p.k + p.neps);  // op_rmsnorm.cuh:44-45
+#pragma unroll
+    for (int u = 0; u < XB; ++u) {
+      const int c = u * 256 + tid, kk = c * 4;
+      if (c < cpr) {
+        float o[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[e] = kk < p.k ? (v[u][e] * inv) * __uint_as_float(wr[u][e]) : 0.f;
+        *(float4 *)(gxs + kk) = make_float4(o[0], o[1], o[2], o[3]);
+      }
+    }
+  } else {
+    issue(a0, b0, 0);
     // x rows in 16-byte chunks: thread tid takes chunks tid + 256u of every
     // row, XB per row requested before any is stored (clamped addresses,
     // zeros selected afterwards: no branch around a load).  One pass covers
@@ -594,7 +672,8 @@ namespace {
 // checked by linear_run; this checks the layout the kernel reads
 int gemv_t_run(const bn_view *x, const bn_view *w, const bn_view *y, int rope_cols,
                int position_offset, int head_dim, const RopeFreqs &fr, int epi, float *k_dst,
-               float *v_dst, int app_col, int app_w, int64_t app_rs, const char *op, void *stream) {
+               float *v_dst, int app_col, int app_w, int64_t app_rs, const LinNorm *nrm,
+               const char *op, void *stream) {
   const int dt = x->dtype;
   const int64_t ve = dt == BN_BF16 ? 8 : 4;  // elements per 16 bytes
   const size_t es = dtype_size(dt);
@@ -616,6 +695,21 @@ int gemv_t_run(const bn_view *x, const bn_view *w, const bn_view *y, int rope_co
                                         std::to_string(GV_XMAX) + " staged x elements");
   if (k_dst && (dt != BN_F32 || app_col < 0 || app_col % 4 || app_w % 4 || app_col + 2 * app_w > n))
     return fail(BN_ERR_UNSUPPORTED, std::string(op) + ": bad K/V append columns");
+  const char *hx = (const char *)x->data + x->offset * (int64_t)es;
+  if (nrm) {  // one fp32 row of h, staged in one pass; h_out written while h and d are read
+    if (dt != BN_F32 || m != 1 || k < 4 || k > kNormRowF32 || !nrm->w)
+      return fail(BN_ERR_UNSUPPORTED, std::string(op) + ": a normalised input is one fp32 row of 4.." +
+                                          std::to_string(kNormRowF32) + " elements with its weight");
+    if ((reinterpret_cast<uintptr_t>(nrm->d) | reinterpret_cast<uintptr_t>(nrm->w) |
+         reinterpret_cast<uintptr_t>(nrm->h_out)) & 15u)
+      return fail(BN_ERR_UNSUPPORTED, std::string(op) + ": the norm's rows must be 16-byte aligned");
+    auto overlaps = [&](const void *a, const void *b) {
+      const char *pa = (const char *)a, *pb = (const char *)b;
+      return a && b && pa < pb + (size_t)k * 4 && pb < pa + (size_t)k * 4;
+    };
+    if (overlaps(nrm->h_out, hx) || overlaps(nrm->h_out, nrm->d))
+      return fail(BN_ERR_INVALID_ARG, std::string(op) + ": the norm's h_out must not overlap h or d");
+  }
   int st;
   if ((st = require_device(op, {x, w, y}))) return st;
   if (y->h == 0 || y->w == 0) return BN_OK;
@@ -628,21 +722,28 @@ int gemv_t_run(const bn_view *x, const bn_view *w, const bn_view *y, int rope_co
   p.m = m; p.n = n; p.k = k;
   p.rope_cols = rope_cols; p.head_dim = rope_cols ? head_dim : 2; p.pos0 = position_offset;
   p.k_dst = k_dst; p.v_dst = v_dst; p.app_col = app_col; p.app_w = app_w; p.app_rs = app_rs;
+  if (nrm) {
+    p.nd = nrm->d; p.nw = nrm->w; p.nh_out = nrm->h_out; p.neps = nrm->eps;
+  }
   const int mr = m <= 1 ? 1 : (m <= 2 ? 2 : 4);
-  const size_t lds = (size_t)mr * kp * sizeof(float);
+  const size_t lds = (size_t)(nrm ? 2 : mr) * kp * sizeof(float);
   // four waves per workgroup, two weight rows (one output pair, or one
   // gate | up output) per wave
   const int waves = n / 2;
   const dim3 grid((unsigned)((waves + 3) / 4)), block(256);
   hipStream_t s = as_stream(stream);
-#define BN_GV(T, MR, E) hipLaunchKernelGGL((linear_gemv_t_kernel<T, MR, E>), grid, block, lds, s, p, fr)
+#define BN_GV(T, MR, E, ...) \
+  hipLaunchKernelGGL((linear_gemv_t_kernel<T, MR, E, ##__VA_ARGS__>), grid, block, lds, s, p, fr)
 #define BN_GV_M(T, E)                 \
   do {                                \
     if (mr == 1) BN_GV(T, 1, E);      \
     else if (mr == 2) BN_GV(T, 2, E); \
     else BN_GV(T, 4, E);              \
   } while (0)
-  if (dt == BN_F32) {
+  if (nrm) {
+    if (epi == EPI_SILU) BN_GV(float, 1, EPI_SILU, true);
+    else BN_GV(float, 1, EPI_PLAIN, true);
+  } else if (dt == BN_F32) {
     if (epi == EPI_SILU) BN_GV_M(float, EPI_SILU);
     else BN_GV_M(float, EPI_PLAIN);
   } else {
@@ -663,7 +764,7 @@ int gemv_t_run(const bn_view *x, const bn_view *w, const bn_view *y, int rope_co
 int linear_run(const bn_view *x, const bn_view *w, const bn_view *y, int rope_cols,
                int position_offset, int head_dim, float theta, void *workspace,
                size_t workspace_bytes, int epi, float *k_dst, float *v_dst, int app_col, int app_w,
-               int64_t app_rs, void *stream) {
+               int64_t app_rs, void *stream, const LinNorm *nrm) {
   const char *op = epi == EPI_SILU ? "Linear+SwiGLU" : "Linear";
   const unsigned mask = (1u << BN_F32) | (1u << BN_BF16);
   int st;
@@ -699,7 +800,8 @@ int linear_run(const bn_view *x, const bn_view *w, const bn_view *y, int rope_co
   // the few-rows streaming kernel without a k split
   if ((int64_t)w->h * w->w > 0 && w->stride_h == 1 && w->stride_w != 1)
     return gemv_t_run(x, w, y, rope_cols, position_offset, head_dim, fr, epi, k_dst, v_dst, app_col,
-                      app_w, app_rs, op, stream);
+                      app_w, app_rs, nrm, op, stream);
+  if (nrm) return fail(BN_ERR_UNSUPPORTED, std::string(op) + ": a normalised input needs an output-major w");
   if (!unit(x) || !unit(w) || !unit(y))
     return fail(BN_ERR_UNSUPPORTED, std::string(op) + ": rows must be contiguous (stride_w == 1)");
   if (!ok(x) || !ok(w) || !ok(y) || x->w % ve || y->w % ve)

@@ -80,6 +80,7 @@ template <> struct Chunk<bf16_t> {
 
 constexpr int kRowsPerBlock = 4;  // 4 waves, one row each
 constexpr int kMaxChunks = 8;     // chunks per lane kept in registers (at most)
+static_assert(64 * kMaxChunks * 4 == kNormRowF32, "fp32 rows of the one-wave kernels");
 
 // y = rope?(x / rms * w); requires cols % VEC == 0, cols <= 64*NCH*VEC,
 // head_dim % VEC == 0 when ROPE.  NCH = 16-byte chunks per lane.
@@ -104,13 +105,16 @@ __global__ __launch_bounds__(256) void rmsnorm_rows_kernel(
     wraw[i] = load_raw(w + w_off + cc * VEC);
   }
   float v[NCH][VEC];
+  // sum of squares as one fma chain in element order (spelled out, so the
+  // compiler cannot pick another contraction: projections that form this
+  // norm in their own staging reproduce these bits)
   float ss = 0.f;
 #pragma unroll
   for (int i = 0; i < NCH; ++i) {
     Chunk<T>::cvt(xraw[i], v[i]);
     if (lane + 64 * i < nchunks) {
 #pragma unroll
-      for (int j = 0; j < VEC; ++j) ss += v[i][j] * v[i][j];
+      for (int j = 0; j < VEC; ++j) ss = fmaf(v[i][j], v[i][j], ss);
     }
   }
   ss = wave_sum(ss);
@@ -203,7 +207,7 @@ __global__ __launch_bounds__(256) void add_rmsnorm_rows_kernel(
     if (lane + 64 * i < nchunks) {
       Chunk<T>::store(h + (int64_t)row * h_rs + (lane + 64 * i) * VEC, v[i]);
 #pragma unroll
-      for (int j = 0; j < VEC; ++j) ss += v[i][j] * v[i][j];
+      for (int j = 0; j < VEC; ++j) ss = fmaf(v[i][j], v[i][j], ss);  // one fma chain, as above
     }
   }
   ss = wave_sum(ss);
