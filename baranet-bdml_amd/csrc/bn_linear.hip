@@ -685,10 +685,13 @@ int gemv_t_run(const bn_view *x, const bn_view *w, const bn_view *y, int rope_co
   auto rows_ok = [&](const bn_view *v) {
     return (int64_t)v->h * v->w == 0 || (v->stride_w == 1 && v->stride_h % ve == 0 && base_ok(v));
   };
-  if (!rows_ok(x) || !rows_ok(y) || !base_ok(w) || w->stride_w % ve || k % ve || y->w % 2)
+  // x is staged and w streamed 16 bytes at a time; y is stored one element
+  // at a time (any row stride)
+  const bool y_ok = (int64_t)y->h * y->w == 0 || y->stride_w == 1;
+  if (!rows_ok(x) || !y_ok || !base_ok(w) || w->stride_w % ve || k % ve || y->w % 2)
     return fail(BN_ERR_UNSUPPORTED,
-                std::string(op) + ": an output-major w needs 16-byte aligned rows of x, y and w, k a "
-                                  "multiple of 16 bytes and an even output width");
+                std::string(op) + ": an output-major w needs 16-byte aligned rows of x and w, k a "
+                                  "multiple of 16 bytes, contiguous rows of y and an even output width");
   if (m > GV_M || (int64_t)m * kp > GV_XMAX)
     return fail(BN_ERR_UNSUPPORTED, std::string(op) + ": an output-major w takes at most " +
                                         std::to_string(GV_M) + " rows of x and " +

@@ -154,7 +154,8 @@ int bn_matmul(const bn_view *a, const bn_view *b, const bn_view *c, void *stream
  * bytes, the view's element (0, 0) 16-byte aligned): for M <= 4 and
  * M*ceil(K / (64*elements per 16 bytes))*64*elements per 16 bytes <= 16384
  * this streams each output's contiguous weights once with no k split (no
- * workspace; N even); other M are BN_ERR_UNSUPPORTED for that layout. */
+ * workspace; N even; x rows 16-byte aligned, y rows contiguous at any
+ * stride); other M are BN_ERR_UNSUPPORTED for that layout. */
 size_t bn_linear_rope_workspace_size(int dtype, int m, int n, int k);
 int bn_linear_rope(const bn_view *x, const bn_view *w, const bn_view *y,
                    int rope_cols, int position_offset, int head_dim, float theta,

@@ -261,8 +261,12 @@ def test_linear_rope_output_major_validation():
     wt = lambda k, n, sw=None: V(k, n, stride_h=1, stride_w=k if sw is None else sw)
     s, m = st("bn_linear_rope", V(5, 256), wt(256, 128), V(5, 128), 0, 0, 64, 1e4, None, 0, None)
     assert s == B.BN_ERR_UNSUPPORTED and "at most 4 rows" in m
-    s, m = st("bn_linear_rope", V(1, 256), wt(256, 126), V(1, 126), 0, 0, 64, 1e4, None, 0, None)
+    s, m = st("bn_linear_rope", V(1, 256), wt(256, 127), V(1, 127), 0, 0, 64, 1e4, None, 0, None)
     assert s == B.BN_ERR_UNSUPPORTED and "even output width" in m
+    # y is stored one element at a time: a row stride that is not a multiple
+    # of 16 bytes passes the layout checks (host views stop at the device check)
+    s, m = st("bn_linear_rope", V(2, 256), wt(256, 126), V(2, 126), 0, 0, 64, 1e4, None, 0, None)
+    assert s == B.BN_ERR_NOT_DEVICE
     s, m = st("bn_linear_rope", V(1, 256), wt(256, 128, 258), V(1, 128), 0, 0, 64, 1e4, None, 0, None)
     assert s == B.BN_ERR_UNSUPPORTED  # stride between outputs not a multiple of 16 bytes
     s, m = st("bn_linear_rope", V(2, 16384), wt(16384, 64), V(2, 64), 0, 0, 64, 1e4, None, 0, None)

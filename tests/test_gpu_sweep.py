@@ -12,7 +12,11 @@ compares every element with the oracle:
 * decode: every kernel the host can pick (fp32 single pass, fp32 split-K,
   bf16 one workgroup per (sequence, KV head), bf16 split rows, bf16 split
   MFMA), with lengths 0, 1, max_len and past max_len among the random ones;
-* backward (bf16): random groups, offsets and both mask modes.
+* backward (bf16): random groups, offsets and both mask modes;
+* projection + RoPE (fp32, bf16): row-major weights over 1-300 rows (the
+  tiled kernel, with and without a k split, and the few-rows streaming
+  kernel) and output-major weights over 1-4 rows, random widths, rotated
+  column counts and positions.
 
 Each case prints its shape in the assertion message, and the seeds are fixed,
 so a failure names a reproducible input.
@@ -193,3 +197,40 @@ def test_prefill_backward_sweep(i):
         vis = np.arange(Skv)[None, :] <= np.arange(Sq)[:, None] + off
         assert np.all(got[0][:, ~vis.any(1)] == 0.0)
         assert np.all(got[1][:, ~vis.any(0)] == 0.0) and np.all(got[2][:, ~vis.any(0)] == 0.0)
+
+
+# -------------------------------------------------- projection + RoPE
+def linear_case(layout, i):
+    """(M, K, N, rope_cols, offset, dtype): row-major w takes the tiled MFMA
+    kernel (k split when the grid is small) or, for a few rows, the
+    streaming kernel and its slab reduction; output-major w (the transposed
+    view of [N, K] storage) the one-launch streaming kernel (1-4 rows)."""
+    rng = np.random.default_rng(6000 + 31 * (layout == "out") + i)
+    dtype = ("f32", "bf16")[i % 2]
+    if layout == "row":
+        M = int(rng.choice([1, 2, 3, 8, 9, 64, 65, 300]))
+        K, N = 8 * int(rng.integers(1, 190)), 8 * int(rng.integers(1, 150))
+    else:
+        M = int(rng.integers(1, 5))
+        K, N = 8 * int(rng.integers(1, 1100)), 2 * int(rng.integers(1, 1500))
+        K = min(K, (16384 // M - 512) // 8 * 8)  # the staged x rows fit the kernel's LDS
+    rc = 64 * int(rng.integers(0, N // 64 + 1))
+    return M, K, N, rc, int(rng.integers(0, 5000)), dtype
+
+
+@pytest.mark.parametrize("i", range(10))
+@pytest.mark.parametrize("layout", ["row", "out"])
+def test_linear_rope_sweep(layout, i):
+    M, K, N, rc, off, dtype = case = linear_case(layout, i)
+    rng = np.random.default_rng(6500 + 31 * (layout == "out") + i)
+    x = draw(rng, (M, K), dtype)
+    w = (draw(rng, (K, N), dtype) / np.sqrt(K)).astype(np.float32)
+    if dtype == "bf16":
+        w = bf16_round(w)
+    if layout == "row":
+        wd = dev(w, TD[dtype])
+    else:  # [N, K] storage passed as its [K, N] view
+        wd = dev(np.ascontiguousarray(w.T), TD[dtype]).t()
+    y = B.linear_rope(dev(x, TD[dtype]), wd, rope_cols=rc, position_offset=off)
+    ref = O.linear_rope(x, w, rc, off, 64, 1e4)
+    assert_close(host(y), ref, TOL[dtype], f"linear_rope {layout} {case}")
