@@ -146,14 +146,17 @@ def test_native_decode_matches_generate(prompt, new, out_major):
         assert torch.equal(La["k_cache"], Lb["k_cache"]) and torch.equal(La["v_cache"], Lb["v_cache"])
 
 
-@pytest.mark.parametrize("hidden,heads,kv_heads", [(1024, 16, 2), (3072, 48, 6)])
-def test_native_decode_matches_generate_other_widths(hidden, heads, kv_heads):
+@pytest.mark.parametrize("hidden,heads,kv_heads,layers", [(1024, 16, 2, 2), (3072, 48, 6, 2),
+                                                          (2048, 32, 4, 1), (2048, 32, 4, 3)])
+def test_native_decode_matches_generate_other_widths(hidden, heads, kv_heads, layers):
     """hidden 1024: the decode-step norms formed in the projections' x
     staging cover one 16-byte chunk per thread; hidden 3072: wider than the
     one-wave norm kernels' rows, so the native loop launches the norm kernels
-    as the step loop does.  Tokens and caches bit-identical to generate()."""
+    as the step loop does; 1 and 3 layers: the two residual buffers swap an
+    odd number of times per step.  Tokens and caches bit-identical to
+    generate()."""
     cfg = TinyLlamaConfig(vocab_size=512, hidden_size=hidden, intermediate_size=1024,
-                          num_hidden_layers=2, num_attention_heads=heads,
+                          num_hidden_layers=layers, num_attention_heads=heads,
                           num_key_value_heads=kv_heads)
     a, b = (TinyLlama(cfg, max_len=64, seed=2) for _ in range(2))
     ids = torch.from_numpy(np.random.default_rng(11).integers(0, 512, 9)).cuda()
