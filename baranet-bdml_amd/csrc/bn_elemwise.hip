@@ -354,6 +354,66 @@ __global__ __launch_bounds__(256) void argmax_kernel(DView<const T> x, DView<uin
   if (t == 0) y.at(r, 0) = si[0];
 }
 
+// argmax of contiguous fp32 rows (16-byte aligned, width a multiple of 4):
+// 1024 threads, each scanning 16-byte chunks t, t + 1024, ... in column
+// order with four chunks in flight (two rounds for a 32000-wide row), x[0]
+// loaded with the first round instead of before it; the candidates merge
+// by the same rule as argmax_kernel (larger value, then smaller column),
+// by wave shuffles and one LDS step.
+__global__ __launch_bounds__(1024) void argmax_rows_f32_kernel(const float *x, int64_t rs, int w,
+                                                               uint32_t *y, int64_t ys) {
+  constexpr uint32_t NONE = 0xffffffffu;
+  constexpr int U = 4;
+  __shared__ float sv[16];
+  __shared__ uint32_t si[16];
+  const int r = blockIdx.x, t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const float *row = x + (int64_t)r * rs;
+  const int nch = w / 4;
+  const float x0 = row[0];
+  float best = 0.f;
+  uint32_t bi = NONE;
+  for (int c0 = t; c0 < nch; c0 += 1024 * U) {
+    float4 v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) v[u] = *(const float4 *)(row + 4 * min(c0 + 1024 * u, nch - 1));
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int c = c0 + 1024 * u;
+      const float e4[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (c < nch && !(e4[e] != e4[e]) && (bi == NONE || e4[e] > best)) {
+          best = e4[e];
+          bi = (uint32_t)(4 * c + e);
+        }
+    }
+  }
+  // (v, i) beats (bv, bidx): a candidate against none, a larger value, or an
+  // equal value at a smaller column -- a total order, so both lanes of a
+  // butterfly pair keep the same winner
+  auto merge = [&](int width) {
+    for (int m = width; m >= 1; m >>= 1) {
+      const float ov = __shfl_xor(best, m, 64);
+      const uint32_t oi = (uint32_t)__shfl_xor((int)bi, m, 64);
+      if (oi != NONE && (bi == NONE || ov > best || (ov == best && oi < bi))) {
+        best = ov;
+        bi = oi;
+      }
+    }
+  };
+  merge(32);
+  if (lane == 0) {
+    sv[wave] = best;
+    si[wave] = bi;
+  }
+  __syncthreads();
+  if (wave > 0) return;
+  best = lane < 16 ? sv[lane] : 0.f;
+  bi = lane < 16 ? si[lane] : NONE;
+  merge(8);
+  if (lane == 0) y[(int64_t)r * ys] = x0 != x0 ? 0u : bi;  // NaN at column 0: column 0
+}
+
 inline dim3 grid1d(int64_t n) { return dim3((unsigned)((n + 255) / 256)); }
 
 // Plain GEMMs (each operand row-major or a transposed view, output row-major)
@@ -675,7 +735,11 @@ int bn_argmax(const bn_view *x, const bn_view *y, void *stream) {
   if ((st = ensure_device())) return st;
   if (x->h == 0 || x->w == 0) return BN_OK;
   if (x->h > 0x7fffffff) return fail(BN_ERR_UNSUPPORTED, "argmax: too many rows");
-  if (x->dtype == BN_F32)
+  if (x->dtype == BN_F32 && rows_aligned(x, 16) && x->w % 4 == 0)
+    hipLaunchKernelGGL(argmax_rows_f32_kernel, dim3((unsigned)x->h), dim3(1024), 0, as_stream(stream),
+                       (const float *)x->data + x->offset, (int64_t)x->stride_h, (int)x->w,
+                       (uint32_t *)y->data + y->offset, (int64_t)y->stride_h);
+  else if (x->dtype == BN_F32)
     hipLaunchKernelGGL(argmax_kernel<float>, dim3((unsigned)x->h), dim3(256), 0, as_stream(stream),
                        dview<const float>(x), dview<uint32_t>(y));
   else

@@ -469,6 +469,16 @@ def test_argmax_rows_ties_nan_strided():
     one = torch.empty((1, 1), dtype=torch.int32, device="cuda")
     B.call("bn_argmax", V(ad[6:7, :1]), V(one), S0)
     assert int(one.item()) == 0
+    # contiguous widths around the fast path's rounds (1024 threads x 4 chunks
+    # of 4 columns): one chunk, a partial round, several rounds; ties and NaN
+    for wdt in (4, 100, 4100, 70000):
+        b = np.round(r.standard_normal((4, wdt)) * 2).astype(np.float32)  # many ties
+        b[1, 0] = np.nan
+        b[2, 3::7] = np.nan
+        b[3, -1] = 99.0
+        bm = torch.empty((4, 1), dtype=torch.int32, device="cuda")
+        B.call("bn_argmax", V(dev(b)), V(bm), S0)
+        np.testing.assert_array_equal(host(bm)[:, 0], [_argmax_sequential(row) for row in b])
     # uint32 input
     u = r.integers(0, 1 << 31, (3, 5000)).astype(np.int32)
     u[0, [10, 4000]] = (1 << 31) - 1
