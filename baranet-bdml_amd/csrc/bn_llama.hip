@@ -22,14 +22,29 @@ namespace bn {
 namespace {
 
 // x = embed[token]; the token comes from `tok` (device) or, when tok is
-// null, from `first`; ids past the table are clamped (argmax never gives one)
+// null, from `first`; ids past the table are clamped (argmax never gives one).
+// vec (a 16-byte aligned table; hidden is a multiple of 4): 16-byte chunks,
+// all of a thread's requested before any is stored
 __global__ __launch_bounds__(256) void embed_gather_kernel(const float *embed, const uint32_t *tok,
                                                            uint32_t first, int vocab, float *x,
-                                                           int hidden) {
+                                                           int hidden, int vec) {
   uint32_t t = tok ? *tok : first;
   t = t < (uint32_t)vocab ? t : (uint32_t)(vocab - 1);
   const float *row = embed + (int64_t)t * hidden;
-  for (int i = threadIdx.x; i < hidden; i += 256) x[i] = row[i];
+  if (!vec) {
+    for (int i = threadIdx.x; i < hidden; i += 256) x[i] = row[i];
+    return;
+  }
+  constexpr int U = 4;
+  const int n4 = hidden / 4;
+  for (int c0 = threadIdx.x; c0 < n4; c0 += 256 * U) {
+    float4 v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) v[u] = ((const float4 *)row)[min(c0 + 256 * u, n4 - 1)];
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (c0 + 256 * u < n4) ((float4 *)x)[c0 + 256 * u] = v[u];
+  }
 }
 
 // out row r = table row ids[r] (one workgroup per row); an id outside the
@@ -200,7 +215,8 @@ extern "C" int bn_llama_decode(const bn_llama_config *c, const float *embed, con
     const int pos = position + t;
     hipLaunchKernelGGL(embed_gather_kernel, dim3(1), dim3(256), 0, s, embed,
                        t ? (const uint32_t *)(tokens_out + t - 1) : (const uint32_t *)nullptr,
-                       (uint32_t)first_token, c->vocab, hdn, hid);
+                       (uint32_t)first_token, c->vocab, hdn, hid,
+                       (int)((reinterpret_cast<uintptr_t>(embed) & 15u) == 0));
     if ((e = hipGetLastError()) != hipSuccess) {
       st = hip_fail(e, __FILE__, __LINE__);
       break;
