@@ -653,6 +653,12 @@ class LlamaModelCpp {
   LlamaModelCpp(const LlamaCfg &cfg, bool on_device, const std::string &attention)
       : cfg_(cfg), on_device_(on_device) {
     cfg_.validate();
+    // the reference's constructor allocates whatever it is given; the forward
+    // here reads layer 0 and sizes buffers from these, so they must be positive
+    if (cfg_.num_hidden_layers <= 0 || cfg_.vocab_size <= 0 || cfg_.hidden_size <= 0 ||
+        cfg_.intermediate_size <= 0)
+      throw std::runtime_error(
+          "LLaMAModelCpp: num_hidden_layers, vocab_size, hidden_size and intermediate_size must be positive");
     if (attention != "fused_head" && attention != "per_head")
       throw std::runtime_error("LLaMAModelCpp: attention must be 'fused_head' or 'per_head'");
     per_head_ = attention == "per_head";

@@ -61,6 +61,9 @@ constexpr int kLinEpiPlain = 0, kLinEpiSilu = 1;
 // row kernels (64 lanes x 8 chunks of 4; wider rows take a strided kernel
 // with another summation order)
 constexpr int kNormRowF32 = 2048;
+// fp32 elements of x an output-major few-rows projection stages in LDS
+// (64 KB per workgroup: rows staged x k padded to 256 for fp32)
+constexpr int kGemvStagedMax = 16384;
 // A normalised input for an output-major projection of one fp32 row (a
 // decode step; k <= kNormRowF32): the kernel reads x as the residual stream
 // h and projects rmsnorm(h + d) * w instead (d null: rmsnorm(h) * w), formed as

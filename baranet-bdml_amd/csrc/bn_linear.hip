@@ -371,7 +371,7 @@ __global__ __launch_bounds__(256) void linear_small_kernel(LinParams p) {
 // staged in LDS once per workgroup as fp32.
 constexpr int GV_M = 4;        // rows of x, at most
 constexpr int GV_ROUND = 8;    // 16-byte loads per weight row and lane in a round
-constexpr int GV_XMAX = 16384; // fp32 elements of x in LDS (64 KB)
+constexpr int GV_XMAX = kGemvStagedMax; // fp32 elements of x in LDS: staged rows x padded k (64 KB)
 
 // NRM: x = rmsnorm(h + d) * w formed in the staging (one fp32 row of at
 // most kNormRowF32 elements: two 16-byte chunks per thread)
@@ -418,8 +418,10 @@ __global__ __launch_bounds__(256) void linear_gemv_t_kernel(LinParams p, RopeFre
       __attribute__((always_inline)) {
 #pragma unroll
     for (int u = 0; u < GV_ROUND; ++u) {
-      // slots past the padded row carry zero weights; their x reads stay in range
-      const int xo = min((l0 + u) * SPAN, kp - SPAN) + lane * VE;
+      // slots past the padded row carry no weights: skipped (wave-uniform),
+      // so an Inf in x meets no zero weight (fma(0, Inf) would be NaN)
+      if (l0 + u >= nl) break;
+      const int xo = (l0 + u) * SPAN + lane * VE;
       float wa[VE], wb[VE];
       if constexpr (sizeof(T) == 4) {
 #pragma unroll
@@ -692,7 +694,9 @@ int gemv_t_run(const bn_view *x, const bn_view *w, const bn_view *y, int rope_co
     return fail(BN_ERR_UNSUPPORTED,
                 std::string(op) + ": an output-major w needs 16-byte aligned rows of x and w, k a "
                                   "multiple of 16 bytes, contiguous rows of y and an even output width");
-  if (m > GV_M || (int64_t)m * kp > GV_XMAX)
+  // the kernel stages mr rows (3 rows run the 4-row instance)
+  const int mr = m <= 1 ? 1 : (m <= 2 ? 2 : 4);
+  if (m > GV_M || (int64_t)mr * kp > GV_XMAX)
     return fail(BN_ERR_UNSUPPORTED, std::string(op) + ": an output-major w takes at most " +
                                         std::to_string(GV_M) + " rows of x and " +
                                         std::to_string(GV_XMAX) + " staged x elements");
@@ -728,7 +732,6 @@ int gemv_t_run(const bn_view *x, const bn_view *w, const bn_view *y, int rope_co
   if (nrm) {
     p.nd = nrm->d; p.nw = nrm->w; p.nh_out = nrm->h_out; p.neps = nrm->eps;
   }
-  const int mr = m <= 1 ? 1 : (m <= 2 ? 2 : 4);
   const size_t lds = (size_t)(nrm ? 2 : mr) * kp * sizeof(float);
   // four waves per workgroup, two weight rows (one output pair, or one
   // gate | up output) per wave

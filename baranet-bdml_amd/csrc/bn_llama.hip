@@ -137,6 +137,13 @@ int check_config(const bn_llama_config *c) {
                 std::string(op) + ": head_dim (hidden / n_heads) must be 64 and n_heads a multiple of n_kv_heads");
   if (c->hidden % 4 || c->intermediate % 4 || c->vocab % 4)
     return fail(BN_ERR_UNSUPPORTED, std::string(op) + ": hidden, intermediate and vocab must be multiples of 4");
+  // output-major projections stage their fp32 input row in LDS, padded to
+  // whole wave-wide loads (256 elements): refused here, before any launch,
+  // rather than by the first projection that cannot stage it
+  auto staged = [](int k) { return ((int64_t)k + 255) / 256 * 256; };
+  if (c->weights_out_major && (staged(c->hidden) > kGemvStagedMax || staged(c->intermediate) > kGemvStagedMax))
+    return fail(BN_ERR_UNSUPPORTED, std::string(op) + ": output-major weights take hidden and intermediate "
+                                                      "sizes of at most " + std::to_string(kGemvStagedMax));
   return BN_OK;
 }
 

@@ -114,14 +114,17 @@ class TinyLlama:
         # (callable (layer, first position of the rows) -> bool; None: all)
         self.trace_select = None
         self._where = (0, 0)
-        self.path_log = None  # list of (kind, launch) when set
+        # list of (kind, launch, algorithmic work) when set; work is bytes for
+        # the HBM-bound kinds and flops for prefill attention
+        self.path_log = None
 
     # ------------------------------------------------------------ path kernels
-    def _timed(self, fn, kind):
+    def _timed(self, fn, kind, work=0):
         """Runs a path-kernel launch; with path_log set (a list), also keeps
-        (kind, fn) so the launches can be replayed from a captured graph."""
+        (kind, fn, work) so the launches can be replayed from a captured graph
+        and priced against their roofline."""
         if self.path_log is not None:
-            self.path_log.append((kind, fn))
+            self.path_log.append((kind, fn, work))
         if not self.timing:
             return fn()
         s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -148,7 +151,7 @@ class TinyLlama:
         def run():
             bnhip.call("bn_rmsnorm", C.byref(bnhip.view(x)), C.byref(bnhip.view(weight)),
                        C.byref(bnhip.view(y)), self.cfg.rms_norm_eps, bnhip.stream_of())
-        self._timed(run, "rmsnorm")
+        self._timed(run, "rmsnorm", 4 * (2 * x.numel() + weight.numel()))  # x in, y out
         self._record("rmsnorm", [x, weight], y, eps=self.cfg.rms_norm_eps)
         return y
 
@@ -161,7 +164,7 @@ class TinyLlama:
             bnhip.call("bn_add_rmsnorm", C.byref(bnhip.view(hdn)), C.byref(bnhip.view(delta)),
                        C.byref(bnhip.view(weight)), C.byref(bnhip.view(hdn)), C.byref(bnhip.view(y)),
                        self.cfg.rms_norm_eps, bnhip.stream_of())
-        self._timed(run, "rmsnorm")
+        self._timed(run, "rmsnorm", 4 * (4 * hdn.numel() + weight.numel()))  # h, delta in; h, y out
         if self._tracing():
             self._record("add_rmsnorm", [before, delta, weight], torch.stack([hdn, y]),
                          eps=self.cfg.rms_norm_eps)
@@ -180,7 +183,7 @@ class TinyLlama:
         def run():
             bnhip.call("bn_rope", C.byref(bnhip.view(x)), C.byref(bnhip.view(x)), offset,
                        self.cfg.head_dim, self.cfg.rope_theta, bnhip.stream_of())
-        self._timed(run, "rope")
+        self._timed(run, "rope", 4 * 2 * x.numel())  # read and written in place
         self._record("rope", [before] if before is not None else [], x, offset=offset,
                      head_dim=self.cfg.head_dim, theta=self.cfg.rope_theta)
         return x
@@ -195,7 +198,8 @@ class TinyLlama:
                               head_dim=self.cfg.head_dim, theta=self.cfg.rope_theta,
                               workspace=self.lin_ws)
         if rope_cols:
-            self._timed(run, "qkv_rope")  # carries the RoPE of the step
+            # carries the RoPE of the step; work = the projection's bytes
+            self._timed(run, "qkv_rope", 4 * (x.numel() + w.numel() + y.numel()))
             self._record("linear_rope", [x, w], y, rope_cols=rope_cols, offset=pos0,
                          head_dim=self.cfg.head_dim, theta=self.cfg.rope_theta)
         else:
@@ -208,8 +212,10 @@ class TinyLlama:
         q4 = q.view(1, S, cfg.num_attention_heads, cfg.head_dim)
         k4 = k.view(1, S, cfg.num_key_value_heads, cfg.head_dim)
         v4 = v.view(1, S, cfg.num_key_value_heads, cfg.head_dim)
+        # causal QK^T and PV MACs x 2
+        flops = 4 * cfg.num_attention_heads * cfg.head_dim * S * (S + 1) // 2
         o = self._timed(lambda: bnhip.gqa_prefill(q4, k4, v4, scale=1.0 / math.sqrt(cfg.head_dim)),
-                        "attention")
+                        "prefill_attention", flops)
         self._record("prefill", [q4, k4, v4], o)
         return o.view(S, cfg.hidden_size)
 
@@ -219,7 +225,10 @@ class TinyLlama:
         lens = torch.tensor([length], dtype=torch.int32, device="cuda")
         o = self._timed(lambda: bnhip.gqa_decode(q3, layer["k_cache"], layer["v_cache"], lens,
                                                  scale=1.0 / math.sqrt(cfg.head_dim),
-                                                 workspace=self.ws), "attention")
+                                                 workspace=self.ws), "decode_attention",
+                        # fp32 K and V rows of the cached positions, q in, o out
+                        4 * (2 * length * cfg.num_key_value_heads * cfg.head_dim +
+                             2 * cfg.num_attention_heads * cfg.head_dim))
         self._record("decode", [q3, layer["k_cache"][:, :length], layer["v_cache"][:, :length]], o,
                      length=length)
         return o.view(1, cfg.hidden_size)

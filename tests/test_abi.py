@@ -271,6 +271,12 @@ def test_linear_rope_output_major_validation():
     assert s == B.BN_ERR_UNSUPPORTED  # stride between outputs not a multiple of 16 bytes
     s, m = st("bn_linear_rope", V(2, 16384), wt(16384, 64), V(2, 64), 0, 0, 64, 1e4, None, 0, None)
     assert s == B.BN_ERR_UNSUPPORTED and "staged x elements" in m
+    # three rows run the four-row instance: 4 x 4608 staged elements exceed the
+    # budget although 3 x 4608 would not; one and two rows of 4608 fit
+    s, m = st("bn_linear_rope", V(3, 4608), wt(4608, 64), V(3, 64), 0, 0, 64, 1e4, None, 0, None)
+    assert s == B.BN_ERR_UNSUPPORTED and "staged x elements" in m
+    s, m = st("bn_linear_rope", V(2, 4608), wt(4608, 64), V(2, 64), 0, 0, 64, 1e4, None, 0, None)
+    assert s == B.BN_ERR_NOT_DEVICE
     s, m = st("bn_linear_rope", V(4, 256), wt(256, 128), V(4, 128), 64, 3, 64, 1e4, None, 0, None)
     assert s == B.BN_ERR_NOT_DEVICE and m == "Linear: only GPU implementation available"
 
@@ -291,7 +297,7 @@ def test_linear_rope_workspace_size():
 
 def llama_cfg(**kw):
     d = dict(n_layers=22, hidden=2048, n_heads=32, n_kv_heads=4, intermediate=5632, vocab=32000,
-             max_len=640, rms_eps=1e-5, rope_theta=1e4)
+             max_len=640, rms_eps=1e-5, rope_theta=1e4, weights_out_major=0)
     d.update(kw)
     return B.BnLlamaConfig(*d.values())
 
@@ -318,6 +324,17 @@ def test_llama_decode_validation():
     assert s == B.BN_ERR_UNSUPPORTED and "multiples of 4" in m
     s, m = dec(llama_cfg(n_layers=0), 0, 0, 1)
     assert s == B.BN_ERR_SHAPE
+    # output-major weights stage each projection's input row (padded to 256
+    # fp32) in 64 KB of LDS: wider rows are refused before any launch, and
+    # the workspace query reports 0; row-major weights take them
+    wide_i = llama_cfg(intermediate=16388, weights_out_major=1)
+    assert L.bn_llama_decode_workspace_size(C.byref(wide_i)) == 0
+    s, m = dec(wide_i, 0, 0, 1)
+    assert s == B.BN_ERR_UNSUPPORTED and "output-major" in m
+    wide_h = llama_cfg(hidden=16640, n_heads=260, weights_out_major=1)
+    assert L.bn_llama_decode_workspace_size(C.byref(wide_h)) == 0
+    assert L.bn_llama_decode_workspace_size(C.byref(llama_cfg(intermediate=16384, weights_out_major=1))) > 0
+    assert L.bn_llama_decode_workspace_size(C.byref(llama_cfg(intermediate=16388))) > 0
     s, m = dec(c, 0, 600, 41)
     assert s == B.BN_ERR_SHAPE and "max_len" in m
     assert dec(c, 0, 600, 40)[0] != B.BN_ERR_SHAPE

@@ -179,6 +179,17 @@ def test_llama_model_cpp_signature_defaults():
         bten.LLaMAModelCpp(small_cfg(), False, "bogus")
 
 
+@pytest.mark.parametrize("field", ["num_hidden_layers", "vocab_size", "intermediate_size"])
+@pytest.mark.parametrize("value", [0, -1])
+def test_llama_model_cpp_refuses_empty_sizes(field, value):
+    """A model with no layers (or no vocabulary / MLP) is refused at
+    construction: its forward would index layer 0 of an empty stack."""
+    c = small_cfg()
+    setattr(c, field, value)
+    with pytest.raises(RuntimeError, match="must be positive"):
+        bten.LLaMAModelCpp(c, False)
+
+
 def test_bf16_host_tensor_rounds_to_nearest_even():
     vals = np.array([[1.0, 1.0 + 2 ** -8, 1.0 + 3 * 2 ** -8, -2.5, 3.14159265, 0.0]],
                     np.float32)

@@ -401,6 +401,23 @@ def test_linear_rope_output_major_weight(case, dtype):
         assert torch.equal(y1[0], y[1])
 
 
+def test_linear_rope_output_major_inf_in_last_span():
+    """k = 5632 fp32 is 22 wave-wide loads: the last round of 8 has two slots
+    past the row.  An Inf in the last span of x must give the reference's
+    +/-Inf (Inf * w summed with finite terms), not the NaN of a zero weight
+    met in a slot past the row."""
+    M, K, N = 1, 5632, 256
+    r = rng(64)
+    x = r.standard_normal((M, K)).astype(np.float32)
+    x[0, K - 1] = np.inf
+    wt = (r.standard_normal((N, K)) / np.sqrt(K)).astype(np.float32)
+    wt[:, K - 1] = np.where(wt[:, K - 1] >= 0, 0.5, -0.5)
+    y = host(B.linear_rope(dev(x), dev(wt).t(), rope_cols=0))
+    ref = O.linear_rope(x, np.ascontiguousarray(wt.T), 0, 0, 64, 1e4)
+    assert not np.isnan(ref).any() and np.isinf(ref).all()
+    np.testing.assert_array_equal(y, ref)
+
+
 def test_linear_rope_output_major_strided_and_limits():
     # w the transposed view of the first 320 rows and 256 columns of a wider
     # [400, 264] buffer (stride between outputs 264), y a column slice
