@@ -37,6 +37,7 @@ namespace {
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int BM = 128;  // query rows per workgroup
 constexpr int BN = 64;   // keys per LDS block
@@ -52,11 +53,11 @@ struct PrefillParams {
   float *lse;  // optional [batch, n_heads, seq_q]: natural-log row log-sum-exp of scale*s
 };
 
-// natural-log log-sum-exp of the row from its reference max (raw score
-// units) and the sum of exp2(s*c - m*c): log(sum exp(scale*s)) = (m*c +
-// log2(l)) * ln 2; -inf when no key is visible
-__device__ __forceinline__ float row_lse(float m, float l, float c) {
-  return l > 0.f ? (m * c + __log2f(l)) * 0.6931471805599453f : -INFINITY;
+// natural-log log-sum-exp of the row from its reference max times c (mc)
+// and the sum of exp2(s*c - mc): log(sum exp(scale*s)) = (mc + log2(l)) *
+// ln 2; -inf when no key is visible
+__device__ __forceinline__ float row_lse(float mc, float l) {
+  return l > 0.f ? (mc + __log2f(l)) * 0.6931471805599453f : -INFINITY;
 }
 
 struct Work {
@@ -218,6 +219,13 @@ constexpr int kOcc = 2;  // workgroups per CU the register budget is sized for
 // MFMA (re-swept on the head-packed kernel: 3-5 ahead, 4-6 after, 2/6; this
 // is best or tied on configs 2 and 5)
 constexpr int kSchedV0 = 4, kSchedV1 = 5;
+// Row sums of P on the matrix cores (v_mfma_f32_16x16x32_bf16 against a 0/1
+// selector) instead of a v_dot2 chain on the VALU; a tile's sum is checked
+// at the start of the next step, when the MFMA has long finished.
+#ifndef BN_PREFILL_RSM
+#define BN_PREFILL_RSM 1
+#endif
+constexpr bool kRsm = BN_PREFILL_RSM;
 
 template <int RT, int OCC, bool HP>
 __global__ __launch_bounds__(256, OCC) void prefill_bf16_kernel(PrefillParams p) {
@@ -302,18 +310,24 @@ __global__ __launch_bounds__(256, OCC) void prefill_bf16_kernel(PrefillParams p)
     *(u32x4_t *)(vs + (crow + 32) * VP16 + ccol) = v1;
   };
 
-  float m[RT], l[RT];  // reference max (raw score units), row-sum partial
-  float mcv[RT];       // m * c, kept with m (it moves only in the fixup)
+  float l[RT];    // row sum (kRsm: of the whole row; otherwise this half-wave's partial)
+  float mcv[RT];  // m * c: the reference max m (it moves only in the fixup) times c
   f32x16_t o[RT][2];
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
-    m[rt] = -INFINITY;
     mcv[rt] = -INFINITY;
     l[rt] = 0.f;
     o[rt][0] = f32x16_t{};
     o[rt][1] = f32x16_t{};
   }
   const bf16x2_t ones = {(__bf16)1.0f, (__bf16)1.0f};
+  // Row-sum selector, the A operand of v_mfma_f32_16x16x32_bf16 (lane l holds
+  // A[m = l%16][k = 8(l/16) .. +7]): A[m][k] = 1 where (m/4)%2 == (k/8)%2.
+  // B = this step's P^T registers (lane l: 8 keys of query l%32), so D row m
+  // sums the lanes whose query is the one D row m's lanes hold: every lane
+  // receives the row sum of its own query over both half-waves.
+  // (formed where it is used: four registers fewer across the loop)
+  const uint32_t rs_bits = (((lane & 15) >> 2) & 1) == ((lane >> 4) & 1) ? 0x3f803f80u : 0u;
   const int tr_off = (4 * hf + ((lane & 15) >> 2)) * VP16 + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
 
   // --- pieces of a step
@@ -354,9 +368,29 @@ __global__ __launch_bounds__(256, OCC) void prefill_bf16_kernel(PrefillParams p)
         for (int rt = 0; rt < RT; ++rt)
           o[rt][dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va[u][dt], pb[rt][u], o[rt][dt], 0, 0, 0);
   };
+  // p = exp2(s * c - mc) as bf16 MFMA operands (the row sum on the matrix cores)
+  auto exps_p = [&](const f32x16_t &s, float mc, bf16x8_t (&pb)[2]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) pb[u][j] = (__bf16)__builtin_amdgcn_exp2f(fmaf(s[8 * u + j], c, -mc));
+  };
+  // the row sum of a tile's bf16 P over both half-waves (D[0] once the MFMAs finish)
+  auto rowsum = [&](const bf16x8_t (&pb)[2]) __attribute__((always_inline)) {
+    uint32_t b = rs_bits;
+    asm volatile("" : "+v"(b));  // keeps the selector from being hoisted out of the loop
+    const bf16x8_t rs_sel = __builtin_bit_cast(bf16x8_t, u32x4_t{b, b, b, b});
+    f32x4_t d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(rs_sel, pb[0], f32x4_t{}, 0, 0, 0);
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(rs_sel, pb[1], d, 0, 0, 0);
+  };
   // p = exp2(s * c - mc) as bf16 MFMA operands and the row sum of those bf16 values
   auto exps = [&](const f32x16_t &s, float mc, bf16x8_t (&pb)[2], float &rs)
       __attribute__((always_inline)) {
+    if constexpr (kRsm) {
+      exps_p(s, mc, pb);
+      rs = rowsum(pb)[0];
+      return;
+    }
     // one chain of eight dot2s, the first from an inline zero (no register
     // to clear, no second chain to add)
     float r = 0.f;
@@ -392,19 +426,20 @@ __global__ __launch_bounds__(256, OCC) void prefill_bf16_kernel(PrefillParams p)
 #pragma unroll
     for (int i = 1; i < 16; ++i) mx = fmaxf(mx, s[i]);
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float m_true = fmaxf(m[rt], mx);  // -inf while nothing is visible
-    const bool move = m[rt] == -INFINITY || (m_true - m[rt]) * c > kRescaleLog2;
-    const float m_new = move ? m_true : m[rt];
+    // in units of m*c: the true running max, moved to only when it grew by
+    // more than 2^8 in probability (or nothing was visible yet)
+    const float mt = fmaxf(mcv[rt], mx * c);  // -inf while nothing is visible
+    const bool move = mcv[rt] == -INFINITY || mt - mcv[rt] > kRescaleLog2;
+    const float m_new = move ? mt : mcv[rt];
     const float mn = m_new == -INFINITY ? 0.f : m_new;
-    const float alpha = __builtin_amdgcn_exp2f((m[rt] - mn) * c);  // m = -inf -> 0
+    const float alpha = __builtin_amdgcn_exp2f(mcv[rt] - mn);  // m = -inf -> 0
     l[rt] *= alpha;
 #pragma unroll
     for (int dt = 0; dt < 2; ++dt)
 #pragma unroll
       for (int i = 0; i < 16; ++i) o[rt][dt][i] *= alpha;
-    m[rt] = m_new;
-    mcv[rt] = m_new * c;
-    exps(s, mn * c, pb, rs);
+    mcv[rt] = m_new;
+    exps(s, mn, pb, rs);
   };
   // bad: this lane's row sum is above the limit or NaN; one ballot, no
   // bool materialised per lane
@@ -457,8 +492,58 @@ __global__ __launch_bounds__(256, OCC) void prefill_bf16_kernel(PrefillParams p)
     finish(bad, sc, pc, rs);
   };
 
+  // Row sums on the matrix cores: step t first settles tile t-1 -- its row
+  // sum (rsp, from the MFMAs at the end of step t-1) is checked and, when a p
+  // passed the limit (or is NaN), tile t-1 runs the fixup on its raw scores,
+  // which are still in sn (not yet overwritten by tile t+1's scores), before
+  // its P V; then the step's products, tile t's softmax into pc, and tile t's
+  // row-sum MFMAs into rsc.  The softmax of the last step a wave runs is a
+  // tile past its range (P = 0), so every real tile is settled.
+  auto step_rsm = [&](auto masked_tag, int t, const bf16_t *vs, const bf16_t *ks, f32x16_t (&sc)[RT],
+                      f32x16_t (&sn)[RT], bf16x8_t (&pp)[RT][2], bf16x8_t (&pc)[RT][2],
+                      float (&rsp)[RT], float (&rsc)[RT]) __attribute__((always_inline)) {
+    constexpr bool MASKED = decltype(masked_tag)::value;
+    {
+      bool bad = false;
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) bad = bad || !(rsp[rt] <= kSumLimit);
+      if (__builtin_amdgcn_ballot_w64(bad) != 0) {
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) fixup(rt, sn[rt], pp[rt], rsp[rt]);
+      }
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) l[rt] += rsp[rt];
+    }
+    if (!MASKED) {
+    } else if (t >= ntw) {
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) sc[rt][i] = -INFINITY;
+    } else {
+      mask(t, sc);
+    }
+    bf16x8_t va[2][2], ka[4];
+    vfrags(vs, va);
+    kfrags(ks, ka);
+    pv(va, pp);
+    scores(ka, sn);
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) exps_p(sc[rt], mcv[rt], pc[rt]);
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) rsc[rt] = rowsum(pc[rt])[0];
+    __builtin_amdgcn_sched_group_barrier(0x100, 12, 0);
+    __builtin_amdgcn_sched_group_barrier(0x002, kSchedV0, 0);
+#pragma unroll
+    for (int i = 0; i < 10 * RT; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, kSchedV1 - 1, 0);
+    }
+  };
+
   f32x16_t sa[RT], sb[RT];
   bf16x8_t pa[RT][2], pbb[RT][2];
+  float rsa[RT], rsb[RT];  // row sums of the tiles in pa / pbb (kRsm)
   if (nblk > 0) {
     gload_k(0);
     gload_v(0);
@@ -484,7 +569,10 @@ __global__ __launch_bounds__(256, OCC) void prefill_bf16_kernel(PrefillParams p)
     for (int rt = 0; rt < RT; ++rt) {
       float rs;
       fixup(rt, sa[rt], pa[rt], rs);
-      l[rt] += rs;
+      if constexpr (kRsm)
+        rsa[rt] = rs;  // settled by step 1
+      else
+        l[rt] += rs;
     }
   }
   // iteration 0 stores K_2 into K_0's buffer, which step 0 reads: every wave
@@ -505,9 +593,15 @@ __global__ __launch_bounds__(256, OCC) void prefill_bf16_kernel(PrefillParams p)
     // ntw still adds P V of its last tile); the others' barriers and staging
     // go on, and the SIMD's other waves get the issue slots
     constexpr bool MASKED = decltype(masked_tag)::value;
-    if (!MASKED || 2 * j + 1 <= ntw) step(masked_tag, 2 * j + 1, vc, kn, sb, sa, pa, pbb);
-    if (!MASKED || 2 * j + 2 <= ntw)
-      step(masked_tag, 2 * j + 2, vc + 32 * VP16, kn + 32 * KP16, sa, sb, pbb, pa);
+    if constexpr (kRsm) {
+      if (!MASKED || 2 * j + 1 <= ntw) step_rsm(masked_tag, 2 * j + 1, vc, kn, sb, sa, pa, pbb, rsa, rsb);
+      if (!MASKED || 2 * j + 2 <= ntw)
+        step_rsm(masked_tag, 2 * j + 2, vc + 32 * VP16, kn + 32 * KP16, sa, sb, pbb, pa, rsb, rsa);
+    } else {
+      if (!MASKED || 2 * j + 1 <= ntw) step(masked_tag, 2 * j + 1, vc, kn, sb, sa, pa, pbb);
+      if (!MASKED || 2 * j + 2 <= ntw)
+        step(masked_tag, 2 * j + 2, vc + 32 * VP16, kn + 32 * KP16, sa, sb, pbb, pa);
+    }
     lstore_k(j & 1);        // K_{j+2} into K_j's buffer (K_j last read in iteration j-1)
     lstore_v((j + 1) & 1);  // V_{j+1} into V_{j-1}'s buffer
     gload_k(j + 3);         // rows past seq_kv read as 0
@@ -521,10 +615,12 @@ __global__ __launch_bounds__(256, OCC) void prefill_bf16_kernel(PrefillParams p)
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
     const int qrow = q_wave0 + row_step * rt + r32;
-    const float lt = l[rt] + __shfl_xor(l[rt], 32, 64);
+    // kRsm: each lane's l is the whole row's; otherwise the two half-waves'
+    // partials are added
+    const float lt = kRsm ? l[rt] : l[rt] + __shfl_xor(l[rt], 32, 64);
     const float inv = lt > 0.f ? 1.0f / lt : 0.f;  // no visible key -> zeros
     if (p.lse && hf == 0 && qrow < p.seq_q)
-      p.lse[((int64_t)w.b * p.n_heads + w.h + head_of(rt)) * p.seq_q + qrow] = row_lse(m[rt], lt, c);
+      p.lse[((int64_t)w.b * p.n_heads + w.h + head_of(rt)) * p.seq_q + qrow] = row_lse(mcv[rt], lt);
     if (qrow < p.seq_q) {
       bf16_t *orow = O + (int64_t)head_of(rt) * HD + (int64_t)qrow * p.o_rs;
 #pragma unroll
@@ -669,7 +765,7 @@ __global__ __launch_bounds__(256, 2) void prefill_f32_kernel(PrefillParams p) {
   const float lt = l + __shfl_xor(l, 32, 64);
   const float inv = lt > 0.f ? 1.0f / lt : 0.f;
   if (p.lse && hf == 0 && row_ok)
-    p.lse[((int64_t)w.b * p.n_heads + w.h) * p.seq_q + qrow] = row_lse(m, lt, p.c);
+    p.lse[((int64_t)w.b * p.n_heads + w.h) * p.seq_q + qrow] = row_lse(m * p.c, lt);
   if (row_ok) {
     float *orow = O + (int64_t)qrow * p.o_rs;
 #pragma unroll
