@@ -197,7 +197,11 @@ __device__ __forceinline__ Work decode_work_packed(const PrefillParams &p) {
 // while the matrix cores work:
 //   * the fast path is p = exp2(s * c - m * c), c = scale*log2(e), against a
 //     reference max m that is NOT recomputed per tile: one fma, one
-//     transcendental, half a bf16 pack and half a dot2 (row sum) per score;
+//     transcendental and half a bf16 pack per score; the tile's row sums run
+//     on the matrix cores (v_mfma_f32_16x16x32_bf16 against a 0/1 selector),
+//     checked at the start of the next step, when those MFMAs have long
+//     finished (measured against a v_dot2 chain on the VALU: +3.5% on
+//     config 2, +2.5% on config 5);
 //   * m moves only in a rare exact fixup, taken when a tile's row sum exceeds
 //     2^16 (some p > 2^16, which includes inf and NaN), and then only when it
 //     grew by more than 2^8; the first tile (m = -inf) runs the fixup alone;
@@ -216,16 +220,10 @@ __device__ __forceinline__ Work decode_work_packed(const PrefillParams &p) {
 constexpr float kSumLimit = 65536.f;
 constexpr int kOcc = 2;  // workgroups per CU the register budget is sized for
 // step interleave: VALU instructions ahead of the first MFMA, then after each
-// MFMA (re-swept on the head-packed kernel: 3-5 ahead, 4-6 after, 2/6; this
-// is best or tied on configs 2 and 5)
-constexpr int kSchedV0 = 4, kSchedV1 = 5;
-// Row sums of P on the matrix cores (v_mfma_f32_16x16x32_bf16 against a 0/1
-// selector) instead of a v_dot2 chain on the VALU; a tile's sum is checked
-// at the start of the next step, when the MFMA has long finished.
-#ifndef BN_PREFILL_RSM
-#define BN_PREFILL_RSM 1
-#endif
-constexpr bool kRsm = BN_PREFILL_RSM;
+// MFMA (4 after each of the 20 MFMAs of a step with the row sums on the
+// matrix cores; 2 or 6 ahead, and 5 after the 16 products with 2 after the
+// row sums, measured equal or slower on configs 2 and 5)
+constexpr int kSchedV0 = 4, kSchedV1 = 4;
 
 template <int RT, int OCC, bool HP>
 __global__ __launch_bounds__(256, OCC) void prefill_bf16_kernel(PrefillParams p) {
@@ -310,7 +308,7 @@ __global__ __launch_bounds__(256, OCC) void prefill_bf16_kernel(PrefillParams p)
     *(u32x4_t *)(vs + (crow + 32) * VP16 + ccol) = v1;
   };
 
-  float l[RT];    // row sum (kRsm: of the whole row; otherwise this half-wave's partial)
+  float l[RT];    // row sum over both half-waves
   float mcv[RT];  // m * c: the reference max m (it moves only in the fixup) times c
   f32x16_t o[RT][2];
 #pragma unroll
@@ -320,7 +318,6 @@ __global__ __launch_bounds__(256, OCC) void prefill_bf16_kernel(PrefillParams p)
     o[rt][0] = f32x16_t{};
     o[rt][1] = f32x16_t{};
   }
-  const bf16x2_t ones = {(__bf16)1.0f, (__bf16)1.0f};
   // Row-sum selector, the A operand of v_mfma_f32_16x16x32_bf16 (lane l holds
   // A[m = l%16][k = 8(l/16) .. +7]): A[m][k] = 1 where (m/4)%2 == (k/8)%2.
   // B = this step's P^T registers (lane l: 8 keys of query l%32), so D row m
@@ -383,26 +380,12 @@ __global__ __launch_bounds__(256, OCC) void prefill_bf16_kernel(PrefillParams p)
     f32x4_t d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(rs_sel, pb[0], f32x4_t{}, 0, 0, 0);
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(rs_sel, pb[1], d, 0, 0, 0);
   };
-  // p = exp2(s * c - mc) as bf16 MFMA operands and the row sum of those bf16 values
+  // p = exp2(s * c - mc) and the tile's row sum over both half-waves, read
+  // as soon as its MFMAs finish (the fixup's exact path)
   auto exps = [&](const f32x16_t &s, float mc, bf16x8_t (&pb)[2], float &rs)
       __attribute__((always_inline)) {
-    if constexpr (kRsm) {
-      exps_p(s, mc, pb);
-      rs = rowsum(pb)[0];
-      return;
-    }
-    // one chain of eight dot2s, the first from an inline zero (no register
-    // to clear, no second chain to add)
-    float r = 0.f;
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) pb[u][j] = (__bf16)__builtin_amdgcn_exp2f(fmaf(s[8 * u + j], c, -mc));
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        r = __builtin_amdgcn_fdot2_f32_bf16(bf16x2_t{pb[u][2 * j], pb[u][2 * j + 1]}, ones, r, false);
-    }
-    rs = r;
+    exps_p(s, mc, pb);
+    rs = rowsum(pb)[0];
   };
   // causal / tail mask of tile t (keys kb..kb+31) in place
   auto mask = [&](int t, f32x16_t (&sc)[RT]) __attribute__((always_inline)) {
@@ -441,57 +424,6 @@ __global__ __launch_bounds__(256, OCC) void prefill_bf16_kernel(PrefillParams p)
     mcv[rt] = m_new;
     exps(s, mn, pb, rs);
   };
-  // bad: this lane's row sum is above the limit or NaN; one ballot, no
-  // bool materialised per lane
-  auto finish = [&](bool bad, const f32x16_t (&sc)[RT], bf16x8_t (&pb)[RT][2], float (&rs)[RT])
-      __attribute__((always_inline)) {
-    if (__builtin_amdgcn_ballot_w64(bad) != 0) {
-#pragma unroll
-      for (int rt = 0; rt < RT; ++rt) fixup(rt, sc[rt], pb[rt], rs[rt]);
-    }
-#pragma unroll
-    for (int rt = 0; rt < RT; ++rt) l[rt] += rs[rt];
-  };
-
-  // step t (1 <= t): O += V_{t-1}^T P_{t-1} (V rows vs), scores of tile t+1
-  // (K rows ks) into sn, softmax of tile t (sc) into pc, all in one basic
-  // block.  Tiles past the wave's causal range are all -inf: P = 0.
-  auto step = [&](auto masked_tag, int t, const bf16_t *vs, const bf16_t *ks, f32x16_t (&sc)[RT],
-                  f32x16_t (&sn)[RT], const bf16x8_t (&pp)[RT][2], bf16x8_t (&pc)[RT][2])
-      __attribute__((always_inline)) {
-    constexpr bool MASKED = decltype(masked_tag)::value;
-    if (!MASKED) {
-    } else if (t >= ntw) {
-#pragma unroll
-      for (int rt = 0; rt < RT; ++rt)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) sc[rt][i] = -INFINITY;
-    } else {
-      mask(t, sc);
-    }
-    bf16x8_t va[2][2], ka[4];
-    vfrags(vs, va);
-    kfrags(ks, ka);
-    pv(va, pp);
-    scores(ka, sn);
-    float rs[RT];
-    bool bad = false;
-#pragma unroll
-    for (int rt = 0; rt < RT; ++rt) {
-      exps(sc[rt], mcv[rt], pc[rt], rs[rt]);  // m = -inf: inf/NaN -> fixup
-      bad = bad || !(rs[rt] <= kSumLimit);
-    }
-    // LDS reads first, then one MFMA every few VALU instructions
-    __builtin_amdgcn_sched_group_barrier(0x100, 12, 0);
-    __builtin_amdgcn_sched_group_barrier(0x002, kSchedV0, 0);
-#pragma unroll
-    for (int i = 0; i < 8 * RT; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x002, kSchedV1, 0);
-    }
-    finish(bad, sc, pc, rs);
-  };
-
   // Row sums on the matrix cores: step t first settles tile t-1 -- its row
   // sum (rsp, from the MFMAs at the end of step t-1) is checked and, when a p
   // passed the limit (or is NaN), tile t-1 runs the fixup on its raw scores,
@@ -499,7 +431,7 @@ __global__ __launch_bounds__(256, OCC) void prefill_bf16_kernel(PrefillParams p)
   // its P V; then the step's products, tile t's softmax into pc, and tile t's
   // row-sum MFMAs into rsc.  The softmax of the last step a wave runs is a
   // tile past its range (P = 0), so every real tile is settled.
-  auto step_rsm = [&](auto masked_tag, int t, const bf16_t *vs, const bf16_t *ks, f32x16_t (&sc)[RT],
+  auto step = [&](auto masked_tag, int t, const bf16_t *vs, const bf16_t *ks, f32x16_t (&sc)[RT],
                       f32x16_t (&sn)[RT], bf16x8_t (&pp)[RT][2], bf16x8_t (&pc)[RT][2],
                       float (&rsp)[RT], float (&rsc)[RT]) __attribute__((always_inline)) {
     constexpr bool MASKED = decltype(masked_tag)::value;
@@ -537,13 +469,13 @@ __global__ __launch_bounds__(256, OCC) void prefill_bf16_kernel(PrefillParams p)
 #pragma unroll
     for (int i = 0; i < 10 * RT; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x002, kSchedV1 - 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, kSchedV1, 0);
     }
   };
 
   f32x16_t sa[RT], sb[RT];
   bf16x8_t pa[RT][2], pbb[RT][2];
-  float rsa[RT], rsb[RT];  // row sums of the tiles in pa / pbb (kRsm)
+  float rsa[RT], rsb[RT];  // row sums of the tiles in pa / pbb
   if (nblk > 0) {
     gload_k(0);
     gload_v(0);
@@ -569,10 +501,7 @@ __global__ __launch_bounds__(256, OCC) void prefill_bf16_kernel(PrefillParams p)
     for (int rt = 0; rt < RT; ++rt) {
       float rs;
       fixup(rt, sa[rt], pa[rt], rs);
-      if constexpr (kRsm)
-        rsa[rt] = rs;  // settled by step 1
-      else
-        l[rt] += rs;
+      rsa[rt] = rs;  // settled by step 1
     }
   }
   // iteration 0 stores K_2 into K_0's buffer, which step 0 reads: every wave
@@ -593,15 +522,9 @@ __global__ __launch_bounds__(256, OCC) void prefill_bf16_kernel(PrefillParams p)
     // ntw still adds P V of its last tile); the others' barriers and staging
     // go on, and the SIMD's other waves get the issue slots
     constexpr bool MASKED = decltype(masked_tag)::value;
-    if constexpr (kRsm) {
-      if (!MASKED || 2 * j + 1 <= ntw) step_rsm(masked_tag, 2 * j + 1, vc, kn, sb, sa, pa, pbb, rsa, rsb);
-      if (!MASKED || 2 * j + 2 <= ntw)
-        step_rsm(masked_tag, 2 * j + 2, vc + 32 * VP16, kn + 32 * KP16, sa, sb, pbb, pa, rsb, rsa);
-    } else {
-      if (!MASKED || 2 * j + 1 <= ntw) step(masked_tag, 2 * j + 1, vc, kn, sb, sa, pa, pbb);
-      if (!MASKED || 2 * j + 2 <= ntw)
-        step(masked_tag, 2 * j + 2, vc + 32 * VP16, kn + 32 * KP16, sa, sb, pbb, pa);
-    }
+    if (!MASKED || 2 * j + 1 <= ntw) step(masked_tag, 2 * j + 1, vc, kn, sb, sa, pa, pbb, rsa, rsb);
+    if (!MASKED || 2 * j + 2 <= ntw)
+      step(masked_tag, 2 * j + 2, vc + 32 * VP16, kn + 32 * KP16, sa, sb, pbb, pa, rsb, rsa);
     lstore_k(j & 1);        // K_{j+2} into K_j's buffer (K_j last read in iteration j-1)
     lstore_v((j + 1) & 1);  // V_{j+1} into V_{j-1}'s buffer
     gload_k(j + 3);         // rows past seq_kv read as 0
@@ -615,9 +538,7 @@ __global__ __launch_bounds__(256, OCC) void prefill_bf16_kernel(PrefillParams p)
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
     const int qrow = q_wave0 + row_step * rt + r32;
-    // kRsm: each lane's l is the whole row's; otherwise the two half-waves'
-    // partials are added
-    const float lt = kRsm ? l[rt] : l[rt] + __shfl_xor(l[rt], 32, 64);
+    const float lt = l[rt];  // the whole row's (both half-waves)
     const float inv = lt > 0.f ? 1.0f / lt : 0.f;  // no visible key -> zeros
     if (p.lse && hf == 0 && qrow < p.seq_q)
       p.lse[((int64_t)w.b * p.n_heads + w.h + head_of(rt)) * p.seq_q + qrow] = row_lse(mcv[rt], lt);

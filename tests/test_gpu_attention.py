@@ -140,6 +140,49 @@ def test_prefill_zero_query_prefix_means():
     assert_close(got, ref, FP32_TOL, "prefix means")
 
 
+@pytest.mark.parametrize("shape", [(4, 2048, 2048, 32, 4, 0), (2, 4100, 4160, 32, 4, 60),
+                                   (1, 16384, 16384, 16, 2, 0)])
+def test_prefill_bf16_every_row_prefix_means(shape):
+    """Q = 0 in bf16 at config 2's shape, a ragged one with an offset and a
+    long one with two KV heads: every output row of every head is the mean of
+    the V rows it sees (query i sees keys 0 .. i + offset), so a row tile
+    computed twice, skipped or given the wrong keys shows (the output starts
+    as NaN)."""
+    Bn, Sq, Skv, H, Hkv, off = shape
+    v = bf16_round(np.random.default_rng(21).standard_normal((Bn, Skv, Hkv, 64)).astype(np.float32))
+    k = bf16_round(np.random.default_rng(22).standard_normal((Bn, Skv, Hkv, 64)).astype(np.float32))
+    q = torch.zeros((Bn, Sq, H, 64), device="cuda", dtype=torch.bfloat16)
+    o = torch.full((Bn, Sq, H, 64), float("nan"), device="cuda", dtype=torch.bfloat16)
+    B.gqa_prefill(q, dev(k, torch.bfloat16), dev(v, torch.bfloat16), o, scale=0.125, seq_offset=off)
+    got = host(o)
+    csum = np.cumsum(v.astype(np.float64), axis=1)
+    last = np.minimum(np.arange(Sq) + off, Skv - 1)
+    means = csum[:, last] / (last + 1)[None, :, None, None]
+    ref = np.repeat(means, H // Hkv, axis=2)
+    assert np.all(np.isfinite(got))
+    assert_close(got, ref, BF16_TOL, f"bf16 prefix means {shape}")
+
+
+def test_prefill_bf16_long_offset_shape_vs_oracle():
+    """B=2, Sq=4100 (a ragged last row tile), Skv=4160, offset 60, 32/4 heads
+    (1032 head-packed row tiles): whole heads against the oracle, and a second
+    call on the same buffers gives the same bits."""
+    Bn, Sq, Skv, H, Hkv, off = 2, 4100, 4160, 32, 4, 60
+    q = draw((Bn, Sq, H, 64), 31, "bf16")
+    k = draw((Bn, Skv, Hkv, 64), 32, "bf16")
+    v = draw((Bn, Skv, Hkv, 64), 33, "bf16")
+    qd, kd, vd = dev(q, torch.bfloat16), dev(k, torch.bfloat16), dev(v, torch.bfloat16)
+    o1 = B.gqa_prefill(qd, kd, vd, scale=0.125, seq_offset=off)
+    o2 = B.gqa_prefill(qd, kd, vd, scale=0.125, seq_offset=off)
+    assert torch.equal(o1, o2)
+    got = host(o1)
+    for b, h in [(0, 5), (1, 30)]:
+        g = h // 8
+        ref = O.gqa_prefill(q[b:b + 1, :, h:h + 1], k[b:b + 1, :, g:g + 1], v[b:b + 1, :, g:g + 1],
+                            0.125, True, off)
+        assert_close(got[b:b + 1, :, h:h + 1], ref, BF16_TOL, f"b={b} h={h}")
+
+
 # ------------------------------------------------------------------- decode
 DECODE_CASES = [
     # B, Lmax, H, Hkv, lens
