@@ -111,6 +111,8 @@ def lib():
         "bn_gqa_decode_workspace_size": ([i, i, i, i], sz),
         "bn_gqa_decode": ([i, vp, vp, vp, vp, vp] + [i] * 5 + [f, vp, sz, vp], i),
         "bn_gqa_decode_noalloc": ([i, vp, vp, vp, vp, vp] + [i] * 5 + [f, vp], i),
+        "bn_gqa_decode_planned_workspace_size": ([i, i, i, i, i], sz),
+        "bn_gqa_decode_planned": ([i, vp, vp, vp, vp, vp, vp] + [i] * 5 + [f, vp, sz, vp], i),
     }
     for name, (args, res) in sig.items():
         fn = getattr(L, name)
@@ -271,6 +273,28 @@ def gqa_decode(q, k_cache, v_cache, seq_lens, o=None, scale=None, workspace=None
     call("bn_gqa_decode", _torch_dtype_code(q), q.data_ptr(), k_cache.data_ptr(),
          v_cache.data_ptr(), seq_lens.data_ptr(), o.data_ptr(), B, Lmax, H, Hkv, D, sc,
          ws_ptr, ws_bytes, stream_of(stream))
+    return o
+
+
+def gqa_decode_planned(q, k_cache, v_cache, seq_lens, h_seq_lens, o=None, scale=None,
+                       workspace=None, stream=None):
+    """gqa_decode with the lengths also on the host (h_seq_lens: a sequence of
+    ints, the values of the device tensor seq_lens): equal shares of the
+    batch's tiles per compute unit when the lengths are ragged."""
+    import numpy as np
+    import torch
+    B, H, D = q.shape
+    _, Lmax, Hkv, _ = k_cache.shape
+    if o is None:
+        o = torch.empty_like(q)
+    sc = 1.0 / math.sqrt(D) if scale is None else scale
+    hl = np.ascontiguousarray(np.asarray(h_seq_lens, dtype=np.int32))
+    assert hl.shape == (B,)
+    ws_ptr, ws_bytes = (None, 0) if workspace is None else (workspace.data_ptr(),
+                                                            workspace.numel() * workspace.element_size())
+    call("bn_gqa_decode_planned", _torch_dtype_code(q), q.data_ptr(), k_cache.data_ptr(),
+         v_cache.data_ptr(), seq_lens.data_ptr(), hl.ctypes.data, o.data_ptr(), B, Lmax, H, Hkv, D,
+         sc, ws_ptr, ws_bytes, stream_of(stream))
     return o
 
 

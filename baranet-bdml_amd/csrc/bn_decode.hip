@@ -22,7 +22,10 @@
 //     across chunks by a small combine kernel over (m, l, acc) partials.
 // Scores live in the log2 domain: s = (q.k) * scale*log2(e), p = exp2(s - m).
 
+#include <algorithm>
+#include <atomic>
 #include <mutex>
+#include <vector>
 
 #include "bn_common.hpp"
 
@@ -31,6 +34,12 @@
 // to a kernel (on the host the name is only a stand-in); it uses the device
 // address hipGetSymbolAddress returns for the current device.
 static __device__ __align__(256) float scratch[BN_GQA_DECODE_SCRATCH_BYTES / sizeof(float)];
+
+// Per-unit part counters of bn_gqa_decode_planned: slots of 256 counters,
+// zero at load time; each launch takes the next slot of a host-side ring and
+// every cut unit's last part clears its counter, so a slot is zero again when
+// its turn comes round (launches share a slot only when 16 are in flight).
+static __device__ __align__(256) uint32_t plan_counters[16 * 256];
 
 // bf16 K/V cache loads are non-temporal (streamed once, kept out of L2/MALL):
 // +24% on config 3 against plain loads.
@@ -831,6 +840,346 @@ __global__ __launch_bounds__(64 * WWV) void decode_bf16_whole_kernel(DecodeParam
   }
 }
 
+// Planned ragged decode (bn_gqa_decode_planned): the lengths are known on
+// the host, which deals the batch's 32-key tiles -- units (sequence, KV head)
+// in order -- into equal contiguous shares, one per workgroup and compute
+// unit, so that every compute unit streams the same number of bytes and a
+// long cache is cut across neighbouring workgroups instead of one compute
+// unit streaming it alone after the others have finished.  A workgroup's
+// share touches a few units (segments); its waves take the share's tiles in
+// turn (tile i -> wave i % 4, the loads running on across segment
+// boundaries), keep one (m, l, acc) per segment, and merge them through LDS
+// at the end.  A unit lying wholly in the share is written directly; a cut
+// unit's part writes an (m, l, acc) record, and the last of its parts to
+// arrive (a per-unit counter, agent-scope release / acquire) merges the
+// records and writes the output -- in the same launch.
+constexpr int kPlanBins = 256;   // workgroups of a planned launch, at most
+constexpr int kPlanUnits = 256;  // (sequence, KV head) units, at most
+constexpr int kPlanSeg = 8;      // units one share may touch, at most
+constexpr int kPlanSlots = 16;   // counter slots (plan_counters): planned launches in flight
+
+static_assert(kPlanSlots * kPlanUnits == 16 * 256, "plan_counters holds kPlanSlots slots of kPlanUnits");
+
+struct PlanParams {
+  const void *q, *k, *v;
+  void *o;
+  float *rec;     // part records [record][G][HD + 2]: m (log2 units), l, acc
+  uint32_t *cnt;  // this launch's per-unit counters: zero at launch, cleared by each unit's last part
+  int batch, max_len, n_heads, n_kv_heads, n_units, share, total;  // share: sequence tiles per group
+  float c;                         // scale * log2(e)
+  uint32_t wg_start[kPlanBins];    // group: first sequence (bits 0..15), its first tile (16..31)
+  uint32_t unit[kPlanUnits];       // record base (0..11), first group (12..23), parts (24..31)
+  int32_t len[kPlanUnits];         // per sequence: length, clamped to [0, max_len]
+};
+
+template <int G>
+__global__ __launch_bounds__(64 * WWV) void decode_bf16_planned_kernel(PlanParams p) {
+  __shared__ __attribute__((aligned(16))) bf16_t KT[WWV][TK * WKP];
+  __shared__ __attribute__((aligned(16))) bf16_t VT[WWV][TK * WKP];
+  __shared__ float red_m[kPlanSeg][WWV][G], red_l[kPlanSeg][WWV][G];
+  __shared__ float red_o[kPlanSeg][WWV][G][HD];
+  __shared__ int s_last;
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l16 = lane & 15, grp = lane >> 4;
+  const int bin = blockIdx.x, Hkv = p.n_kv_heads;
+  // workgroups come in groups of Hkv, one per KV head, that walk the same
+  // share of the batch's sequences together (consecutive ids: dispatched at
+  // the same time), so the KV heads' slices of a cache row are read close in
+  // time, as in the whole-cache kernel
+  const int grp_id = bin / Hkv, gh = bin - grp_id * Hkv;
+  const int64_t kv_rs = (int64_t)Hkv * HD;
+  auto tiles_of = [&](int b) { return (p.len[b] + TK - 1) / TK; };
+
+  // units with no key at all: zeros, each written by workgroup u % gridDim.x
+  for (int u = bin; u < p.n_units; u += gridDim.x) {
+    if (p.len[u / Hkv] == 0) {
+      bf16_t *out = (bf16_t *)p.o + ((int64_t)(u / Hkv) * p.n_heads + (int64_t)(u % Hkv) * G) * HD;
+      for (int idx = tid; idx < G * HD; idx += 64 * WWV) out[idx] = f32_to_bf16(0.f);
+    }
+  }
+  // This group's share [grp_id * share, +ntile) of the batch's sequence
+  // tiles, as segments (one sequence each, sequences with keys in order) of
+  // this workgroup's KV head.  Every wave walks them itself in scalar
+  // registers -- no table, no barrier before the first loads -- forward only,
+  // since a wave's tiles increase.
+  const int ntile = min(p.share, p.total - grp_id * p.share);
+  struct Seg {
+    int s, b, end, kb0, len;  // sequence b; keys of local tile i: kb0 + 32 * i
+    const bf16_t *kr, *vr;
+  };
+  auto seg_set = [&](Seg &x, int b, int lb, int t) __attribute__((always_inline)) {
+    const int g = gh;
+    x.b = b;
+    x.len = p.len[b];
+    x.end = min(ntile, lb + (x.len + TK - 1) / TK - t);
+    x.kb0 = TK * (t - lb);
+    x.kr = (const bf16_t *)p.k + (int64_t)b * p.max_len * kv_rs + (int64_t)g * HD;
+    x.vr = (const bf16_t *)p.v + (int64_t)b * p.max_len * kv_rs + (int64_t)g * HD;
+  };
+  auto seg_first = [&](Seg &x) __attribute__((always_inline)) {
+    x.s = 0;
+    seg_set(x, (int)(p.wg_start[grp_id] & 0xffffu), 0, (int)(p.wg_start[grp_id] >> 16));
+  };
+  auto seg_next = [&](Seg &x) __attribute__((always_inline)) {
+    int b = x.b + 1;
+    while (b + 1 < p.batch && tiles_of(b) == 0) ++b;  // sequences without keys hold no tile
+    ++x.s;
+    seg_set(x, b, x.end, 0);
+  };
+  auto seg_adv = [&](Seg &x, int i) __attribute__((always_inline)) {
+    while (i >= x.end && x.end < ntile) seg_next(x);
+  };
+  int nseg = 0;
+  if (ntile > 0) {
+    Seg x;
+    seg_first(x);
+    while (x.end < ntile && x.s + 1 < kPlanSeg) seg_next(x);
+    nseg = x.s + 1;
+  }
+
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  struct RegTile {
+    u32x4 k0, k1, k2, k3, v0, v1, v2, v3;
+  };
+  const int crow = lane >> 3, ccol = (lane & 7) * 8;
+  auto gload = [&](RegTile &r, int i, const Seg &x) __attribute__((always_inline)) {
+    const int kb = x.kb0 + TK * i, kw1 = x.len;
+    const bf16_t *Kr = x.kr, *Vr = x.vr;
+    const int last = min(kb + TK, kw1) - 1;  // past the end: a valid row, masked to P = 0
+    const int64_t o0 = (int64_t)min(kb + crow, last) * kv_rs + ccol;
+    const int64_t o1 = (int64_t)min(kb + crow + 8, last) * kv_rs + ccol;
+    const int64_t o2 = (int64_t)min(kb + crow + 16, last) * kv_rs + ccol;
+    const int64_t o3 = (int64_t)min(kb + crow + 24, last) * kv_rs + ccol;
+    r.k0 = __builtin_nontemporal_load((const u32x4 *)(Kr + o0)); r.v0 = __builtin_nontemporal_load((const u32x4 *)(Vr + o0));
+    r.k1 = __builtin_nontemporal_load((const u32x4 *)(Kr + o1)); r.v1 = __builtin_nontemporal_load((const u32x4 *)(Vr + o1));
+    r.k2 = __builtin_nontemporal_load((const u32x4 *)(Kr + o2)); r.v2 = __builtin_nontemporal_load((const u32x4 *)(Vr + o2));
+    r.k3 = __builtin_nontemporal_load((const u32x4 *)(Kr + o3)); r.v3 = __builtin_nontemporal_load((const u32x4 *)(Vr + o3));
+  };
+  // the query rows of a segment's unit: lane (grp, l16) holds head l16's
+  // d = 8grp .. +7 and 32 + 8grp .. +7 (the MFMA B operand)
+  auto gload_q = [&](dbf16x8_t (&qv)[2], const Seg &x) __attribute__((always_inline)) {
+    const int b = x.b, g = gh;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+      qv[t] = l16 < G ? *(const dbf16x8_t *)((const bf16_t *)p.q +
+                                            ((int64_t)b * p.n_heads + g * G + l16) * HD + 8 * grp + 32 * t)
+                      : dbf16x8_t{};
+  };
+  bf16_t *const kt = KT[wave], *const vt = VT[wave];
+  auto lstore = [&](const RegTile &r) __attribute__((always_inline)) {
+    *(u32x4 *)(kt + crow * WKP + ccol) = r.k0;
+    *(u32x4 *)(kt + (crow + 8) * WKP + ccol) = r.k1;
+    *(u32x4 *)(kt + (crow + 16) * WKP + ccol) = r.k2;
+    *(u32x4 *)(kt + (crow + 24) * WKP + ccol) = r.k3;
+    *(u32x4 *)(vt + crow * WKP + ccol) = r.v0;
+    *(u32x4 *)(vt + (crow + 8) * WKP + ccol) = r.v1;
+    *(u32x4 *)(vt + (crow + 16) * WKP + ccol) = r.v2;
+    *(u32x4 *)(vt + (crow + 24) * WKP + ccol) = r.v3;
+  };
+
+  float m = -INFINITY, l = 0.f;
+  df32x4_t o[4] = {df32x4_t{}, df32x4_t{}, df32x4_t{}, df32x4_t{}};
+  dbf16x8_t qb[2], qn[2];
+  const float c = p.c;
+  // one 32-key tile from this wave's LDS tile: keys kb .. kb + 31 of a unit of kw1 keys
+  auto compute = [&](int kb, int kw1) __attribute__((always_inline)) {
+    const bf16_t *kl = kt + 8 * grp;
+    df32x4_t s[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const bf16_t *kp = kl + (16 * u + l16) * WKP;
+      s[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*(const dbf16x8_t *)(kp), qb[0], df32x4_t{},
+                                                     0, 0, 0);
+      s[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*(const dbf16x8_t *)(kp + 32), qb[1], s[u],
+                                                     0, 0, 0);
+    }
+    if (kb + TK > kw1) {
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (kb + 16 * u + 4 * grp + i >= kw1) s[u][i] = -INFINITY;
+    }
+    float mx = fmaxf(fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3])),
+                     fmaxf(fmaxf(s[1][0], s[1][1]), fmaxf(s[1][2], s[1][3])));
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float m_new = fmaxf(m, mx);  // finite: every tile holds at least one key
+    const float mc = m_new * c;
+    const float alpha = __builtin_amdgcn_exp2f(m * c - mc);  // m = -inf -> 0
+    float rs = 0.f;
+    dbf16x8_t pb;
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float e = __builtin_amdgcn_exp2f(fmaf(s[u][i], c, -mc));
+        rs += e;
+        pb[4 * u + i] = (__bf16)e;
+      }
+    l = l * alpha + rs;
+    m = m_new;
+    const bf16_t *vp = vt + (4 * grp + (l16 >> 2)) * WKP + 4 * (l16 & 3);
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+      o[dt] *= alpha;
+      const dbf16x4_t lo = lds_read_tr16(vp + 16 * dt);
+      const dbf16x4_t hi = lds_read_tr16(vp + 16 * WKP + 16 * dt);
+      const dbf16x8_t a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb, o[dt], 0, 0, 0);
+    }
+  };
+  // this wave's state of segment s into LDS (o[dt][i] = O^T[16dt + 4grp + i][head l16])
+  auto flush = [&](int s) __attribute__((always_inline)) {
+    float lt = l + __shfl_xor(l, 16, 64);
+    lt += __shfl_xor(lt, 32, 64);
+    if (l16 < G) {
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) red_o[s][wave][l16][16 * dt + 4 * grp + i] = o[dt][i];
+      if (grp == 0) {
+        red_m[s][wave][l16] = m * c;  // -inf: no key of s in this wave
+        red_l[s][wave][l16] = lt;
+      }
+    }
+  };
+  auto reset = [&]() __attribute__((always_inline)) {
+    m = -INFINITY;
+    l = 0.f;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) o[dt] = df32x4_t{};
+  };
+
+  // One register tile ahead per wave, as the whole-cache kernel: cur is the
+  // segment of the tile computed, pre that of the tile in the registers;
+  // when pre enters a new segment its query rows are loaded into qn, taken
+  // over by qb when the wave's tiles reach that segment.
+  int sc = -1;  // segment of the wave's running state
+  if (wave < ntile) {  // wave-uniform
+    Seg cur, pre;
+    seg_first(cur);
+    seg_adv(cur, wave);
+    gload_q(qb, cur);
+    RegTile ta;
+    gload(ta, wave, cur);
+    lstore(ta);
+    pre = cur;
+    if (wave + WWV < ntile) {
+      seg_adv(pre, wave + WWV);
+      if (pre.s != cur.s) gload_q(qn, pre);
+      gload(ta, wave + WWV, pre);
+    }
+    __builtin_amdgcn_wave_barrier();
+    for (int i = wave; i < ntile; i += WWV) {
+      if (cur.s != sc) {  // a new segment: the previous one's state to LDS, a fresh state
+        if (sc >= 0) flush(sc);
+        for (int x = sc + 1; x < cur.s; ++x) {
+          reset();
+          flush(x);
+        }
+        reset();
+        sc = cur.s;
+      }
+      compute(cur.kb0 + TK * i, cur.len);
+      if (i + WWV < ntile) {
+        __builtin_amdgcn_wave_barrier();
+        lstore(ta);
+        if (pre.s != cur.s) {
+          qb[0] = qn[0];
+          qb[1] = qn[1];
+        }
+        cur = pre;
+        if (i + 2 * WWV < ntile) {
+          const int s0 = pre.s;
+          seg_adv(pre, i + 2 * WWV);
+          if (pre.s != s0) gload_q(qn, pre);
+          gload(ta, i + 2 * WWV, pre);
+        }
+        __builtin_amdgcn_wave_barrier();
+      }
+    }
+  }
+  if (sc >= 0) flush(sc);
+  reset();
+  for (int x = sc + 1; x < nseg; ++x) flush(x);
+  __syncthreads();
+
+  // Merge the waves of each segment.  A unit wholly in this share is
+  // written; a cut unit's part writes its record through to memory
+  // (system-scope stores, waited for), then counts itself on the unit's
+  // counter; the part that counts last reads every record past the caches
+  // (system-scope loads) and writes the output.  No cache write-back or
+  // invalidation (an agent-scope release/acquire pair per part measured
+  // twice the kernel's time on config 3; atomic exchanges and atomic adds
+  // of zero for the records, five times).
+  Seg x;
+  if (nseg > 0) seg_first(x);
+  for (int s = 0; s < nseg; ++s) {
+    if (s > 0) seg_next(x);
+    const int b = x.b, g = gh, u = b * Hkv + g;
+    const uint32_t info = p.unit[u];
+    const int parts = (int)(info >> 24), part = grp_id - (int)((info >> 12) & 0xfffu);
+    if (parts > 1 && (part < 0 || part >= parts)) continue;  // a plan inconsistent with the walk: no write
+    bf16_t *out = (bf16_t *)p.o + ((int64_t)b * p.n_heads + (int64_t)g * G) * HD;
+    float *rec = p.rec + (int64_t)((info & 0xfffu) + part) * G * (HD + 2);
+    for (int idx = tid; idx < G * HD; idx += 64 * WWV) {
+      const int h = idx / HD, d = idx - h * HD;
+      float M = red_m[s][0][h];
+#pragma unroll
+      for (int w = 1; w < WWV; ++w) M = fmaxf(M, red_m[s][w][h]);  // finite: some wave has keys
+      float L = 0.f, A = 0.f;
+#pragma unroll
+      for (int w = 0; w < WWV; ++w) {
+        const float wt = __builtin_amdgcn_exp2f(red_m[s][w][h] - M);
+        L += red_l[s][w][h] * wt;
+        A += red_o[s][w][h][d] * wt;
+      }
+      if (parts <= 1) {
+        out[idx] = f32_to_bf16(A / L);
+      } else {
+        float *r = rec + h * (HD + 2);
+        __hip_atomic_store(r + 2 + d, A, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        if (d == 0) {
+          __hip_atomic_store(r, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+          __hip_atomic_store(r + 1, L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        }
+      }
+    }
+    if (parts <= 1) continue;  // uniform
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's record stores done
+    __syncthreads();
+    if (tid == 0) {
+      const uint32_t seen = __hip_atomic_fetch_add(p.cnt + u, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const bool last = seen == (uint32_t)parts - 1;
+      if (last) __hip_atomic_store(p.cnt + u, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      s_last = last;
+    }
+    __syncthreads();
+    if (s_last) {
+      float *rec0 = p.rec + (int64_t)(info & 0xfffu) * G * (HD + 2);
+      for (int idx = tid; idx < G * HD; idx += 64 * WWV) {
+        const int h = idx / HD, d = idx - h * HD;
+        // system-scope loads: past the caches, from where the stores went
+        auto rd = [&](const float *a) { return __hip_atomic_load(a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM); };
+        float M = -INFINITY;
+        for (int q = 0; q < parts; ++q) M = fmaxf(M, rd(rec0 + (q * G + h) * (HD + 2)));
+        float L = 0.f, A = 0.f;
+        for (int q = 0; q < parts; ++q) {
+          float *r = rec0 + (q * G + h) * (HD + 2);
+          const float wt = __builtin_amdgcn_exp2f(rd(r) - M);
+          L += rd(r + 1) * wt;
+          A += rd(r + 2 + d) * wt;
+        }
+        out[idx] = f32_to_bf16(A / L);
+      }
+    }
+    __syncthreads();  // s_last is rewritten by the next segment
+  }
+}
+
 // One thread per (b, head, d): merge the chunks [0, ceil(len/chunk)) in one
 // pass (running log-sum-exp), four chunks' loads in flight at a time.
 template <typename T>
@@ -962,6 +1311,9 @@ constexpr int kMaxScratchDevices = 64;
 static std::mutex g_scratch_mu;
 static void *g_scratch_ptr[kMaxScratchDevices];
 
+static void *g_plan_cnt_ptr[kMaxScratchDevices];
+static std::atomic<uint32_t> g_plan_next{0};
+
 int decode_scratch_setup(int device) {
   if (device < 0 || device >= kMaxScratchDevices)
     return fail(BN_ERR_UNSUPPORTED, "bn_init: device " + std::to_string(device) +
@@ -969,10 +1321,14 @@ int decode_scratch_setup(int device) {
                                         std::to_string(kMaxScratchDevices) + " devices)");
   std::lock_guard<std::mutex> lk(g_scratch_mu);
   if (g_scratch_ptr[device]) return BN_OK;
-  void *ptr = nullptr;
+  void *ptr = nullptr, *cnt = nullptr;
   BN_HIP_TRY(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
   if (!ptr) return fail(BN_ERR_HIP, "bn_init: decode scratch has no device address");
+  // the planned decode's part counters, looked up with the scratch
+  BN_HIP_TRY(hipGetSymbolAddress(&cnt, HIP_SYMBOL(plan_counters)));
+  if (!cnt) return fail(BN_ERR_HIP, "bn_init: decode plan counters have no device address");
   g_scratch_ptr[device] = ptr;
+  g_plan_cnt_ptr[device] = cnt;
   return BN_OK;
 }
 
@@ -981,6 +1337,17 @@ void *decode_scratch(int device) {
   if (device < 0 || device >= kMaxScratchDevices) return nullptr;
   std::lock_guard<std::mutex> lk(g_scratch_mu);
   return g_scratch_ptr[device];
+}
+// the next counter slot of the planned decode on `device` (null: not set up)
+uint32_t *plan_counter_slot(int device) {
+  if (device < 0 || device >= kMaxScratchDevices) return nullptr;
+  void *base;
+  {
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    base = g_plan_cnt_ptr[device];
+  }
+  if (!base) return nullptr;
+  return (uint32_t *)base + (g_plan_next.fetch_add(1) % kPlanSlots) * kPlanUnits;
 }
 }  // namespace
 }  // namespace bn
@@ -1107,6 +1474,65 @@ int gqa_decode_impl(int dtype, const void *q, const void *k_cache, const void *v
   }
   return st;
 }
+// The planned launch's share plan from the host lengths: groups of
+// n_kv_heads workgroups (one per KV head) split the batch's sequence tiles
+// into equal contiguous shares.  False when the batch is not worth planning
+// (longest sequence within 1.25x of the mean: the whole-cache kernel is
+// balanced already) or does not fit the plan's limits.
+bool build_plan(const int32_t *h_lens, int batch, int max_len, int n_kv_heads, int n_heads, int cus,
+                PlanParams &pl, int &bins, int &records) {
+  (void)n_heads;
+  const int units = batch * n_kv_heads;
+  if (units > kPlanUnits || batch > kPlanUnits || cus <= 0) return false;
+  std::vector<int> tiles(batch);
+  int64_t total = 0;
+  int tmax = 0;
+  for (int b = 0; b < batch; ++b) {
+    const int len = h_lens[b] < 0 ? 0 : (h_lens[b] > max_len ? max_len : h_lens[b]);
+    pl.len[b] = len;
+    tiles[b] = (len + TK - 1) / TK;
+    total += tiles[b];
+    tmax = std::max(tmax, tiles[b]);
+  }
+  if (total == 0 || total > 0xffffff || (int64_t)tmax * batch * 4 <= total * 5) return false;
+  const int groups0 = (int)std::min<int64_t>(std::min(cus, kPlanBins) / n_kv_heads, total);
+  if (groups0 <= 0) return false;
+  const int share = (int)((total + groups0 - 1) / groups0);
+  const int groups = (int)((total + share - 1) / share);
+  bins = groups * n_kv_heads;
+  if (share > 0xffff || tmax > 0xffff) return false;
+  // prefix of each sequence's tiles; group k takes tiles [k*share, (k+1)*share)
+  std::vector<int64_t> pre(batch + 1, 0);
+  for (int b = 0; b < batch; ++b) pre[b + 1] = pre[b] + tiles[b];
+  int b = 0;
+  for (int k = 0; k < groups; ++k) {
+    const int64_t g0 = (int64_t)k * share;
+    while (b < batch && pre[b] + tiles[b] <= g0) ++b;  // skips empty sequences
+    pl.wg_start[k] = (uint32_t)b | ((uint32_t)(g0 - pre[b]) << 16);
+    // the sequences this share touches (with keys), at most kPlanSeg
+    int n = 0;
+    for (int v = b; v < batch && pre[v] < g0 + share; ++v) n += tiles[v] > 0;
+    if (n > kPlanSeg) return false;
+  }
+  records = 0;
+  for (int v = 0; v < batch; ++v) {
+    int c0 = 0, parts = 1;
+    if (tiles[v] > 0) {
+      c0 = (int)(pre[v] / share);
+      parts = (int)((pre[v] + tiles[v] - 1) / share) - c0 + 1;
+    }
+    for (int g = 0; g < n_kv_heads; ++g) {  // each KV head's unit: parts in the same groups
+      const int base = parts > 1 ? records : 0;
+      if (parts > 1) records += parts;
+      if (records > 0xfff || c0 > 0xfff || parts > 0xff) return false;
+      pl.unit[v * n_kv_heads + g] = (uint32_t)base | ((uint32_t)c0 << 12) | ((uint32_t)parts << 24);
+    }
+  }
+  pl.share = share;
+  pl.total = (int)total;
+  pl.n_units = units;
+  return true;
+}
 }  // namespace
 }  // namespace bn
 
@@ -1125,6 +1551,87 @@ int bn_gqa_decode_noalloc(int dtype, const void *q, const void *k_cache, const v
                           int n_kv_heads, int head_dim, float scale, void *stream) {
   return gqa_decode_impl(dtype, q, k_cache, v_cache, seq_lens, o, batch, max_len, n_heads,
                          n_kv_heads, head_dim, scale, nullptr, 0, true, stream);
+}
+
+size_t bn_gqa_decode_planned_workspace_size(int batch, int max_len, int n_heads, int n_kv_heads,
+                                            int head_dim) {
+  if (batch <= 0 || max_len <= 0 || n_heads <= 0 || n_kv_heads <= 0 || n_heads % n_kv_heads ||
+      head_dim != HD)
+    return 0;
+  // the unplanned fallback's partials, or the plan's part records (at most
+  // one per unit plus one per workgroup boundary)
+  const size_t recs = ((size_t)batch * n_kv_heads + kPlanBins) * (n_heads / n_kv_heads) * (HD + 2) *
+                      sizeof(float);
+  return std::max(bn_gqa_decode_workspace_size(batch, max_len, n_heads, head_dim), recs);
+}
+
+int bn_gqa_decode_planned(int dtype, const void *q, const void *k_cache, const void *v_cache,
+                          const int32_t *seq_lens, const int32_t *h_seq_lens, void *o, int batch,
+                          int max_len, int n_heads, int n_kv_heads, int head_dim, float scale,
+                          void *workspace, size_t workspace_bytes, void *stream) {
+  const char *op = "GQA decode (planned)";
+  if (batch > 0 && !h_seq_lens)
+    return fail(BN_ERR_INVALID_ARG, std::string(op) + ": NULL host lengths");
+  if (workspace && batch > 0) {
+    const size_t want = bn_gqa_decode_planned_workspace_size(batch, max_len, n_heads, n_kv_heads, head_dim);
+    if (want && workspace_bytes < want)
+      return fail(BN_ERR_INVALID_ARG, std::string(op) + ": workspace of " +
+                                          std::to_string(workspace_bytes) + " bytes, need " +
+                                          std::to_string(want));
+  }
+  // the plan applies to bf16 caches of 1, 2, 4 or 8 query heads per KV head
+  // with at least as many units as compute units; anything else (and every
+  // argument check) is bn_gqa_decode's
+  const int G = n_kv_heads > 0 ? n_heads / n_kv_heads : 0;
+  bool planned = dtype == BN_BF16 && head_dim == HD && batch > 0 && max_len > 0 && n_kv_heads > 0 &&
+                 n_heads % n_kv_heads == 0 && (G == 1 || G == 2 || G == 4 || G == 8) &&
+                 (scale > 0.f) && std::isfinite(scale) && q && k_cache && v_cache && seq_lens && o &&
+                 !(((uintptr_t)q | (uintptr_t)k_cache | (uintptr_t)v_cache) & 15u);
+  int st;
+  PlanParams pl;
+  int bins = 0, records = 0;
+  if (planned) {
+    if ((st = ensure_device())) return st;
+    const int cus = device_cu_count();
+    planned = (int64_t)batch * n_kv_heads >= cus &&
+              build_plan(h_seq_lens, batch, max_len, n_kv_heads, n_heads, cus, pl, bins, records);
+  }
+  if (!planned)
+    return gqa_decode_impl(dtype, q, k_cache, v_cache, seq_lens, o, batch, max_len, n_heads, n_kv_heads,
+                           head_dim, scale, workspace, workspace_bytes, false, stream);
+  pl.q = q; pl.k = k_cache; pl.v = v_cache; pl.o = o;
+  pl.batch = batch; pl.max_len = max_len; pl.n_heads = n_heads; pl.n_kv_heads = n_kv_heads;
+  pl.c = scale * 1.4426950408889634f;
+  pl.cnt = plan_counter_slot(library_device());
+  if (!pl.cnt)
+    return fail(BN_ERR_HIP, std::string(op) + ": plan counters not set up for device " +
+                                std::to_string(library_device()));
+  hipStream_t s = as_stream(stream);
+  void *ws = workspace;
+  bool own = false;
+  const size_t need = (size_t)std::max(records, 1) * G * (HD + 2) * sizeof(float);
+  if (!ws && records > 0) {
+    if ((st = bn_alloc(&ws, need, stream))) return st;
+    own = true;
+  }
+  pl.rec = (float *)ws;
+  const dim3 grid((unsigned)bins), block(64 * WWV);
+  switch (G) {
+    case 1: hipLaunchKernelGGL(decode_bf16_planned_kernel<1>, grid, block, 0, s, pl); break;
+    case 2: hipLaunchKernelGGL(decode_bf16_planned_kernel<2>, grid, block, 0, s, pl); break;
+    case 4: hipLaunchKernelGGL(decode_bf16_planned_kernel<4>, grid, block, 0, s, pl); break;
+    default: hipLaunchKernelGGL(decode_bf16_planned_kernel<8>, grid, block, 0, s, pl); break;
+  }
+  st = BN_OK;
+  {
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) st = hip_fail(e, __FILE__, __LINE__);
+  }
+  if (own) {
+    int st2 = bn_free(ws, stream);
+    if (st == BN_OK) st = st2;
+  }
+  return st;
 }
 
 }  // extern "C"

@@ -340,6 +340,29 @@ int bn_gqa_decode(int dtype, const void *q, const void *k_cache,
                   int head_dim, float scale, void *workspace,
                   size_t workspace_bytes, void *stream);
 
+/* bn_gqa_decode with the lengths also on the host (h_seq_lens: host int32
+ * [batch], the values seq_lens holds on the device), as a serving loop has
+ * them.  Replaces the same row as bn_gqa_decode (the last row of the causal
+ * softmax, op_softmax.cuh:89-99, over the cache llama_model.py:135-141
+ * recomputes).  From the host lengths the call plans equal shares of the
+ * batch's 32-key tiles, one per compute unit, so a ragged batch's long caches
+ * are cut across several workgroups and merged in the same launch instead of
+ * streaming alone at the end; bf16 caches, 1/2/4/8 query heads per KV head,
+ * at least as many (sequence, KV head) units as compute units (at most 256)
+ * and a longest cache above 1.25x the mean.  Every other call (a balanced
+ * batch included) runs bn_gqa_decode on seq_lens.  workspace: device memory of
+ * bn_gqa_decode_planned_workspace_size() bytes, or NULL (the pool).  Two
+ * planned calls in flight at once on one GPU share part counters only when
+ * 16 planned launches are in flight together. */
+size_t bn_gqa_decode_planned_workspace_size(int batch, int max_len, int n_heads,
+                                            int n_kv_heads, int head_dim);
+int bn_gqa_decode_planned(int dtype, const void *q, const void *k_cache,
+                          const void *v_cache, const int32_t *seq_lens,
+                          const int32_t *h_seq_lens, void *o, int batch,
+                          int max_len, int n_heads, int n_kv_heads, int head_dim,
+                          float scale, void *workspace, size_t workspace_bytes,
+                          void *stream);
+
 /* No counterpart in the reference.  For callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, harnesses that
  * forbid hipMalloc): bn_gqa_decode with the same arguments, kernels and

@@ -145,6 +145,34 @@ def test_decode_noalloc_validation(kw, status):
     assert m.startswith("GQA decode (no allocation):")
 
 
+@pytest.mark.parametrize("kw,status,stem", [
+    (dict(hl=0), B.BN_ERR_INVALID_ARG, "GQA decode (planned): NULL host lengths"),
+    (dict(ws=0x9000, wsb=16), B.BN_ERR_INVALID_ARG, "GQA decode (planned): workspace of 16 bytes"),
+    (dict(H=24), B.BN_ERR_UNSUPPORTED, "GQA decode: "),   # every other check is bn_gqa_decode's
+    (dict(lens=0), B.BN_ERR_INVALID_ARG, "GQA decode: "),
+    (dict(q=0x1008), B.BN_ERR_UNSUPPORTED, "GQA decode: "),
+])
+def test_decode_planned_validation(kw, status, stem):
+    a = dict(dt=B.BN_BF16, q=0x1000, k=0x2000, v=0x3000, lens=0x5000, hl=0x6000, o=0x4000, B=64,
+             L=4096, H=32, Hkv=4, D=64, sc=0.125, ws=None, wsb=0)
+    a.update(kw)
+    s, m = st("bn_gqa_decode_planned", a["dt"], a["q"], a["k"], a["v"], a["lens"], a["hl"], a["o"],
+              a["B"], a["L"], a["H"], a["Hkv"], a["D"], a["sc"], a["ws"], a["wsb"], None)
+    assert s == status, m
+    assert m.startswith(stem), m
+
+
+def test_decode_planned_workspace_size():
+    L = B.lib()
+    # the fallback's partials (config 3) exceed the plan's records
+    assert L.bn_gqa_decode_planned_workspace_size(64, 4096, 32, 4, 64) == \
+        L.bn_gqa_decode_workspace_size(64, 4096, 32, 64)
+    # short caches: the records ((64*4 + 256) parts of 8 heads x 66 floats) are larger
+    assert L.bn_gqa_decode_planned_workspace_size(64, 128, 32, 4, 64) == (64 * 4 + 256) * 8 * 66 * 4
+    assert L.bn_gqa_decode_planned_workspace_size(64, 128, 32, 4, 32) == 0
+    assert L.bn_gqa_decode_planned_workspace_size(64, 128, 30, 4, 64) == 0
+
+
 def test_decode_noalloc_refuses_partials_above_scratch():
     """fp32 split path: 16 sequences of 2^20 keys in 1024-key chunks need
     16*32*1024*66*4 bytes of partials, above the 32 MiB array; the refusal
