@@ -274,13 +274,31 @@ def bench_linear(steps, warmup, seed=6):
     return out
 
 
-def bench_decode(ragged, steps, warmup, seed=2):
+def decode_lengths(kind, B_=64, L=4096, seed=2):
+    """Config 3's lengths: uniform 4096, the ragged U[512, 4096] draw, and two
+    more ragged patterns for the planned path: two length classes (512 and
+    4096 alternating) and four 4096-key caches among 600-key ones."""
     import numpy as np
+    r = np.random.default_rng(seed)
+    if kind == "ragged":
+        return r.integers(512, L + 1, B_).astype(np.int32)
+    if kind == "two_class":
+        return np.where(np.arange(B_) % 2 == 0, 512, L).astype(np.int32)
+    if kind == "skewed":
+        out = np.full(B_, 600, np.int32)
+        out[[3, 20, 41, 62]] = L
+        return out
+    return np.full(B_, L, np.int32)
+
+
+def bench_decode(kind, steps, warmup, seed=2, planned=False):
+    """Config 3 decode; planned=True times bn_gqa_decode_planned (the host
+    lengths plan equal tile shares per compute unit) instead of
+    bn_gqa_decode."""
     import torch
     import bnhip
     B_, L, H, Hkv = 64, 4096, 32, 4
-    r = np.random.default_rng(seed)
-    lens = r.integers(512, 4097, B_).astype(np.int32) if ragged else np.full(B_, L, np.int32)
+    lens = decode_lengths(kind, B_, L, seed)
     g = torch.Generator(device="cuda").manual_seed(seed)
     sets = []
     for _ in range(2):  # 2 x 268 MB > 256 MB MALL: every launch streams from HBM
@@ -288,21 +306,42 @@ def bench_decode(ragged, steps, warmup, seed=2):
                      torch.randn((B_, L, Hkv, 64), generator=g, device="cuda").bfloat16(),
                      torch.randn((B_, L, Hkv, 64), generator=g, device="cuda").bfloat16()))
     ld = torch.from_numpy(lens).cuda()
-    ws = bnhip.decode_workspace(B_, L, H)
+    nws = bnhip.lib().bn_gqa_decode_planned_workspace_size(B_, L, H, Hkv, 64)
+    ws = torch.empty(nws, dtype=torch.uint8, device="cuda")
     o = torch.empty((B_, H, 64), device="cuda", dtype=torch.bfloat16)
 
     def run(i):
         q, kc, vc = sets[i % 2]
-        bnhip.gqa_decode(q, kc, vc, ld, o, scale=0.125, workspace=ws)
+        if planned:
+            bnhip.gqa_decode_planned(q, kc, vc, ld, lens, o, scale=0.125, workspace=ws)
+        else:
+            bnhip.gqa_decode(q, kc, vc, ld, o, scale=0.125, workspace=ws)
 
     ms = time_launches(run, steps, warmup)
     nb = decode_bytes(lens, Hkv, 64, B_, H, 2)
     gbs = nb / (ms * 1e-3) / 1e9
+    desc = {"uniform": "uniform 4096", "ragged": f"ragged U[512,4096] seed {seed}",
+            "two_class": "512 and 4096 alternating", "skewed": "four 4096 among 600"}[kind]
+    key = {"uniform": "decode", "ragged": "decode_ragged"}.get(kind, "")
     return {"value": round(gbs, 2), "unit": "GB/s", "ms_per_launch": round(ms, 5),
-            "bytes_per_launch": nb, "lengths": "uniform 4096" if not ragged else
-            f"ragged U[512,4096] seed {seed}, sum {int(lens.sum())}",
+            "bytes_per_launch": nb, "lengths": f"{desc}, sum {int(lens.sum())}",
+            "entry_point": "bn_gqa_decode_planned" if planned else "bn_gqa_decode",
             "roofline": roofline("hbm", gbs, PEAK_HBM_GBS, "GB/s",
-                                 measured_traffic("decode_ragged" if ragged else "decode"))}
+                                 measured_traffic("decode_planned_" + kind) if planned
+                                 else measured_traffic(key))}
+
+
+def bench_decode_planned(steps, warmup):
+    """The planned decode beside bn_gqa_decode on three ragged patterns."""
+    out = {}
+    for kind in ("ragged", "two_class", "skewed"):
+        pl = bench_decode(kind, steps, warmup, planned=True)
+        plain = bench_decode(kind, steps, warmup) if kind != "ragged" else None
+        out[kind] = {"planned": pl}
+        if plain is not None:
+            out[kind]["bn_gqa_decode"] = plain
+    out["roofline"] = dict(out["two_class"]["planned"]["roofline"], kind="two_class planned")
+    return out
 
 
 def bench_rmsnorm_rope(steps, warmup):
@@ -798,7 +837,7 @@ def main():
                          "so a kernel trace holds exactly one prefill + 128 steps)")
     ap.add_argument("--only", default="",
                     help="comma list of extra workloads (default: all but copy): "
-                         "decode,ragged,fp32,norm,long,addnorm,swiglu,linear,bwd,block,tinyllama,copy; "
+                         "decode,ragged,planned,fp32,norm,long,addnorm,swiglu,linear,bwd,block,tinyllama,copy; "
                          "'head' = headline prefill only")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -827,11 +866,15 @@ def main():
     print(f"prefill bf16: {head['value']} TFLOP/s ({head['ms_per_launch']} ms)", file=sys.stderr,
           flush=True)
     if want("decode"):
-        out["decode"] = bench_decode(False, K, W)
+        out["decode"] = bench_decode("uniform", K, W)
         print(f"decode: {out['decode']['value']} GB/s", file=sys.stderr, flush=True)
     if want("ragged"):
-        out["decode_ragged"] = bench_decode(True, K, W)
+        out["decode_ragged"] = bench_decode("ragged", K, W)
         print(f"decode ragged: {out['decode_ragged']['value']} GB/s", file=sys.stderr, flush=True)
+    if want("planned"):
+        out["decode_planned"] = bench_decode_planned(K, W)
+        print(f"decode planned: { {k: v['planned']['value'] for k, v in out['decode_planned'].items() if k != 'roofline'} }",
+              file=sys.stderr, flush=True)
     if want("fp32"):
         out["prefill_fp32"] = bench_prefill(4, 2048, 32, 4, "fp32", max(K // 2, 3), 2)
         print(f"prefill fp32: {out['prefill_fp32']['value']} TFLOP/s", file=sys.stderr, flush=True)
@@ -870,6 +913,9 @@ def main():
         out["cpu_baseline"] = cpu_baseline_prefill()
         cpu = {"decode": lambda: cpu_baseline_decode(False),
                "decode_ragged": lambda: cpu_baseline_decode(True),
+               "decode_planned": lambda: dict(cpu_baseline_decode(True),
+                                              note="the ragged pattern's oracle run (the planned path "
+                                                   "computes the same rows)"),
                # the oracle computes in fp32 whatever the GPU dtype: the same sample
                "prefill_fp32": lambda: dict(out["cpu_baseline"],
                                             note="same oracle run as the headline's (fp32)"),
