@@ -75,10 +75,128 @@ struct LinNorm {
   float *h_out;
   float eps;
 };
+// A merged input for an output-major projection of one fp32 row: x is the
+// attention output of a split short-cache decode (decode_short_partials),
+// formed in the staging from its partial records -- x[h*64 + d] merges the
+// n_split records of query head h (`part`: [n_heads][n_split][kDecRec]) over
+// the valid splits of the sequence's length (`lens[0]`, device, clamped to
+// [0, max_len]) -- with the arithmetic of the decode's own combine kernel,
+// so the product has the bits of bn_gqa_decode followed by the projection.
+struct LinMerge {
+  const float *part;
+  const int32_t *lens;
+  int n_split, max_len;
+  int len;  // >= 0: the sequence's length, given by the host (lens is not read)
+};
 int linear_run(const bn_view *x, const bn_view *w, const bn_view *y, int rope_cols,
                int position_offset, int head_dim, float theta, void *workspace,
                size_t workspace_bytes, int epi, float *k_dst, float *v_dst, int app_col, int app_w,
-               int64_t app_rs, void *stream, const LinNorm *nrm = nullptr);
+               int64_t app_rs, void *stream, const LinNorm *nrm = nullptr,
+               const LinMerge *mrg = nullptr);
+
+// ------------------------------------------------ split decode partials
+// A split decode writes, per (sequence, query head), n_split records of
+// kDecRec floats: m (the split's largest score, log2 units), l (its sum of
+// exp2(s - m)) and acc[64] (its sum of exp2(s - m) * v).  Splits at or past
+// the sequence's valid count hold no keys and are never read as numbers.
+constexpr int kDecRec = 66;
+// The short-cache split decode (fp32 caches of at most kShortMaxLen keys,
+// at most kShortMaxUnits (sequence, query head) pairs): kShortSplits splits
+// per (sequence, query head), each of short_split_chunk(len) keys.
+constexpr int kShortMaxLen = 1024, kShortMaxUnits = 256, kShortSplits = 4;
+__host__ __device__ inline int short_split_chunk(int len, int n_split) {
+  const int c = ((len + n_split - 1) / n_split + 3) & ~3;  // whole 4-key lane groups
+  return c < 4 ? 4 : c;
+}
+// Launches the short-cache split decode alone: fp32 q [batch, n_heads, 64],
+// caches [batch, max_len, n_kv_heads, 64], partial records into `part`
+// ([batch * n_heads][kShortSplits][kDecRec]); the caller merges them
+// (bn_decode.hip's combine, or an output projection's LinMerge staging).
+// Shapes are the caller's to check: short_path_ok() true.
+// host_len >= 0: every sequence's length, given by the host (seq_lens is
+// not read; a decode loop knows its position).
+bool short_path_ok(int dtype, int batch, int max_len, int n_heads);
+int decode_short_partials(const float *q, const float *k_cache, const float *v_cache,
+                          const int32_t *seq_lens, int host_len, float *part, int batch, int max_len,
+                          int n_heads, int n_kv_heads, float scale, hipStream_t s);
+
+// The merge of 4 consecutive d of one (sequence, head) over records
+// [0, nvalid), in groups of 8 records (loads of a group first, then its
+// merge, with the running max rescaled between groups).  Records at or past
+// nvalid are read from an in-range slot and skipped by a select (never
+// multiplied by a zero weight: they may hold Inf or NaN).
+struct DecMerge {
+  float ms[8], ls[8];
+  float4 as[8];
+  float M, L, A[4];
+  __device__ __forceinline__ void start() {
+    M = -INFINITY;
+    L = 0.f;
+    A[0] = A[1] = A[2] = A[3] = 0.f;
+  }
+  // SYS: system-scope loads, past the caches (records another workgroup of
+  // the same launch wrote through to memory); the same values either way
+  template <bool SYS = false>
+  __device__ __forceinline__ void load8(const float *part, int n_split, int s0, int d0) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float *ps = part + min(s0 + j, n_split - 1) * kDecRec;
+      if constexpr (SYS) {
+        auto rd = [](const float *a) { return __hip_atomic_load(a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM); };
+        ms[j] = rd(ps);
+        ls[j] = rd(ps + 1);
+        as[j] = make_float4(rd(ps + 2 + d0), rd(ps + 3 + d0), rd(ps + 4 + d0), rd(ps + 5 + d0));
+      } else {
+        const float2 ml = *reinterpret_cast<const float2 *>(ps);  // 264-byte records: 8-byte aligned
+        ms[j] = ml.x;
+        ls[j] = ml.y;
+        as[j] = make_float4(ps[2 + d0], ps[3 + d0], ps[4 + d0], ps[5 + d0]);
+      }
+    }
+  }
+  // the same values in two parts: acc from the records, (m, l) from a table
+  // of pairs (stride 2 floats; e.g. gathered into LDS)
+  __device__ __forceinline__ void load_acc8(const float *part, int n_split, int s0, int d0) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float *ps = part + min(s0 + j, n_split - 1) * kDecRec;
+      as[j] = make_float4(ps[2 + d0], ps[3 + d0], ps[4 + d0], ps[5 + d0]);
+    }
+  }
+  __device__ __forceinline__ void load_ml8(const float *ml, int n_split, int s0) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float2 v = *reinterpret_cast<const float2 *>(ml + 2 * min(s0 + j, n_split - 1));
+      ms[j] = v.x;
+      ls[j] = v.y;
+    }
+  }
+  __device__ __forceinline__ void merge8(int s0, int nvalid) {
+    float mx = M;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) mx = s0 + j < nvalid ? fmaxf(mx, ms[j]) : mx;
+    const float mu = mx == -INFINITY ? 0.f : mx;       // nothing valid yet: weights stay 0
+    const float fo = __builtin_amdgcn_exp2f(M - mu);  // M = -inf -> 0
+    L *= fo;
+    A[0] *= fo; A[1] *= fo; A[2] *= fo; A[3] *= fo;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const bool ok = s0 + j < nvalid;
+      const float f = __builtin_amdgcn_exp2f(ms[j] - mu);
+      L = ok ? fmaf(ls[j], f, L) : L;
+      A[0] = ok ? fmaf(as[j].x, f, A[0]) : A[0];
+      A[1] = ok ? fmaf(as[j].y, f, A[1]) : A[1];
+      A[2] = ok ? fmaf(as[j].z, f, A[2]) : A[2];
+      A[3] = ok ? fmaf(as[j].w, f, A[3]) : A[3];
+    }
+    M = mx;
+  }
+  // the merged values (an empty sequence: zeros)
+  __device__ __forceinline__ float4 result() const {
+    const float inv = L > 0.f ? 1.0f / L : 0.f;
+    return make_float4(A[0] * inv, A[1] * inv, A[2] * inv, A[3] * inv);
+  }
+};
 
 // ------------------------------------------------------------ validation
 inline size_t dtype_size(int dt) { return dt == BN_BF16 ? 2 : 4; }

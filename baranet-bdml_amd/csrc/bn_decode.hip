@@ -41,6 +41,11 @@ static __device__ __align__(256) float scratch[BN_GQA_DECODE_SCRATCH_BYTES / siz
 // its turn comes round (launches share a slot only when 16 are in flight).
 static __device__ __align__(256) uint32_t plan_counters[16 * 256];
 
+// Per-(sequence, query head) split counters of the short-cache decode's
+// in-launch merge: slots of kShortMaxUnits counters, zero at load time, a
+// host-side ring of slots; each unit's last split clears its counter.
+static __device__ __align__(256) uint32_t short_counters[16 * 256];
+
 // bf16 K/V cache loads are non-temporal (streamed once, kept out of L2/MALL):
 // +24% on config 3 against plain loads.
 
@@ -52,6 +57,9 @@ constexpr int NT = 8;  // keys per lane group between softmax rescales
 // single pass: 10 keys per lane group, up to 640 keys (16 waves x 4 groups x
 // 10) in one load round (3-6% faster than 8 at config 4's lengths)
 constexpr int kSingleNT = 10;
+// short-cache split (DEC_SHORT): keys per lane group per round, waves per
+// workgroup and query heads per workgroup
+constexpr int kShortNT = 10, kShortWV = 4, kShortG = 1;
 
 template <typename T> struct DecVec;
 template <> struct DecVec<float> {
@@ -86,19 +94,38 @@ struct DecodeParams {
   void *o;
   float *ws;  // partials: [batch*n_heads][n_split][HD + 2]
   int batch, max_len, n_heads, n_kv_heads, n_split, chunk;
-  float c;  // scale * log2(e)
+  float c;        // scale * log2(e)
+  int hlen = -1;  // >= 0: every sequence's length, from the host (lens not read)
+  // DEC_SHORT: per-(sequence, query head) counters (zero at launch, cleared
+  // again by each unit's last split): the last split to arrive merges the
+  // unit's records and writes the output in the same launch; null: the
+  // records are left for a combine
+  uint32_t *cnt = nullptr;
 };
 
-// WV waves per workgroup.  SINGLE (G = 1): one workgroup per (sequence,
-// query head) covers the whole cache of its KV head (each wave a contiguous
-// key range) and writes the output itself -- no partials, no combine launch;
-// for short caches and few sequences, where the split version is
-// latency-bound.  The workgroups of one KV head read the same cache rows
-// (from L2 after the first), each doing 1/G of the arithmetic.
-template <typename T, int G, int WV, bool SINGLE>
+// WV waves per workgroup; MODE:
+//   DEC_SPLIT: one workgroup per (sequence, KV head, chunk of p.chunk keys)
+//     serving the KV head's G query heads; the waves interleave blocks of
+//     KPI*NT keys over the chunk; writes the chunk's partial records.
+//   DEC_SINGLE (G = 1): one workgroup per (sequence, query head) covers the
+//     whole cache of its KV head (each wave a contiguous key range) and
+//     writes the output itself -- no partials, no combine launch.
+//   DEC_SHORT: one workgroup per (sequence, G query heads of one KV head,
+//     split); split s takes keys [s*chunk, (s+1)*chunk) of the sequence's
+//     length with chunk = short_split_chunk(len, n_split), each wave a
+//     contiguous part; writes the split's partial records.  For short caches
+//     and few sequences, where one workgroup per query head is bound by what
+//     one compute unit can stream (every workgroup reads the whole cache).
+// The workgroups that read the same cache rows (the query heads of one KV
+// head, in SINGLE and SHORT) get consecutive unit numbers, and units are
+// numbered so that consecutive ones go to one XCD (workgroups are dealt to
+// the 8 XCDs in turn): they read those rows from one L2.
+constexpr int DEC_SPLIT = 0, DEC_SINGLE = 1, DEC_SHORT = 2;
+template <typename T, int G, int WV, int MODE>
 __global__ __launch_bounds__(64 * WV) void decode_split_kernel(DecodeParams p) {
+  constexpr bool SINGLE = MODE == DEC_SINGLE, CONTIG = MODE != DEC_SPLIT;
   constexpr int VEC = DecVec<T>::VEC;
-  constexpr int NT = SINGLE ? kSingleNT : bn::NT;
+  constexpr int NT = MODE == DEC_SHORT ? kShortNT : (SINGLE ? kSingleNT : bn::NT);
   constexpr int LPK = HD / VEC;  // lanes per key
   constexpr int KPI = 64 / LPK;  // keys per wave per load instruction
   __shared__ float red_m[WV][G], red_l[WV][G];
@@ -108,48 +135,68 @@ __global__ __launch_bounds__(64 * WV) void decode_split_kernel(DecodeParams p) {
   const int sub = lane % LPK;  // 16-byte slice of the key row
   const int grp = lane / LPK;  // key slot within the wave
   static_assert(!SINGLE || G == 1, "single pass: one query head per workgroup");
-  const int split = SINGLE ? 0 : blockIdx.x % p.n_split;
-  // SINGLE: consecutive (sequence, query head) units -- the query heads of one
-  // KV head -- go to one XCD (workgroups are dealt to the 8 XCDs in turn), so
-  // they read that KV head's cache rows from one L2
-  int bg = SINGLE ? blockIdx.x : blockIdx.x / p.n_split;
-  if (SINGLE && (gridDim.x & 7) == 0)
-    bg = (blockIdx.x & 7) * (gridDim.x >> 3) + (blockIdx.x >> 3);
-  const int units = SINGLE ? p.n_heads : p.n_kv_heads;
-  const int b = bg / units;
-  // KV head g; query heads h0 .. h0 + G - 1
-  const int g = SINGLE ? (bg % units) / (p.n_heads / p.n_kv_heads) : bg % units;
-  const int h0 = SINGLE ? bg % units : g * G;
+  int u = blockIdx.x;
+  if (CONTIG && (gridDim.x & 7) == 0) u = (blockIdx.x & 7) * (gridDim.x >> 3) + (blockIdx.x >> 3);
+  int b, g, h0, split = 0;
+  if constexpr (MODE == DEC_SPLIT) {
+    split = u % p.n_split;
+    const int bg = u / p.n_split;
+    b = bg / p.n_kv_heads;
+    g = bg % p.n_kv_heads;
+    h0 = g * G;
+  } else if constexpr (SINGLE) {
+    b = u / p.n_heads;
+    h0 = u % p.n_heads;
+    g = h0 / (p.n_heads / p.n_kv_heads);
+  } else {  // units (sequence, KV head, split, query-head group), the last fastest
+    const int qpg = p.n_heads / p.n_kv_heads / G;  // query-head groups per KV head
+    const int qg = u % qpg;
+    u /= qpg;
+    split = u % p.n_split;
+    u /= p.n_split;
+    g = u % p.n_kv_heads;
+    b = u / p.n_kv_heads;
+    h0 = g * (p.n_heads / p.n_kv_heads) + qg * G;
+  }
 
-  int len = p.lens[b];
+  // this lane's slice of the G query vectors, pre-scaled into the log2
+  // domain; requested before the length (its loads do not wait for it)
+  float qv[G][VEC];
+#pragma unroll
+  for (int h = 0; h < G; ++h) {
+    const T *qp = (const T *)p.q + ((int64_t)b * p.n_heads + h0 + h) * HD + sub * VEC;
+    DecVec<T>::load(qp, qv[h]);
+  }
+  int len = p.hlen >= 0 ? p.hlen : p.lens[b];
   len = len < 0 ? 0 : (len > p.max_len ? p.max_len : len);
   if (SINGLE && len == 0) {  // no key: zeros
     for (int idx = tid; idx < G * HD; idx += 64 * WV)
       Elem<T>::store((T *)p.o + ((int64_t)b * p.n_heads + h0) * HD + idx, 0.f);
     return;
   }
-  const int k_begin = SINGLE ? 0 : split * p.chunk;
-  if (k_begin >= len) return;  // the combine kernel ignores chunks past len
-  const int k_end = SINGLE ? len : min(k_begin + p.chunk, len);
-  // SINGLE: wave w takes keys [kw0, kw1), a contiguous range; else the waves
+  const int chunk = MODE == DEC_SHORT ? short_split_chunk(len, p.n_split) : p.chunk;
+  const int k_begin = SINGLE ? 0 : split * chunk;
+  if (k_begin >= len) {  // the combine ignores chunks past len
+    if (MODE == DEC_SHORT && p.cnt && len == 0 && split == 0)  // no key, no merge: zeros
+      for (int idx = tid; idx < G * HD; idx += 64 * WV)
+        Elem<T>::store((T *)p.o + ((int64_t)b * p.n_heads + h0) * HD + idx, 0.f);
+    return;
+  }
+  const int k_end = SINGLE ? len : min(k_begin + chunk, len);
+  // CONTIG: wave w takes keys [kw0, kw1), a contiguous range; else the waves
   // interleave blocks of KPI*NT keys over the chunk
   const int per = ((k_end - k_begin + WV - 1) / WV + KPI - 1) / KPI * KPI;
-  const int kw0 = SINGLE ? k_begin + wave * per : k_begin + wave * KPI * NT;
-  const int kw1 = SINGLE ? min(kw0 + per, k_end) : k_end;
+  const int kw0 = CONTIG ? k_begin + wave * per : k_begin + wave * KPI * NT;
+  const int kw1 = CONTIG ? min(kw0 + per, k_end) : k_end;
 
   const int64_t kv_rs = (int64_t)p.n_kv_heads * HD;
   const T *Kb = (const T *)p.k + ((int64_t)b * p.max_len) * kv_rs + (int64_t)g * HD + sub * VEC;
   const T *Vb = (const T *)p.v + ((int64_t)b * p.max_len) * kv_rs + (int64_t)g * HD + sub * VEC;
 
-  // this lane's slice of the G query vectors, pre-scaled into the log2 domain
-  float qv[G][VEC];
 #pragma unroll
-  for (int h = 0; h < G; ++h) {
-    const T *qp = (const T *)p.q + ((int64_t)b * p.n_heads + h0 + h) * HD + sub * VEC;
-    DecVec<T>::load(qp, qv[h]);
+  for (int h = 0; h < G; ++h)
 #pragma unroll
     for (int e = 0; e < VEC; ++e) qv[h][e] *= p.c;
-  }
 
   float m[G], l[G], acc[G][VEC];
 #pragma unroll
@@ -160,7 +207,7 @@ __global__ __launch_bounds__(64 * WV) void decode_split_kernel(DecodeParams p) {
     for (int e = 0; e < VEC; ++e) acc[h][e] = 0.f;
   }
 
-  const int step = SINGLE ? KPI * NT : WV * KPI * NT;
+  const int step = CONTIG ? KPI * NT : WV * KPI * NT;
   for (int base = kw0; base < kw1; base += step) {
     // K and V of the NT keys of this lane group are requested together (one
     // memory round trip per NT keys); keys past the chunk read the chunk's
@@ -173,10 +220,11 @@ __global__ __launch_bounds__(64 * WV) void decode_split_kernel(DecodeParams p) {
       DecVec<T>::load(Kb + (int64_t)key * kv_rs, kk[t]);
       DecVec<T>::load(Vb + (int64_t)key * kv_rs, vv[t]);
     }
-    // single pass: every load of the round is issued before any is consumed.
-    // Left alone, the scheduler trades them for registers (load, wait, use,
-    // next: ten round trips); 116 VGPRs still fit 16 waves per workgroup.
-    if constexpr (SINGLE) __builtin_amdgcn_sched_barrier(0);
+    // contiguous ranges: every load of the round is issued before any is
+    // consumed.  Left alone, the scheduler trades them for registers (load,
+    // wait, use, next: ten round trips); 116 VGPRs still fit 16 waves per
+    // workgroup.
+    if constexpr (CONTIG) __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
       const int key = base + t * KPI + grp;
@@ -263,11 +311,57 @@ __global__ __launch_bounds__(64 * WV) void decode_split_kernel(DecodeParams p) {
       Elem<T>::store((T *)p.o + ((int64_t)b * p.n_heads + h0 + h) * HD + d, A / L);
       continue;
     }
-    float *part = p.ws + (((int64_t)b * p.n_heads + h0 + h) * p.n_split + split) * (HD + 2);
+    float *part = p.ws + (((int64_t)b * p.n_heads + h0 + h) * p.n_split + split) * kDecRec;
+    if (MODE == DEC_SHORT && p.cnt) {  // through to memory: another workgroup merges them
+      __hip_atomic_store(part + 2 + d, A, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+      if (d == 0) {
+        __hip_atomic_store(part, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        __hip_atomic_store(part + 1, L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+      }
+      continue;
+    }
     part[2 + d] = A;
     if (d == 0) {
       part[0] = M;
       part[1] = L;
+    }
+  }
+  if constexpr (MODE == DEC_SHORT) {
+    if (!p.cnt) return;
+    // the unit's splits holding keys count themselves; the last to arrive
+    // reads their records past the caches and merges them as the combine
+    // kernel does (DecMerge), so the output has the combine's bits
+    __shared__ bool s_last;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's record stores done
+    __syncthreads();
+    if (tid == 0) {
+      const int unit = (b * p.n_heads + h0) / G;
+      const uint32_t nvalid = (uint32_t)((len + chunk - 1) / chunk);
+      const uint32_t seen = __hip_atomic_fetch_add(p.cnt + unit, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const bool last = seen == nvalid - 1;
+      if (last) __hip_atomic_store(p.cnt + unit, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      s_last = last;
+    }
+    __syncthreads();
+    if (!s_last) return;
+    const int nvalid = (len + chunk - 1) / chunk;
+    for (int idx = tid; idx < G * HD / 4; idx += 64 * WV) {
+      const int h = idx / (HD / 4), d0 = (idx % (HD / 4)) * 4;
+      const float *part = p.ws + ((int64_t)b * p.n_heads + h0 + h) * p.n_split * kDecRec;
+      DecMerge mg;
+      mg.load8<true>(part, p.n_split, 0, d0);
+      mg.start();
+      mg.merge8(0, nvalid);
+      for (int s0 = 8; s0 < nvalid; s0 += 8) {
+        mg.load8<true>(part, p.n_split, s0, d0);
+        mg.merge8(s0, nvalid);
+      }
+      const float4 r = mg.result();
+      T *out = (T *)p.o + ((int64_t)b * p.n_heads + h0 + h) * HD + d0;
+      Elem<T>::store(out + 0, r.x);
+      Elem<T>::store(out + 1, r.y);
+      Elem<T>::store(out + 2, r.z);
+      Elem<T>::store(out + 3, r.w);
     }
   }
 }
@@ -850,9 +944,9 @@ __global__ __launch_bounds__(64 * WWV) void decode_bf16_whole_kernel(DecodeParam
 // turn (tile i -> wave i % 4, the loads running on across segment
 // boundaries), keep one (m, l, acc) per segment, and merge them through LDS
 // at the end.  A unit lying wholly in the share is written directly; a cut
-// unit's part writes an (m, l, acc) record, and the last of its parts to
-// arrive (a per-unit counter, agent-scope release / acquire) merges the
-// records and writes the output -- in the same launch.
+// unit's part writes an (m, l, acc) record through to memory, and the last
+// of its parts to arrive (a per-unit counter) reads the records back past
+// the caches, merges them and writes the output -- in the same launch.
 constexpr int kPlanBins = 256;   // workgroups of a planned launch, at most
 constexpr int kPlanUnits = 256;  // (sequence, KV head) units, at most
 constexpr int kPlanSeg = 8;      // units one share may touch, at most
@@ -1186,62 +1280,32 @@ template <typename T>
 __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeParams p) {
   // one thread per 4 consecutive d of one (sequence, head); the partial loads
   // of 8 chunks are issued together with the length load (slots past the
-  // valid chunks read an in-range record and are skipped in the merge)
+  // valid chunks read an in-range record and are skipped in the merge).
+  // chunk 0: the short-cache split's chunk, derived from the length.
   const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (idx >= (int64_t)p.batch * p.n_heads * (HD / 4)) return;
   const int d0 = (int)(idx % (HD / 4)) * 4;
   const int64_t bh = idx / (HD / 4);
   const int b = (int)(bh / p.n_heads);
-  const float *part = p.ws + bh * p.n_split * (HD + 2);
-  float ms[8], ls[8];
-  float4 as[8];
-  auto load8 = [&](int s0) __attribute__((always_inline)) {
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const float *ps = part + min(s0 + j, p.n_split - 1) * (HD + 2);
-      const float2 ml = *reinterpret_cast<const float2 *>(ps);  // 264-byte records: 8-byte aligned
-      ms[j] = ml.x;
-      ls[j] = ml.y;
-      as[j] = make_float4(ps[2 + d0], ps[3 + d0], ps[4 + d0], ps[5 + d0]);
-    }
-  };
-  int len = p.lens[b];
-  load8(0);
+  const float *part = p.ws + bh * p.n_split * kDecRec;
+  DecMerge mg;
+  int len = p.hlen >= 0 ? p.hlen : p.lens[b];
+  mg.load8(part, p.n_split, 0, d0);
   len = len < 0 ? 0 : (len > p.max_len ? p.max_len : len);
-  const int nvalid = (len + p.chunk - 1) / p.chunk;  // chunks holding keys (finite max)
-  float M = -INFINITY, L = 0.f, A[4] = {0.f, 0.f, 0.f, 0.f};
-  auto merge8 = [&](int s0) __attribute__((always_inline)) {
-    float mx = M;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) mx = s0 + j < nvalid ? fmaxf(mx, ms[j]) : mx;
-    const float mu = mx == -INFINITY ? 0.f : mx;       // nothing valid yet: weights stay 0
-    const float fo = __builtin_amdgcn_exp2f(M - mu);  // M = -inf -> 0
-    L *= fo;
-    A[0] *= fo; A[1] *= fo; A[2] *= fo; A[3] *= fo;
-    // slots past the valid chunks hold whatever the workspace held before
-    // (possibly Inf or NaN): they are skipped by a select, never multiplied
-    // by a zero weight
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const bool ok = s0 + j < nvalid;
-      const float f = __builtin_amdgcn_exp2f(ms[j] - mu);
-      L = ok ? fmaf(ls[j], f, L) : L;
-      A[0] = ok ? fmaf(as[j].x, f, A[0]) : A[0];
-      A[1] = ok ? fmaf(as[j].y, f, A[1]) : A[1];
-      A[2] = ok ? fmaf(as[j].z, f, A[2]) : A[2];
-      A[3] = ok ? fmaf(as[j].w, f, A[3]) : A[3];
-    }
-    M = mx;
-  };
-  merge8(0);  // the first 8 chunks need no branch on the length
+  const int chunk = p.chunk > 0 ? p.chunk : short_split_chunk(len, p.n_split);
+  const int nvalid = (len + chunk - 1) / chunk;  // chunks holding keys (finite max)
+  mg.start();
+  mg.merge8(0, nvalid);  // the first 8 chunks need no branch on the length
   for (int s0 = 8; s0 < nvalid; s0 += 8) {
-    load8(s0);
-    merge8(s0);
+    mg.load8(part, p.n_split, s0, d0);
+    mg.merge8(s0, nvalid);
   }
-  const float inv = L > 0.f ? 1.0f / L : 0.f;  // empty sequence -> zeros
+  const float4 r = mg.result();
   T *out = (T *)p.o + bh * HD + d0;
-#pragma unroll
-  for (int e = 0; e < 4; ++e) Elem<T>::store(out + e, A[e] * inv);
+  Elem<T>::store(out + 0, r.x);
+  Elem<T>::store(out + 1, r.y);
+  Elem<T>::store(out + 2, r.z);
+  Elem<T>::store(out + 3, r.w);
 }
 
 // split-K workgroup targets: per-head kernels / whole-row kernel (4 KV heads
@@ -1264,23 +1328,18 @@ void launch_split(const DecodeParams &p, dim3 grid, hipStream_t s) {
     else
       hipLaunchKernelGGL((decode_bf16_mfma_kernel<G>), grid, dim3(256), 0, s, p);
   } else {
-    hipLaunchKernelGGL((decode_split_kernel<T, G, 4, false>), grid, dim3(256), 0, s, p);
+    hipLaunchKernelGGL((decode_split_kernel<T, G, 4, DEC_SPLIT>), grid, dim3(256), 0, s, p);
   }
 }
 
 bool rows_path(const DecodeParams &p, bool bf16) { return bf16 && p.n_kv_heads % 4 == 0; }
 
-// fp32 caches of at most this many keys with at most this many (sequence,
-// query head) pairs take the single-pass kernel
-constexpr int kSingleMaxLen = 1024, kSingleMaxUnits = 256;
-bool single_path(int dtype, int batch, int max_len, int n_heads) {
-  return dtype == BN_F32 && max_len <= kSingleMaxLen && (int64_t)batch * n_heads <= kSingleMaxUnits;
-}
 
-void launch_single(const DecodeParams &p, hipStream_t s) {
-  constexpr int WV = 16;  // waves per workgroup (16 measured faster than 8)
-  hipLaunchKernelGGL((decode_split_kernel<float, 1, WV, true>), dim3((unsigned)(p.batch * p.n_heads)),
-                     dim3(64 * WV), 0, s, p);
+
+void launch_short(const DecodeParams &p, hipStream_t s) {
+  const dim3 grid((unsigned)((int64_t)p.batch * p.n_heads / kShortG * p.n_split));
+  hipLaunchKernelGGL((decode_split_kernel<float, kShortG, kShortWV, DEC_SHORT>), grid, dim3(64 * kShortWV),
+                     0, s, p);
 }
 
 template <typename T>
@@ -1289,6 +1348,7 @@ int launch_decode(const DecodeParams &p, int G, hipStream_t s) {
   const dim3 grid((unsigned)((int64_t)p.batch * (rows ? p.n_kv_heads / 4 : p.n_kv_heads) *
                              p.n_split));
   switch (G) {
+    case 0: launch_short(p, s); break;  // short-cache split (fp32)
     case 1: launch_split<T, 1>(p, grid, s); break;
     case 2: launch_split<T, 2>(p, grid, s); break;
     case 4: launch_split<T, 4>(p, grid, s); break;
@@ -1304,6 +1364,26 @@ int launch_decode(const DecodeParams &p, int G, hipStream_t s) {
 
 }  // namespace
 
+bool short_path_ok(int dtype, int batch, int max_len, int n_heads) {
+  return dtype == BN_F32 && batch > 0 && max_len > 0 && max_len <= kShortMaxLen &&
+         (int64_t)batch * n_heads <= kShortMaxUnits;
+}
+
+int decode_short_partials(const float *q, const float *k_cache, const float *v_cache,
+                          const int32_t *seq_lens, int host_len, float *part, int batch, int max_len,
+                          int n_heads, int n_kv_heads, float scale, hipStream_t s) {
+  DecodeParams p;
+  p.q = q; p.k = k_cache; p.v = v_cache; p.lens = seq_lens; p.o = nullptr; p.ws = part;
+  p.hlen = host_len;
+  p.batch = batch; p.max_len = max_len; p.n_heads = n_heads; p.n_kv_heads = n_kv_heads;
+  p.n_split = kShortSplits;
+  p.chunk = 0;
+  p.c = scale * 1.4426950408889634f;
+  launch_short(p, s);
+  BN_LAUNCH_CHECK();
+  return BN_OK;
+}
+
 // Device address of `scratch` per device, looked up once per device by
 // bn_init (with that device current).  Each GPU holds its own copy of the
 // array at its own address.
@@ -1313,6 +1393,8 @@ static void *g_scratch_ptr[kMaxScratchDevices];
 
 static void *g_plan_cnt_ptr[kMaxScratchDevices];
 static std::atomic<uint32_t> g_plan_next{0};
+static void *g_short_cnt_ptr[kMaxScratchDevices];
+static std::atomic<uint32_t> g_short_next{0};
 
 int decode_scratch_setup(int device) {
   if (device < 0 || device >= kMaxScratchDevices)
@@ -1327,8 +1409,12 @@ int decode_scratch_setup(int device) {
   // the planned decode's part counters, looked up with the scratch
   BN_HIP_TRY(hipGetSymbolAddress(&cnt, HIP_SYMBOL(plan_counters)));
   if (!cnt) return fail(BN_ERR_HIP, "bn_init: decode plan counters have no device address");
+  void *scnt = nullptr;  // the short-cache decode's split counters
+  BN_HIP_TRY(hipGetSymbolAddress(&scnt, HIP_SYMBOL(short_counters)));
+  if (!scnt) return fail(BN_ERR_HIP, "bn_init: short decode counters have no device address");
   g_scratch_ptr[device] = ptr;
   g_plan_cnt_ptr[device] = cnt;
+  g_short_cnt_ptr[device] = scnt;
   return BN_OK;
 }
 
@@ -1349,6 +1435,19 @@ uint32_t *plan_counter_slot(int device) {
   if (!base) return nullptr;
   return (uint32_t *)base + (g_plan_next.fetch_add(1) % kPlanSlots) * kPlanUnits;
 }
+// the next counter slot of the short-cache decode on `device` (null: not set up)
+constexpr int kShortSlots = 16;
+static_assert(kShortSlots * kShortMaxUnits == 16 * 256, "short_counters holds kShortSlots slots");
+uint32_t *short_counter_slot(int device) {
+  if (device < 0 || device >= kMaxScratchDevices) return nullptr;
+  void *base;
+  {
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    base = g_short_cnt_ptr[device];
+  }
+  if (!base) return nullptr;
+  return (uint32_t *)base + (g_short_next.fetch_add(1) % kShortSlots) * kShortMaxUnits;
+}
 }  // namespace
 }  // namespace bn
 
@@ -1360,8 +1459,9 @@ size_t bn_gqa_decode_workspace_size(int batch, int max_len, int n_heads, int hea
   if (batch <= 0 || max_len <= 0 || n_heads <= 0 || head_dim != HD) return 0;
   // n_split does not depend on n_kv_heads by more than the chunk choice; size
   // for the smallest chunk (most splits) so any n_kv_heads fits
-  const int64_t n_split = (max_len + 127) / 128;
-  return (size_t)batch * n_heads * n_split * (HD + 2) * sizeof(float);
+  int64_t n_split = (max_len + 127) / 128;
+  if (short_path_ok(BN_F32, batch, max_len, n_heads)) n_split = std::max<int64_t>(n_split, kShortSplits);
+  return (size_t)batch * n_heads * n_split * kDecRec * sizeof(float);
 }
 
 }  // extern "C"
@@ -1406,19 +1506,8 @@ int gqa_decode_impl(int dtype, const void *q, const void *k_cache, const void *v
   DecodeParams p;
   p.q = q; p.k = k_cache; p.v = v_cache; p.lens = seq_lens; p.o = o;
   p.batch = batch; p.max_len = max_len; p.n_heads = n_heads; p.n_kv_heads = n_kv_heads;
-  if (single_path(dtype, batch, max_len, n_heads)) {  // no partials: the workspace is unused
-    p.ws = nullptr;
-    p.n_split = 1;
-    p.chunk = max_len;
-    p.c = scale * 1.4426950408889634f;
-    int st = ensure_device();
-    if (st) return st;
-    hipStream_t s = as_stream(stream);
-    launch_single(p, s);
-    BN_LAUNCH_CHECK();
-    return BN_OK;
-  }
-  if (dtype == BN_BF16) {  // one workgroup per (sequence, KV head) when that fills the CUs
+  const bool short_split = short_path_ok(dtype, batch, max_len, n_heads);
+  if (!short_split && dtype == BN_BF16) {  // one workgroup per (sequence, KV head) when that fills the CUs
     int st = ensure_device();
     if (st) return st;
     const int cus = device_cu_count();
@@ -1439,11 +1528,16 @@ int gqa_decode_impl(int dtype, const void *q, const void *k_cache, const void *v
       return BN_OK;
     }
   }
-  // the whole-row kernel gives each workgroup 4 KV heads: 1/4 of the workgroups per chunk
-  p.chunk = rows_path(p, dtype == BN_BF16)
-                ? choose_chunk(batch, max_len, n_kv_heads / 4, kRowsMinWg)
-                : choose_chunk(batch, max_len, n_kv_heads, kMinWg);
-  p.n_split = (max_len + p.chunk - 1) / p.chunk;
+  if (short_split) {  // kShortSplits splits of the length; the combine derives the chunk
+    p.chunk = 0;
+    p.n_split = kShortSplits;
+  } else {
+    // the whole-row kernel gives each workgroup 4 KV heads: 1/4 of the workgroups per chunk
+    p.chunk = rows_path(p, dtype == BN_BF16)
+                  ? choose_chunk(batch, max_len, n_kv_heads / 4, kRowsMinWg)
+                  : choose_chunk(batch, max_len, n_kv_heads, kMinWg);
+    p.n_split = (max_len + p.chunk - 1) / p.chunk;
+  }
   p.c = scale * 1.4426950408889634f;
   const size_t need = (size_t)batch * n_heads * p.n_split * (HD + 2) * sizeof(float);
   if (noalloc && need > (size_t)BN_GQA_DECODE_SCRATCH_BYTES)
@@ -1467,7 +1561,19 @@ int gqa_decode_impl(int dtype, const void *q, const void *k_cache, const void *v
     own = true;
   }
   p.ws = (float *)ws;
-  st = dtype == BN_BF16 ? launch_decode<bf16_t>(p, G, s) : launch_decode<float>(p, G, s);
+  if (short_split) {  // one launch: the unit's last split merges its records
+    p.cnt = short_counter_slot(library_device());
+    if (!p.cnt) {
+      st = fail(BN_ERR_HIP, std::string(op) + ": split counters not set up for device " +
+                                std::to_string(library_device()));
+    } else {
+      launch_short(p, s);
+      const hipError_t e = hipGetLastError();
+      st = e == hipSuccess ? BN_OK : hip_fail(e, __FILE__, __LINE__);
+    }
+  } else {
+    st = dtype == BN_BF16 ? launch_decode<bf16_t>(p, G, s) : launch_decode<float>(p, G, s);
+  }
   if (own) {
     int st2 = bn_free(ws, stream);
     if (st == BN_OK) st = st2;

@@ -68,6 +68,11 @@ struct LinParams {
   const float *nd, *nw;
   float *nh_out;
   float neps;
+  // merged input of the output-major kernel (LinMerge): x is formed from a
+  // split decode's partial records
+  const float *mpart;
+  const int32_t *mlens;
+  int msplit, mmax_len, mlen;
 };
 
 // epilogues: EPI_PLAIN writes y (rotated in the first rope_cols columns);
@@ -374,8 +379,9 @@ constexpr int GV_ROUND = 8;    // 16-byte loads per weight row and lane in a rou
 constexpr int GV_XMAX = kGemvStagedMax; // fp32 elements of x in LDS: staged rows x padded k (64 KB)
 
 // NRM: x = rmsnorm(h + d) * w formed in the staging (one fp32 row of at
-// most kNormRowF32 elements: two 16-byte chunks per thread)
-template <typename T, int MR, int EPI, bool NRM = false>
+// most kNormRowF32 elements: two 16-byte chunks per thread).  MRG: x = the
+// merged attention output of a split short-cache decode (one fp32 row).
+template <typename T, int MR, int EPI, bool NRM = false, bool MRG = false>
 __global__ __launch_bounds__(256) void linear_gemv_t_kernel(LinParams p, RopeFreqs fr) {
   // [MR][kp], zeros past k; NRM: then h + d [kp]
   extern __shared__ __attribute__((aligned(16))) float gxs[];
@@ -524,6 +530,51 @@ __global__ __launch_bounds__(256) void linear_gemv_t_kernel(LinParams p, RopeFre
 #pragma unroll
         for (int e = 0; e < 4; ++e) o[e] = kk < p.k ? (v[u][e] * inv) * __uint_as_float(wr[u][e]) : 0.f;
         *(float4 *)(gxs + kk) = make_float4(o[0], o[1], o[2], o[3]);
+      }
+    }
+  } else if constexpr (MRG) {
+    // x[4c .. 4c+3] (query head 4c / 64, d = 4c mod 64) merged from the
+    // head's partial records exactly as decode_combine_kernel merges them
+    // (DecMerge), after the first weight round is requested.  The records'
+    // (m, l) pairs are gathered into LDS once per workgroup (every chunk of
+    // a head needs them); each thread requests its chunks' acc slices, two
+    // chunks per pass, before any merge.
+    static_assert(MR == 1 && sizeof(T) == 4, "the merged input is one fp32 row");
+    issue(a0, b0, 0);
+    const int cpr = kp / 4, nch = p.k / 4, S = p.msplit, nrec = (p.k >> 6) * S;
+    float *gml = gxs + kp;  // (m, l) of record r at gml[2r]
+    DecMerge mg[2];
+    auto acc_of = [&](int c0) __attribute__((always_inline)) {
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int kk = min(c0 + u * 256 + tid, nch - 1) * 4;  // in range: the merge is discarded
+        mg[u].load_acc8(p.mpart + (int64_t)(kk >> 6) * S * kDecRec, S, 0, kk & 63);
+      }
+    };
+    acc_of(0);
+    for (int r = tid; r < nrec; r += 256)
+      *(float2 *)(gml + 2 * r) = *(const float2 *)(p.mpart + (int64_t)r * kDecRec);
+    int len = p.mlen >= 0 ? p.mlen : p.mlens[0];
+    len = len < 0 ? 0 : (len > p.mmax_len ? p.mmax_len : len);
+    const int chunk = short_split_chunk(len, S);
+    const int nvalid = (len + chunk - 1) / chunk;
+    __syncthreads();
+    for (int c0 = 0; c0 < cpr; c0 += 512) {
+      if (c0 > 0) acc_of(c0);
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int c = c0 + u * 256 + tid;
+        const int kk = min(c, nch - 1) * 4;
+        const float *ml = gml + 2 * (kk >> 6) * S;
+        mg[u].load_ml8(ml, S, 0);
+        mg[u].start();
+        mg[u].merge8(0, nvalid);
+        for (int s0 = 8; s0 < nvalid; s0 += 8) {
+          mg[u].load_acc8(p.mpart + (int64_t)(kk >> 6) * S * kDecRec, S, s0, kk & 63);
+          mg[u].load_ml8(ml, S, s0);
+          mg[u].merge8(s0, nvalid);
+        }
+        if (c < cpr) *(float4 *)(gxs + c * 4) = c < nch ? mg[u].result() : make_float4(0.f, 0.f, 0.f, 0.f);
       }
     }
   } else {
@@ -675,7 +726,7 @@ namespace {
 int gemv_t_run(const bn_view *x, const bn_view *w, const bn_view *y, int rope_cols,
                int position_offset, int head_dim, const RopeFreqs &fr, int epi, float *k_dst,
                float *v_dst, int app_col, int app_w, int64_t app_rs, const LinNorm *nrm,
-               const char *op, void *stream) {
+               const LinMerge *mrg, const char *op, void *stream) {
   const int dt = x->dtype;
   const int64_t ve = dt == BN_BF16 ? 8 : 4;  // elements per 16 bytes
   const size_t es = dtype_size(dt);
@@ -703,6 +754,11 @@ int gemv_t_run(const bn_view *x, const bn_view *w, const bn_view *y, int rope_co
   if (k_dst && (dt != BN_F32 || app_col < 0 || app_col % 4 || app_w % 4 || app_col + 2 * app_w > n))
     return fail(BN_ERR_UNSUPPORTED, std::string(op) + ": bad K/V append columns");
   const char *hx = (const char *)x->data + x->offset * (int64_t)es;
+  if (mrg) {  // one fp32 row: n_heads * 64 merged attention outputs
+    if (nrm || dt != BN_F32 || m != 1 || k % 64 || !mrg->part || (!mrg->lens && mrg->len < 0) ||
+        mrg->n_split <= 0 || mrg->max_len <= 0 || kp + (int64_t)(k / 64) * mrg->n_split * 2 > GV_XMAX)
+      return fail(BN_ERR_UNSUPPORTED, std::string(op) + ": a merged input is one fp32 row of whole heads");
+  }
   if (nrm) {  // one fp32 row of h, staged in one pass; h_out written while h and d are read
     if (dt != BN_F32 || m != 1 || k < 4 || k > kNormRowF32 || !nrm->w)
       return fail(BN_ERR_UNSUPPORTED, std::string(op) + ": a normalised input is one fp32 row of 4.." +
@@ -732,7 +788,13 @@ int gemv_t_run(const bn_view *x, const bn_view *w, const bn_view *y, int rope_co
   if (nrm) {
     p.nd = nrm->d; p.nw = nrm->w; p.nh_out = nrm->h_out; p.neps = nrm->eps;
   }
-  const size_t lds = (size_t)(nrm ? 2 : mr) * kp * sizeof(float);
+  if (mrg) {
+    p.mpart = mrg->part; p.mlens = mrg->lens; p.msplit = mrg->n_split; p.mmax_len = mrg->max_len;
+    p.mlen = mrg->len;
+  }
+  // a merged input also holds every record's (m, l) pair
+  const size_t lds = (size_t)(nrm ? 2 : mr) * kp * sizeof(float) +
+                     (mrg ? (size_t)(k / 64) * mrg->n_split * 2 * sizeof(float) : 0);
   // four waves per workgroup, two weight rows (one output pair, or one
   // gate | up output) per wave
   const int waves = n / 2;
@@ -749,6 +811,9 @@ int gemv_t_run(const bn_view *x, const bn_view *w, const bn_view *y, int rope_co
   if (nrm) {
     if (epi == EPI_SILU) BN_GV(float, 1, EPI_SILU, true);
     else BN_GV(float, 1, EPI_PLAIN, true);
+  } else if (mrg) {
+    if (epi == EPI_SILU) BN_GV(float, 1, EPI_SILU, false, true);
+    else BN_GV(float, 1, EPI_PLAIN, false, true);
   } else if (dt == BN_F32) {
     if (epi == EPI_SILU) BN_GV_M(float, EPI_SILU);
     else BN_GV_M(float, EPI_PLAIN);
@@ -770,7 +835,7 @@ int gemv_t_run(const bn_view *x, const bn_view *w, const bn_view *y, int rope_co
 int linear_run(const bn_view *x, const bn_view *w, const bn_view *y, int rope_cols,
                int position_offset, int head_dim, float theta, void *workspace,
                size_t workspace_bytes, int epi, float *k_dst, float *v_dst, int app_col, int app_w,
-               int64_t app_rs, void *stream, const LinNorm *nrm) {
+               int64_t app_rs, void *stream, const LinNorm *nrm, const LinMerge *mrg) {
   const char *op = epi == EPI_SILU ? "Linear+SwiGLU" : "Linear";
   const unsigned mask = (1u << BN_F32) | (1u << BN_BF16);
   int st;
@@ -806,8 +871,9 @@ int linear_run(const bn_view *x, const bn_view *w, const bn_view *y, int rope_co
   // the few-rows streaming kernel without a k split
   if ((int64_t)w->h * w->w > 0 && w->stride_h == 1 && w->stride_w != 1)
     return gemv_t_run(x, w, y, rope_cols, position_offset, head_dim, fr, epi, k_dst, v_dst, app_col,
-                      app_w, app_rs, nrm, op, stream);
-  if (nrm) return fail(BN_ERR_UNSUPPORTED, std::string(op) + ": a normalised input needs an output-major w");
+                      app_w, app_rs, nrm, mrg, op, stream);
+  if (nrm || mrg)
+    return fail(BN_ERR_UNSUPPORTED, std::string(op) + ": a normalised or merged input needs an output-major w");
   if (!unit(x) || !unit(w) || !unit(y))
     return fail(BN_ERR_UNSUPPORTED, std::string(op) + ": rows must be contiguous (stride_w == 1)");
   if (!ok(x) || !ok(w) || !ok(y) || x->w % ve || y->w % ve)

@@ -218,6 +218,9 @@ extern "C" int bn_llama_decode(const bn_llama_config *c, const float *embed, con
   // first workgroup writes the other)
   float *const hdn2 = (float *)(W + pl.hdn2);
   const bool fold = om && hid <= kNormRowF32;
+  // short caches: the attention's split partials are merged by the O
+  // projection (output-major weights)
+  const bool merged = om && dec_ws && short_path_ok(BN_F32, 1, c->max_len, c->n_heads);
   for (int t = 0; st == BN_OK && t < n_tokens; ++t) {
     const int pos = position + t;
     hipLaunchKernelGGL(embed_gather_kernel, dim3(1), dim3(256), 0, s, embed,
@@ -247,11 +250,24 @@ extern "C" int bn_llama_decode(const bn_llama_config *c, const float *embed, con
                            L.v_cache + (int64_t)pos * kv, hid, kv, 0, stream, fold ? &n1 : nullptr)))
         break;
       if (fold && l) std::swap(hc, hn);
-      if ((st = bn_gqa_decode(BN_F32, qkv, L.k_cache, L.v_cache, lens + t, o, 1, c->max_len, c->n_heads,
-                              c->n_kv_heads, hd, scale, dec_ws, pl.dec_bytes, stream)))
-        break;
-      if ((st = bn_linear_rope(&v_o, &wo, &v_attn, 0, 0, hd, c->rope_theta, lin_ws, pl.lin_bytes, stream)))
-        break;
+      if (merged) {
+        // attention as split partials; the O projection merges them in its
+        // x staging (the bits of bn_gqa_decode's combine, one launch fewer)
+        // (the host knows the length: pos + 1 keys after the append)
+        const LinMerge mg = {(const float *)dec_ws, lens + t, kShortSplits, c->max_len, pos + 1};
+        if ((st = decode_short_partials(qkv, L.k_cache, L.v_cache, lens + t, pos + 1, (float *)dec_ws, 1,
+                                        c->max_len, c->n_heads, c->n_kv_heads, scale, s)))
+          break;
+        if ((st = linear_run(&v_o, &wo, &v_attn, 0, 0, hd, c->rope_theta, lin_ws, pl.lin_bytes, kLinEpiPlain,
+                             nullptr, nullptr, 0, 0, 0, stream, nullptr, &mg)))
+          break;
+      } else {
+        if ((st = bn_gqa_decode(BN_F32, qkv, L.k_cache, L.v_cache, lens + t, o, 1, c->max_len, c->n_heads,
+                                c->n_kv_heads, hd, scale, dec_ws, pl.dec_bytes, stream)))
+          break;
+        if ((st = bn_linear_rope(&v_o, &wo, &v_attn, 0, 0, hd, c->rope_theta, lin_ws, pl.lin_bytes, stream)))
+          break;
+      }
       // gate | up projection of rmsnorm(h + attention output); its epilogue
       // writes silu(gate) * up
       const LinNorm n2 = {attn, L.ln2, hn, c->rms_eps};

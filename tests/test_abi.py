@@ -190,6 +190,13 @@ def test_decode_workspace_size():
     n = L.bn_gqa_decode_workspace_size(64, 4096, 32, 64)
     assert n == 64 * 32 * 32 * 66 * 4
     assert L.bn_gqa_decode_workspace_size(64, 4096, 32, 128) == 0
+    # short caches (at most 1024 keys, at most 256 sequence x query-head
+    # pairs: the fp32 short-cache split) keep at least 4 split records per pair
+    assert L.bn_gqa_decode_workspace_size(1, 256, 32, 64) == 1 * 32 * 4 * 66 * 4
+    assert L.bn_gqa_decode_workspace_size(1, 640, 32, 64) == 1 * 32 * 5 * 66 * 4
+    assert L.bn_gqa_decode_workspace_size(4, 1024, 64, 64) == 4 * 64 * 8 * 66 * 4
+    assert L.bn_gqa_decode_workspace_size(1, 1025, 32, 64) == 1 * 32 * 9 * 66 * 4
+    assert L.bn_gqa_decode_workspace_size(9, 256, 32, 64) == 9 * 32 * 2 * 66 * 4
 
 
 def test_pool_bookkeeping_without_device():

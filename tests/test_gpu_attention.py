@@ -272,7 +272,7 @@ def test_decode_bf16_whole_cache_skewed_lengths(lens_kind):
                                               ("bf16", 2, 300, 32, 4), ("bf16", 80, 200, 16, 4)])
 def test_decode_ignores_cache_rows_past_len(dtype, Bn, L, H, Hkv):
     """Cache rows at or past a sequence's length hold NaN (memory the caller
-    never wrote): no kernel may let them reach the output (single-pass fp32,
+    never wrote): no kernel may let them reach the output (short-cache split fp32,
     split and per-KV-head bf16 paths)."""
     r = np.random.default_rng(Bn + L)
     lens = r.integers(1, L + 1, Bn).astype(np.int32)
@@ -315,6 +315,83 @@ def test_decode_workspace_reuse(dtype, Hkv):
             ref = O.gqa_decode(q[b:b + 1], kc[b:b + 1, :Lb], vc[b:b + 1, :Lb],
                                np.array([Lb], np.int32), 0.125)
             assert_close(got[b:b + 1], ref, TOL[dtype], f"call {call} b={b} len={Lb}")
+
+
+def test_decode_short_split_many_calls():
+    """fp32 short caches (config 4's decode): each (sequence, query head)'s
+    keys are cut into 4 splits and the unit's last split to arrive merges the
+    records in the same launch, counting on a slot of a 16-slot counter ring.
+    40 calls in a row (the ring wraps twice) with lengths that leave splits
+    empty (0..5 keys), cut lanes groups (63, 65) and the whole cache: every
+    call matches the oracle, and a call repeated later gives the same bits."""
+    H, Hkv, L = 32, 4, 640
+    Bn = 3
+    q = draw((Bn, H, 64), 90, "f32")
+    kc = draw((Bn, L, Hkv, 64), 91, "f32")
+    vc = draw((Bn, L, Hkv, 64), 92, "f32")
+    qd, kd, vd = dev(q, torch.float32), dev(kc, torch.float32), dev(vc, torch.float32)
+    pattern = [[0, 1, 2], [3, 4, 5], [63, 64, 65], [520, 576, 640], [1, 639, 17]]
+    first = {}
+    for call in range(40):
+        lens = pattern[call % len(pattern)]
+        got = host(B.gqa_decode(qd, kd, vd, torch.tensor(lens, dtype=torch.int32, device="cuda"),
+                                scale=0.125))
+        key = call % len(pattern)
+        if key in first:
+            assert np.array_equal(got, first[key]), f"call {call}: not the bits of call {key}"
+            continue
+        first[key] = got
+        for b, Lb in enumerate(lens):
+            if Lb == 0:
+                assert np.all(got[b] == 0.0)
+                continue
+            ref = O.gqa_decode(q[b:b + 1], kc[b:b + 1, :Lb], vc[b:b + 1, :Lb],
+                               np.array([Lb], np.int32), 0.125)
+            assert_close(got[b:b + 1], ref, FP32_TOL, f"call {call} b={b} len={Lb}")
+
+
+def test_decode_short_split_graph_replays():
+    """The short-cache decode captured in a HIP graph (as bench.py replays a
+    generate's decode launches): three calls on three caches per replay, five
+    replays with eager work and synchronisations between them; every replay
+    equals the eager result bit for bit (the split counters return to zero
+    at the end of each launch, so replays reuse their slots)."""
+    H, Hkv, L = 32, 4, 640
+    lens_list = [[577], [640], [1]]
+    cases = []
+    for i, lens in enumerate(lens_list):
+        q = dev(draw((1, H, 64), 100 + i, "f32"), torch.float32)
+        kc = dev(draw((1, L, Hkv, 64), 110 + i, "f32"), torch.float32)
+        vc = dev(draw((1, L, Hkv, 64), 120 + i, "f32"), torch.float32)
+        ld = torch.tensor(lens, dtype=torch.int32, device="cuda")
+        o = torch.empty((1, H, 64), device="cuda")
+        ws = B.decode_workspace(1, L, H)
+        cases.append((q, kc, vc, ld, o, ws))
+
+    def calls():
+        for q, kc, vc, ld, o, ws in cases:
+            B.gqa_decode(q, kc, vc, ld, o=o, scale=0.125, workspace=ws)
+
+    calls()
+    torch.cuda.synchronize()
+    eager = [c[4].clone() for c in cases]
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            calls()
+    torch.cuda.synchronize()
+    for rep in range(5):
+        for c in cases:
+            c[4].fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        for i, c in enumerate(cases):
+            assert torch.equal(c[4], eager[i]), f"replay {rep} call {i}"
+        calls()  # eager work between the replays
+        torch.cuda.synchronize()
+        for i, c in enumerate(cases):
+            assert torch.equal(c[4], eager[i]), f"eager after replay {rep} call {i}"
 
 
 @pytest.mark.parametrize("dtype,H,Hkv,L", [("bf16", 32, 4, 3000),   # whole-row split kernel

@@ -9,7 +9,7 @@ compares every element with the oracle:
   with one and two row tiles per wave run; ragged row and key tails; causal
   offsets below zero, at Skv - Sq and past it; non-causal; the row
   log-sum-exp beside the output;
-* decode: every kernel the host can pick (fp32 single pass, fp32 split-K,
+* decode: every kernel the host can pick (fp32 short-cache split, fp32 split-K,
   bf16 one workgroup per (sequence, KV head), bf16 split rows, bf16 split
   MFMA), with lengths 0, 1, max_len and past max_len among the random ones;
 * backward (bf16): random groups, offsets and both mask modes;
@@ -113,19 +113,19 @@ CUS = 256   # MI355X compute units: B * Hkv at or above this takes the whole-cac
 def decode_path(dtype, Bn, L, H, Hkv):
     """The kernel the host picks (mirrors the launch rules of bn_gqa_decode)."""
     if dtype == "f32":
-        return "f32_single" if L <= 1024 and Bn * H <= 256 else "f32_split"
+        return "f32_short" if L <= 1024 and Bn * H <= 256 else "f32_split"
     if Bn * Hkv >= CUS:
         return "bf16_whole"
     return "bf16_rows" if Hkv % 4 == 0 else "bf16_mfma"
 
 
-DECODE_TARGETS = ["f32_single", "f32_split", "bf16_whole", "bf16_rows", "bf16_mfma"]
+DECODE_TARGETS = ["f32_short", "f32_split", "bf16_whole", "bf16_rows", "bf16_mfma"]
 
 
 def decode_case(target, i):
     rng = np.random.default_rng(8000 + 97 * DECODE_TARGETS.index(target) + i)
     G = int(rng.choice([1, 2, 4, 8]))
-    if target == "f32_single":
+    if target == "f32_short":
         dtype, Hkv, L = "f32", int(rng.choice([1, 2, 4])), int(rng.integers(1, 1025))
         Bn = int(rng.integers(1, max(2, 256 // (G * Hkv)) + 1))
     elif target == "f32_split":

@@ -3,7 +3,7 @@
 It runs bn_gqa_decode's kernels with the split-K partials in a file-scope
 device array instead of a workspace, so its output must equal
 bn_gqa_decode's bit for bit on every path (bf16 whole-cache, bf16 whole-row
-split, bf16 per-KV-head split, fp32 split, fp32 single pass), over two calls
+split, bf16 per-KV-head split, fp32 split, fp32 short-cache split), over two calls
 in a row where the second is smaller and finds the first call's partials
 still in the array.  The pool's allocation count must not move.  (The
 refusal of partials larger than the array is a host-side check, tested
