@@ -54,11 +54,9 @@ namespace {
 
 constexpr int HD = 64;
 constexpr int NT = 8;  // keys per lane group between softmax rescales
-// single pass: 10 keys per lane group, up to 640 keys (16 waves x 4 groups x
-// 10) in one load round (3-6% faster than 8 at config 4's lengths)
-constexpr int kSingleNT = 10;
-// short-cache split (DEC_SHORT): keys per lane group per round, waves per
-// workgroup and query heads per workgroup
+// short-cache split (DEC_SHORT): keys per lane group per round (one round
+// covers a 640-key cache's 160-key splits: 4 waves x 4 lane groups x 10),
+// waves per workgroup and query heads per workgroup
 constexpr int kShortNT = 10, kShortWV = 4, kShortG = 1;
 
 template <typename T> struct DecVec;
@@ -107,9 +105,6 @@ struct DecodeParams {
 //   DEC_SPLIT: one workgroup per (sequence, KV head, chunk of p.chunk keys)
 //     serving the KV head's G query heads; the waves interleave blocks of
 //     KPI*NT keys over the chunk; writes the chunk's partial records.
-//   DEC_SINGLE (G = 1): one workgroup per (sequence, query head) covers the
-//     whole cache of its KV head (each wave a contiguous key range) and
-//     writes the output itself -- no partials, no combine launch.
 //   DEC_SHORT: one workgroup per (sequence, G query heads of one KV head,
 //     split); split s takes keys [s*chunk, (s+1)*chunk) of the sequence's
 //     length with chunk = short_split_chunk(len, n_split), each wave a
@@ -117,15 +112,15 @@ struct DecodeParams {
 //     and few sequences, where one workgroup per query head is bound by what
 //     one compute unit can stream (every workgroup reads the whole cache).
 // The workgroups that read the same cache rows (the query heads of one KV
-// head, in SINGLE and SHORT) get consecutive unit numbers, and units are
+// head, in SHORT) get consecutive unit numbers, and units are
 // numbered so that consecutive ones go to one XCD (workgroups are dealt to
 // the 8 XCDs in turn): they read those rows from one L2.
-constexpr int DEC_SPLIT = 0, DEC_SINGLE = 1, DEC_SHORT = 2;
+constexpr int DEC_SPLIT = 0, DEC_SHORT = 1;
 template <typename T, int G, int WV, int MODE>
 __global__ __launch_bounds__(64 * WV) void decode_split_kernel(DecodeParams p) {
-  constexpr bool SINGLE = MODE == DEC_SINGLE, CONTIG = MODE != DEC_SPLIT;
+  constexpr bool CONTIG = MODE == DEC_SHORT;
   constexpr int VEC = DecVec<T>::VEC;
-  constexpr int NT = MODE == DEC_SHORT ? kShortNT : (SINGLE ? kSingleNT : bn::NT);
+  constexpr int NT = CONTIG ? kShortNT : bn::NT;
   constexpr int LPK = HD / VEC;  // lanes per key
   constexpr int KPI = 64 / LPK;  // keys per wave per load instruction
   __shared__ float red_m[WV][G], red_l[WV][G];
@@ -134,7 +129,6 @@ __global__ __launch_bounds__(64 * WV) void decode_split_kernel(DecodeParams p) {
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int sub = lane % LPK;  // 16-byte slice of the key row
   const int grp = lane / LPK;  // key slot within the wave
-  static_assert(!SINGLE || G == 1, "single pass: one query head per workgroup");
   int u = blockIdx.x;
   if (CONTIG && (gridDim.x & 7) == 0) u = (blockIdx.x & 7) * (gridDim.x >> 3) + (blockIdx.x >> 3);
   int b, g, h0, split = 0;
@@ -144,10 +138,6 @@ __global__ __launch_bounds__(64 * WV) void decode_split_kernel(DecodeParams p) {
     b = bg / p.n_kv_heads;
     g = bg % p.n_kv_heads;
     h0 = g * G;
-  } else if constexpr (SINGLE) {
-    b = u / p.n_heads;
-    h0 = u % p.n_heads;
-    g = h0 / (p.n_heads / p.n_kv_heads);
   } else {  // units (sequence, KV head, split, query-head group), the last fastest
     const int qpg = p.n_heads / p.n_kv_heads / G;  // query-head groups per KV head
     const int qg = u % qpg;
@@ -169,20 +159,15 @@ __global__ __launch_bounds__(64 * WV) void decode_split_kernel(DecodeParams p) {
   }
   int len = p.hlen >= 0 ? p.hlen : p.lens[b];
   len = len < 0 ? 0 : (len > p.max_len ? p.max_len : len);
-  if (SINGLE && len == 0) {  // no key: zeros
-    for (int idx = tid; idx < G * HD; idx += 64 * WV)
-      Elem<T>::store((T *)p.o + ((int64_t)b * p.n_heads + h0) * HD + idx, 0.f);
-    return;
-  }
   const int chunk = MODE == DEC_SHORT ? short_split_chunk(len, p.n_split) : p.chunk;
-  const int k_begin = SINGLE ? 0 : split * chunk;
+  const int k_begin = split * chunk;
   if (k_begin >= len) {  // the combine ignores chunks past len
     if (MODE == DEC_SHORT && p.cnt && len == 0 && split == 0)  // no key, no merge: zeros
       for (int idx = tid; idx < G * HD; idx += 64 * WV)
         Elem<T>::store((T *)p.o + ((int64_t)b * p.n_heads + h0) * HD + idx, 0.f);
     return;
   }
-  const int k_end = SINGLE ? len : min(k_begin + chunk, len);
+  const int k_end = min(k_begin + chunk, len);
   // CONTIG: wave w takes keys [kw0, kw1), a contiguous range; else the waves
   // interleave blocks of KPI*NT keys over the chunk
   const int per = ((k_end - k_begin + WV - 1) / WV + KPI - 1) / KPI * KPI;
@@ -222,8 +207,7 @@ __global__ __launch_bounds__(64 * WV) void decode_split_kernel(DecodeParams p) {
     }
     // contiguous ranges: every load of the round is issued before any is
     // consumed.  Left alone, the scheduler trades them for registers (load,
-    // wait, use, next: ten round trips); 116 VGPRs still fit 16 waves per
-    // workgroup.
+    // wait, use, next: one round trip per key).
     if constexpr (CONTIG) __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
@@ -292,8 +276,7 @@ __global__ __launch_bounds__(64 * WV) void decode_split_kernel(DecodeParams p) {
   }
   __syncthreads();
 
-  // merge the waves and write this chunk's partial (m, l, acc[HD]) per head,
-  // or (SINGLE) the output
+  // merge the waves and write this chunk's partial (m, l, acc[HD]) per head
   for (int idx = tid; idx < G * HD; idx += 64 * WV) {
     const int h = idx / HD, d = idx % HD;
     float M = red_m[0][h];
@@ -306,10 +289,6 @@ __global__ __launch_bounds__(64 * WV) void decode_split_kernel(DecodeParams p) {
       const float f = __builtin_amdgcn_exp2f(red_m[w2][h] - Mu);
       L += red_l[w2][h] * f;
       A += red_o[w2][h][d] * f;
-    }
-    if (SINGLE) {
-      Elem<T>::store((T *)p.o + ((int64_t)b * p.n_heads + h0 + h) * HD + d, A / L);
-      continue;
     }
     float *part = p.ws + (((int64_t)b * p.n_heads + h0 + h) * p.n_split + split) * kDecRec;
     if (MODE == DEC_SHORT && p.cnt) {  // through to memory: another workgroup merges them

@@ -25,8 +25,11 @@ the concatenated gate/up, down and lm_head -- on bn_linear_rope's
 output-major few-rows kernel (one pass over each weight, no k split), with
 the Q/K rotation fused into the QKV projection; the prompt runs the library
 GEMM (torch) and rotates the Q and K columns in place in one bn_rope launch.  The embedding gather is a torch GPU
-operation.  The config's metric times the attention, RoPE (standalone or
-fused into the decode QKV projection) and RMSNorm kernels.  ``path_ms`` accumulates hip-event time around those
+operation.  The config's metric is the device time of the attention
+(prefill and decode), standalone RoPE (the prompt's bn_rope) and RMSNorm
+kernels; the decode steps' QKV projection, which carries their rotation in
+its epilogue, is logged as its own kind (qkv_rope) and reported beside the
+metric, not in it.  ``path_ms`` accumulates hip-event time around the logged
 kernel launches (an upper bound on their device time; the rocprofv3 kernel
 trace gives the exact per-kernel durations).
 """
