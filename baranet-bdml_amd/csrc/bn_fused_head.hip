@@ -39,6 +39,8 @@
 // (launch, Q and the first tile's K/V, output) and ~3.5 us per tile, of
 // which the dot products take ~0.9 and P.V ~0.4; the rest is the 128 KB of
 // K and V each workgroup pulls per tile through one CU.
+#include <algorithm>
+
 #include "bn_common.hpp"
 
 namespace bn {
@@ -281,6 +283,241 @@ __global__ __launch_bounds__(256) void fused_head_attention_kernel(FusedHeadPara
   }
 }
 
+// ------------------------------------------------------- matrix-core path
+// Longer prompts (seq_q >= kMfmaMinRows) with KV*D = 256 (TinyLLaMA's 4 KV
+// heads of 64) run the same chain on v_mfma_f32_32x32x2f32, in three
+// launches:
+//   1. fh_qsum_kernel: Qs[i][c] = c2 * sum_{r < n_rep} Q_{g*n_rep + r}[i][d]
+//      (c = g*D + d, summed in r order; c2 = scale * log2 e, so the scores
+//      come out in log2 units), [seq_q, 256] in the workspace.
+//   2. fh_mfma_kernel: one workgroup per block of 32 query rows x 128 keys.
+//      Wave w forms S^T = K.Qs^T of the block's four 32-key tiles over its
+//      quarter (64 columns) of the contraction; the four quarters meet in LDS
+//      and are summed in wave order, so every wave holds the same 128 x 32
+//      scores.  Each wave masks them, takes the block's row max m, forms
+//      P = exp2(s - m) and l = sum P, and O[:, 64w .. 64w+63] = P.V for its
+//      quarter of the value columns (P straight from the score registers as
+//      the B operand).  The block writes its record (m, l, O[32][256]).
+//   3. fh_merge_kernel: each query row merges the records of its row tile
+//      (max of m, exp2-weighted sums of l and O), normalises, and writes the
+//      values of KV head g to the row's n_rep heads of group g.
+// Per block a wave runs 128 MFMAs for S and 128 for P.V; the blocks of a
+// prompt spread over every compute unit, where the VALU kernel's longest
+// rows walk every key tile on one compute unit each.
+constexpr int kMfmaMinRows = 512;  // shorter prompts: the VALU kernel (faster at 256 rows)
+constexpr int FH_KVD = 256, FH_ROWS = 32, FH_KEYS = 128;
+constexpr int FH_REC = 2 * FH_ROWS + FH_ROWS * FH_KVD;  // m[32], l[32], O[32][256]
+
+typedef float fh_f32x16 __attribute__((ext_vector_type(16)));
+
+struct FhParams {
+  const float *q, *k, *v;
+  float *o, *qs, *part;
+  int64_t ldq, ldk, ldv, ldo;
+  int sq, sk, n_heads, head_dim, n_rep, n_kc, causal, seq_offset;
+  float c2;  // scale * log2(e)
+};
+
+// visible keys of query row `row`: [0, key_end)
+__device__ __forceinline__ int fh_key_end(const FhParams &p, int row) {
+  if (!p.causal) return p.sk;
+  const int64_t e = (int64_t)row + p.seq_offset + 1;
+  return (int)(e < 0 ? 0 : (e > p.sk ? p.sk : e));
+}
+
+__global__ __launch_bounds__(256) void fh_qsum_kernel(FhParams p) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (int64_t)p.sq * (FH_KVD / 4)) return;
+  const int row = (int)(idx / (FH_KVD / 4)), c = (int)(idx % (FH_KVD / 4)) * 4;
+  const int g = c / p.head_dim, d = c - g * p.head_dim;
+  const float *qr = p.q + (int64_t)row * p.ldq + (int64_t)g * p.n_rep * p.head_dim + d;
+  float4 a = ld4(qr);
+  for (int r = 1; r < p.n_rep; ++r) {
+    const float4 b = ld4(qr + (int64_t)r * p.head_dim);
+    a.x += b.x; a.y += b.y; a.z += b.z; a.w += b.w;
+  }
+  *reinterpret_cast<float4 *>(p.qs + (int64_t)row * FH_KVD + c) =
+      make_float4(a.x * p.c2, a.y * p.c2, a.z * p.c2, a.w * p.c2);
+}
+
+__global__ __launch_bounds__(256, 2) void fh_mfma_kernel(FhParams p) {
+  // the four waves' partial scores: [wave][key tile][register group][lane]
+  __shared__ float4 sbuf[4][4][4][64];
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  const int r32 = lane & 31, hf = lane >> 5;
+  const int kc = blockIdx.x % p.n_kc, rt = blockIdx.x / p.n_kc;
+  const int row0 = rt * FH_ROWS, key0 = kc * FH_KEYS;
+  const int kend_tile = fh_key_end(p, min(row0 + FH_ROWS - 1, p.sq - 1));
+  if (key0 >= kend_tile) return;  // no record: the merge counts the blocks the same way
+
+  // B operand of S^T: query row0 + r32, contraction slot (4u + e, hf) =
+  // column 64w + 8u + 4hf + e of Qs (rows past seq_q: zeros)
+  const int qrow = row0 + r32;
+  float qreg[32];
+#pragma unroll
+  for (int u = 0; u < 8; ++u) {
+    const float4 a = qrow < p.sq ? ld4(p.qs + (int64_t)qrow * FH_KVD + 64 * w + 8 * u + 4 * hf) : zero4();
+    qreg[4 * u] = a.x; qreg[4 * u + 1] = a.y; qreg[4 * u + 2] = a.z; qreg[4 * u + 3] = a.w;
+  }
+  // A operand: key key0 + 32kt + r32 (clamped into the cache; masked below),
+  // the same contraction columns
+  auto load_k = [&](int kt, float4 (&kr)[8]) __attribute__((always_inline)) {
+    const int key = min(key0 + 32 * kt + r32, p.sk - 1);
+    const float *kp = p.k + (int64_t)key * p.ldk + 64 * w + 4 * hf;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) kr[u] = ld4(kp + 8 * u);
+  };
+  fh_f32x16 s[4];
+#pragma unroll
+  for (int kt = 0; kt < 4; ++kt) {
+    float4 cur[8];
+    load_k(kt, cur);
+    s[kt] = fh_f32x16{};
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      s[kt] = __builtin_amdgcn_mfma_f32_32x32x2f32(cur[u].x, qreg[4 * u], s[kt], 0, 0, 0);
+      s[kt] = __builtin_amdgcn_mfma_f32_32x32x2f32(cur[u].y, qreg[4 * u + 1], s[kt], 0, 0, 0);
+      s[kt] = __builtin_amdgcn_mfma_f32_32x32x2f32(cur[u].z, qreg[4 * u + 2], s[kt], 0, 0, 0);
+      s[kt] = __builtin_amdgcn_mfma_f32_32x32x2f32(cur[u].w, qreg[4 * u + 3], s[kt], 0, 0, 0);
+    }
+  }
+  // the quarters of the contraction meet in LDS, summed in wave order
+#pragma unroll
+  for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+      sbuf[w][kt][g][lane] = make_float4(s[kt][4 * g], s[kt][4 * g + 1], s[kt][4 * g + 2], s[kt][4 * g + 3]);
+  __syncthreads();
+#pragma unroll
+  for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      float4 a = sbuf[0][kt][g][lane];
+#pragma unroll
+      for (int w2 = 1; w2 < 4; ++w2) {
+        const float4 b = sbuf[w2][kt][g][lane];
+        a.x += b.x; a.y += b.y; a.z += b.z; a.w += b.w;
+      }
+      s[kt][4 * g] = a.x; s[kt][4 * g + 1] = a.y; s[kt][4 * g + 2] = a.z; s[kt][4 * g + 3] = a.w;
+    }
+
+  // mask, row max, P = exp2(s - m), row sum; register i of s[kt] is key
+  // key0 + 32kt + 8(i/4) + 4hf + i%4 of query qrow
+  const int kend_row = qrow < p.sq ? fh_key_end(p, qrow) : 0;
+  float mx = -INFINITY;
+#pragma unroll
+  for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int key = key0 + 32 * kt + 8 * (i >> 2) + 4 * hf + (i & 3);
+      const float v = key < kend_row ? s[kt][i] : -INFINITY;
+      s[kt][i] = v;
+      mx = fmaxf(mx, v);
+    }
+  mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+  const float mu = mx == -INFINITY ? 0.f : mx;
+  float l = 0.f;
+#pragma unroll
+  for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const float e = __builtin_amdgcn_exp2f(s[kt][i] - mu);
+      s[kt][i] = e;
+      l += e;
+    }
+  l += __shfl_xor(l, 32, 64);
+
+  // O^T[value column][query] += V^T P^T over the block's keys: A = V^T (lane:
+  // column slot r32 of tile dt = value column 64w + 2*r32 + dt, key of the
+  // step's half hf), B = P^T (the score registers)
+  fh_f32x16 o[2] = {fh_f32x16{}, fh_f32x16{}};
+  auto load_v = [&](int kt, float2 (&vr)[16]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int key = min(key0 + 32 * kt + 8 * g + 4 * hf + e, p.sk - 1);
+        vr[4 * g + e] = *reinterpret_cast<const float2 *>(p.v + (int64_t)key * p.ldv + 64 * w + 2 * r32);
+      }
+  };
+#pragma unroll
+  for (int kt = 0; kt < 4; ++kt) {
+    float2 cur[16];
+    load_v(kt, cur);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      o[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(cur[i].x, s[kt][i], o[0], 0, 0, 0);
+      o[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(cur[i].y, s[kt][i], o[1], 0, 0, 0);
+    }
+  }
+
+  // the block's record: m and l per query (wave 0), O[query][column]:
+  // register i of o[dt] is column 64w + 2*(8(i/4) + 4hf + i%4) + dt of query qrow
+  float *rec = p.part + (int64_t)blockIdx.x * FH_REC;
+  if (w == 0 && hf == 0) {
+    rec[r32] = mx;
+    rec[FH_ROWS + r32] = l;
+  }
+  float *orow = rec + 2 * FH_ROWS + r32 * FH_KVD + 64 * w;
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const int c0 = 2 * (8 * g + 4 * hf);
+    *reinterpret_cast<float4 *>(orow + c0) = make_float4(o[0][4 * g], o[1][4 * g], o[0][4 * g + 1], o[1][4 * g + 1]);
+    *reinterpret_cast<float4 *>(orow + c0 + 4) =
+        make_float4(o[0][4 * g + 2], o[1][4 * g + 2], o[0][4 * g + 3], o[1][4 * g + 3]);
+  }
+}
+
+__global__ __launch_bounds__(256) void fh_merge_kernel(FhParams p) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (int64_t)p.sq * (FH_KVD / 4)) return;
+  const int row = (int)(idx / (FH_KVD / 4)), c = (int)(idx % (FH_KVD / 4)) * 4;
+  const int rt = row / FH_ROWS, r = row % FH_ROWS;
+  const int kend_tile = fh_key_end(p, min(rt * FH_ROWS + FH_ROWS - 1, p.sq - 1));
+  const int nblk = (kend_tile + FH_KEYS - 1) / FH_KEYS;  // the blocks that wrote a record
+  const float *rec0 = p.part + (int64_t)rt * p.n_kc * FH_REC;
+  // records four at a time, their loads issued together (slots past nblk
+  // read the last record and are skipped by a select)
+  float M = -INFINITY;
+  for (int b = 0; b < nblk; b += 4) {
+    float m4[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) m4[j] = rec0[(int64_t)min(b + j, nblk - 1) * FH_REC + r];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) M = b + j < nblk ? fmaxf(M, m4[j]) : M;
+  }
+  float4 out = zero4();
+  if (M != -INFINITY) {  // a row with no visible key: the chain's P row is all 0
+    float L = 0.f;
+    float4 A = zero4();
+    for (int b = 0; b < nblk; b += 4) {
+      float m4[4], l4[4];
+      float4 a4[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float *rec = rec0 + (int64_t)min(b + j, nblk - 1) * FH_REC;
+        m4[j] = rec[r];
+        l4[j] = rec[FH_ROWS + r];
+        a4[j] = ld4(rec + 2 * FH_ROWS + r * FH_KVD + c);
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if (b + j >= nblk) break;
+        const float f = __builtin_amdgcn_exp2f(m4[j] - M);  // a block the row cannot see: 0
+        L = fmaf(l4[j], f, L);
+        A.x = fmaf(a4[j].x, f, A.x); A.y = fmaf(a4[j].y, f, A.y);
+        A.z = fmaf(a4[j].z, f, A.z); A.w = fmaf(a4[j].w, f, A.w);
+      }
+    }
+    const float inv = 1.f / L;
+    out = make_float4(A.x * inv, A.y * inv, A.z * inv, A.w * inv);
+  }
+  // KV head g's values go to the n_rep heads of group g
+  const int g = c / p.head_dim, d = c - g * p.head_dim;
+  float *orow = p.o + (int64_t)row * p.ldo + (int64_t)g * p.n_rep * p.head_dim + d;
+  for (int h = 0; h < p.n_rep; ++h) *reinterpret_cast<float4 *>(orow + (int64_t)h * p.head_dim) = out;
+}
+
 // A view the kernel can read with float4 loads: fp32, columns contiguous,
 // every row on a 16-byte boundary.
 bool vec4_rows(const bn_view *v) { return rows_aligned(v, 16); }
@@ -319,6 +556,42 @@ extern "C" int bn_fused_head_attention(const bn_view *q, const bn_view *k, const
                 std::string(op) + ": views need contiguous columns and rows on 16-byte boundaries");
   if ((st = ensure_device())) return st;
   if (q->h == 0) return BN_OK;
+  if (kvd == FH_KVD && q->h >= kMfmaMinRows) {  // the matrix-core path
+    FhParams f;
+    f.q = reinterpret_cast<const float *>(q->data) + q->offset;
+    f.k = reinterpret_cast<const float *>(k->data) + k->offset;
+    f.v = reinterpret_cast<const float *>(v->data) + v->offset;
+    f.o = reinterpret_cast<float *>(o->data) + o->offset;
+    f.ldq = q->stride_h; f.ldk = k->stride_h; f.ldv = v->stride_h; f.ldo = o->stride_h;
+    f.sq = q->h; f.sk = k->h;
+    f.n_heads = n_heads; f.head_dim = head_dim; f.n_rep = n_heads / n_kv_heads;
+    f.n_kc = (k->h + FH_KEYS - 1) / FH_KEYS;
+    f.causal = causal ? 1 : 0;
+    f.seq_offset = seq_offset;
+    f.c2 = scale * 1.4426950408889634f;
+    const int n_rt = (q->h + FH_ROWS - 1) / FH_ROWS;
+    const size_t qs_bytes = (size_t)q->h * FH_KVD * sizeof(float);
+    const size_t part_bytes = (size_t)n_rt * std::max(f.n_kc, 1) * FH_REC * sizeof(float);
+    void *ws = nullptr;
+    if ((st = bn_alloc(&ws, qs_bytes + part_bytes, stream))) return st;
+    f.qs = (float *)ws;
+    f.part = (float *)((char *)ws + qs_bytes);
+    hipStream_t s = as_stream(stream);
+    const unsigned nvec = (unsigned)(((int64_t)q->h * (FH_KVD / 4) + 255) / 256);
+    hipLaunchKernelGGL(fh_qsum_kernel, dim3(nvec), dim3(256), 0, s, f);
+    hipError_t e = hipGetLastError();
+    if (e == hipSuccess && f.n_kc > 0) {
+      hipLaunchKernelGGL(fh_mfma_kernel, dim3((unsigned)(n_rt * f.n_kc)), dim3(256), 0, s, f);
+      e = hipGetLastError();
+    }
+    if (e == hipSuccess) {
+      hipLaunchKernelGGL(fh_merge_kernel, dim3(nvec), dim3(256), 0, s, f);
+      e = hipGetLastError();
+    }
+    st = e == hipSuccess ? BN_OK : hip_fail(e, __FILE__, __LINE__);
+    const int st2 = bn_free(ws, stream);
+    return st ? st : st2;
+  }
   FusedHeadParams p;
   p.q = reinterpret_cast<const float *>(q->data) + q->offset;
   p.k = reinterpret_cast<const float *>(k->data) + k->offset;

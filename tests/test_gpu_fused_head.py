@@ -43,7 +43,8 @@ def run(q, k, v, H, Hkv, D, sc, causal, off, out=None):
     (7, 7, 32, 4, 64, True, -3),         # rows 0..2 see no key: zeros
     (33, 33, 8, 8, 64, True, 0),         # n_rep 1, KV*D = 512 (the limit)
     (20, 20, 4, 1, 64, True, 2),         # one KV head: KV*D = 64
-    (512, 512, 32, 4, 64, True, 0),      # the 512-token prompt of config 4
+    (512, 512, 32, 4, 64, True, 0),      # the 512-token prompt of config 4 (matrix-core path)
+    (511, 511, 32, 4, 64, True, 0),      # the longest prompt of the VALU kernel
     (50, 50, 12, 4, 4, True, 0),         # head_dim 4
 ])
 def test_fused_head_attention(Sq, Sk, H, Hkv, D, causal, off):
@@ -105,3 +106,67 @@ def test_fused_head_attention_rejects_misaligned_rows():
     with pytest.raises(RuntimeError, match="16-byte"):
         B.call("bn_fused_head_attention", V(q2[:, 1:]), V(k), V(k), V(out), 32, 4, 64, 0.125, 1,
                0, None)
+
+
+@pytest.mark.parametrize("Sq,Sk,H,Hkv,causal,off", [
+    (600, 1100, 32, 4, False, 0),   # non-causal, ragged row tile and key block
+    (700, 700, 16, 4, True, 0),     # n_rep 4
+    (530, 800, 32, 4, True, 270),   # rows at positions 270..799 of an 800-key context
+    (560, 560, 32, 4, True, -40),   # rows 0..39 see no key: zeros
+])
+def test_fused_head_attention_matrix_core_rows(Sq, Sk, H, Hkv, causal, off):
+    """The matrix-core path (seq_q >= 512, KV*D = 256): the whole output
+    computed, 64-row blocks at both ends checked against the oracle chain on
+    the same rows (a block starting at row i0 sits at position i0 + off)."""
+    D = 64
+    r = np.random.default_rng(Sq * 7 + Sk)
+    q = r.standard_normal((Sq, H * D)).astype(np.float32)
+    k = r.standard_normal((Sk, Hkv * D)).astype(np.float32)
+    v = r.standard_normal((Sk, Hkv * D)).astype(np.float32)
+    got = host(run(dev(q), dev(k), dev(v), H, Hkv, D, 0.125, causal, off))
+    assert np.isfinite(got).all()
+    if off < 0:
+        assert not got[:-off].any()
+    for i0 in (max(0, -off), Sq - 64):
+        ref = O.fused_head_attention(q[i0:i0 + 64], k, v, D, H // Hkv, 0.125, causal, i0 + off)
+        assert_close(got[i0:i0 + 64], ref, FP32_TOL, f"rows {i0}..{i0 + 63}")
+
+
+@pytest.mark.parametrize("S", [2048])
+def test_fused_head_attention_long_prompt_blocks(S):
+    """The matrix-core path at S = 2048 (TinyLLaMA's heads): 64-row blocks at
+    the start, middle and end of the causal output against the oracle chain
+    on the same rows (rows i0.. at positions i0.. see keys 0..i0+r), and
+    every row of the output finite."""
+    H, Hkv, D = 32, 4, 64
+    r = np.random.default_rng(2048)
+    q = r.standard_normal((S, H * D)).astype(np.float32)
+    k = r.standard_normal((S, Hkv * D)).astype(np.float32)
+    v = r.standard_normal((S, Hkv * D)).astype(np.float32)
+    got = host(run(dev(q), dev(k), dev(v), H, Hkv, D, 0.125, True, 0))
+    assert np.isfinite(got).all()
+    for i0 in (0, 1000, S - 64):
+        ref = O.fused_head_attention(q[i0:i0 + 64], k[:i0 + 64], v[:i0 + 64], D, H // Hkv, 0.125,
+                                     True, i0)
+        assert_close(got[i0:i0 + 64], ref, FP32_TOL, f"S={S} rows {i0}..{i0 + 63}")
+
+
+def test_fused_head_attention_matrix_core_views_and_repeats():
+    """The matrix-core path on packed column views of one QKV buffer, into a
+    column slice of a wider output (columns outside untouched), and the same
+    bits on a repeated call."""
+    S, H, Hkv, D = 540, 32, 4, 64
+    r = np.random.default_rng(7)
+    qkv = r.standard_normal((S, (H + 2 * Hkv) * D)).astype(np.float32)
+    q, k, v = qkv[:, :H * D], qkv[:, H * D:(H + Hkv) * D], qkv[:, (H + Hkv) * D:]
+    d = dev(qkv)
+    big = torch.full((S, H * D + 64), float("nan"), device="cuda")
+    out = big[:, 32:32 + H * D]
+    args = (d[:, :H * D], d[:, H * D:(H + Hkv) * D], d[:, (H + Hkv) * D:], H, Hkv, D, 0.125, True, 0)
+    run(*args, out=out)
+    got = host(big)
+    ref = O.fused_head_attention(q, k, v, D, H // Hkv, 0.125, True, 0)
+    assert_close(got[:, 32:32 + H * D], ref, FP32_TOL, "matrix-core packed views")
+    assert np.isnan(got[:, :32]).all() and np.isnan(got[:, 32 + H * D:]).all()
+    run(*args, out=out)
+    assert np.array_equal(host(big), got, equal_nan=True)
