@@ -467,6 +467,7 @@ def bench_block(steps, warmup):
                    "fused_head_ops = the same chain op by op (repeat_kv x2, QK^T GEMM, scale, "
                    "softmax, PV GEMM)")
     out["fused_head_kernel"] = bench_fused_head_kernel(steps, warmup)
+    out["fused_head_long"] = bench_fused_head_long(steps, warmup)
     # the block's dominant device kernel is the attention launch
     out["roofline"] = dict(out["fused_head_kernel"]["roofline"], kind="fused_head_kernel")
     return out, (x, ws)
@@ -519,6 +520,33 @@ def bench_fused_head_kernel(steps, warmup, S=128):
             "algorithmic_bytes": 4 * (2 * S * 2048 + 2 * S * 256),
             "note": "device_us from graph replays; the chain = repeat_kv x2, bn_matmul (library "
                     "GEMM), scale, softmax, bn_matmul, launched eagerly"}
+
+
+def bench_fused_head_long(steps, warmup, sizes=(512, 2048)):
+    """bn_fused_head_attention on longer prompts (32/4 heads, head_dim 64,
+    fp32, causal), where it runs on the matrix cores: group sums of Q, 32 x
+    128 score blocks on v_mfma_f32_32x32x2f32, a log-sum-exp merge (three
+    launches and a pool allocation per call).  Eager launches back to back,
+    events on the stream; the work counted is the causal half of the two
+    products at the group-summed width (2 x 2 x 256 flops per visible pair)."""
+    import torch
+    import bnhip
+    res = {}
+    for S in sizes:
+        g = torch.Generator(device="cuda").manual_seed(S)
+        q = torch.randn((S, 2048), generator=g, device="cuda")
+        k = torch.randn((S, 256), generator=g, device="cuda")
+        v = torch.randn((S, 256), generator=g, device="cuda")
+        o = torch.empty((S, 2048), device="cuda")
+        fused = lambda i: bnhip.fused_head_attention(q, k, v, 32, 4, 64, o=o, scale=0.125)
+        ms = time_launches(fused, max(steps, 20), warmup)
+        flop = 2 * 2 * 256 * (S * (S + 1) // 2)
+        tf = flop / (ms * 1e-3) / 1e12
+        res[f"S{S}"] = {"us_per_call": round(ms * 1e3, 2), "flop": flop,
+                        "roofline": roofline("mfma", tf, PEAK_FP32_TFLOPS, "TFLOP/s")}
+    res["note"] = ("eager calls (host launch of three kernels and a pool round trip per call: "
+                   "host-bound at 512 rows); device times per kernel in the rocprofv3 summary")
+    return res
 
 
 def cpu_baseline_block(x, ws):
