@@ -64,7 +64,7 @@ PATHS = {
     "bf16_head_split": ("bf16", 16, 2, (5, 2500, [2500, 17, 1024, 2000, 64]),
                         (2, 700, [699, 700])),
     "f32_split": ("f32", 32, 4, (4, 2100, [2100, 1, 1500, 64]), (2, 1500, [1500, 900])),
-    "f32_single": ("f32", 32, 4, (2, 640, [640, 313]), (1, 300, [257])),
+    "f32_short": ("f32", 32, 4, (2, 640, [640, 313]), (1, 300, [257])),
     "bf16_whole": ("bf16", 32, 4, (None, 700, None), (None, 300, None)),
 }
 
