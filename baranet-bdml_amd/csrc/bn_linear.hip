@@ -695,6 +695,121 @@ void plan_split(int dtype, int m, int n, int k, int *nsplit, int *kchunk) {
   *nsplit = k > 0 ? (k + *kchunk - 1) / *kchunk : 1;
 }
 
+// ------------------------------------------------ output-major, many rows
+// y[m][n] = sum_k x[m][k] w[n][k] with w output-major (each output's k
+// weights contiguous) and more rows than the few-rows kernel stages (m > 4;
+// fp32) on v_mfma_f32_32x32x2f32: one workgroup per 32 rows x 128 outputs,
+// wave w on the 32 outputs n0 + 32w ..; k in stages of 32 staged through
+// LDS (x: 32 rows, w: 128 rows of 128 bytes each, every thread one 16-byte
+// chunk of x and four of w per stage, whole cache lines per row), two stage
+// buffers (one barrier per stage), the next stage's loads in flight while
+// this one is multiplied.  Lane (r, hf) reads 16 bytes of its x row and of
+// its w row at k offset 8u + 4hf: the operands of four MFMAs (contraction
+// pairs {8u + e, 8u + 4 + e}).  The epilogue rotates the pairs (2p, 2p+1) of
+// the first rope_cols columns (op_rope.cuh:79-98, fp32 angle (pos0 + m) *
+// freq) with the neighbouring lane's value, and stores.  Workgroups that
+// read the same weight rows go to one XCD.
+constexpr int NT_BM = 32, NT_BN = 128, NT_KS = 32, NT_P = NT_KS + 4;  // LDS row pitch (floats)
+typedef float f32x16_nt __attribute__((ext_vector_type(16)));
+
+__global__ __launch_bounds__(256) void linear_nt_kernel(LinParams p, RopeFreqs fr) {
+  __shared__ __attribute__((aligned(16))) float xs[2][NT_BM * NT_P];
+  __shared__ __attribute__((aligned(16))) float ws[2][NT_BN * NT_P];
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, r32 = lane & 31, hf = lane >> 5;
+  const int n_rt = (p.m + NT_BM - 1) / NT_BM;
+  // workgroups are dealt to the 8 XCDs in turn: logical unit u's XCD is
+  // u / (grid / 8), so consecutive units -- the row tiles of one column
+  // tile -- share an L2
+  int u = blockIdx.x;
+  if ((gridDim.x & 7) == 0) u = (blockIdx.x & 7) * (gridDim.x >> 3) + (blockIdx.x >> 3);
+  const int rt = u % n_rt, ct = u / n_rt;
+  const int m0 = rt * NT_BM, n0 = ct * NT_BN;
+  const int nst = (p.k + NT_KS - 1) / NT_KS;
+  // staging: thread tid holds chunk c = tid of x (row c / 8, k 4*(c % 8))
+  // and chunks tid + 256j of w; rows past m / n read a valid row (their
+  // outputs are not stored), k past p.k reads zeros
+  const int cr = tid >> 3, ck = 4 * (tid & 7);
+  const float *xg = (const float *)p.x + (int64_t)min(m0 + cr, p.m - 1) * p.x_rs + ck;
+  const float *wg[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) wg[j] = (const float *)p.w + (int64_t)min(n0 + cr + 32 * j, p.n - 1) * p.w_rs + ck;
+  float4 xr, wr[4];
+  auto gload = [&](int st) __attribute__((always_inline)) {
+    const int k0 = st * NT_KS;
+    const bool ok = k0 + ck < p.k;  // k is a multiple of 4: a chunk is all in or all out
+    xr = ok ? *(const float4 *)(xg + k0) : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) wr[j] = ok ? *(const float4 *)(wg[j] + k0) : make_float4(0.f, 0.f, 0.f, 0.f);
+  };
+  auto lstore = [&](int b) __attribute__((always_inline)) {
+    *(float4 *)(&xs[b][cr * NT_P + ck]) = xr;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) *(float4 *)(&ws[b][(cr + 32 * j) * NT_P + ck]) = wr[j];
+  };
+  f32x16_nt acc = f32x16_nt{};
+  gload(0);
+  lstore(0);
+  __syncthreads();
+  for (int st = 0; st < nst; ++st) {
+    const int b = st & 1;
+    if (st + 1 < nst) gload(st + 1);
+    const float *xa = &xs[b][r32 * NT_P + 4 * hf];
+    const float *wa = &ws[b][(32 * w + r32) * NT_P + 4 * hf];
+#pragma unroll
+    for (int uu = 0; uu < NT_KS / 8; ++uu) {
+      const float4 a = *(const float4 *)(xa + 8 * uu);
+      const float4 bb = *(const float4 *)(wa + 8 * uu);
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.x, bb.x, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.y, bb.y, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.z, bb.z, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.w, bb.w, acc, 0, 0, 0);
+    }
+    if (st + 1 < nst) lstore(b ^ 1);  // buffer b ^ 1 was last read in stage st - 1
+    __syncthreads();
+  }
+
+  // register i of acc is row m0 + 8(i/4) + 4hf + i%4 of column n0 + 32w + r32;
+  // a rotation pair is the even column's lane and the next one.  The tile's
+  // angles (pos0 + m) * freq take one sincosf each, shared through LDS (the
+  // staging buffers are free after the last barrier): row r, frequency
+  // index q of the tile's columns (q < 64 covers head_dim <= 128 and any
+  // 128 columns: (n % head_dim) / 2 for n in [n0, n0 + 128))
+  const int gn = n0 + 32 * w + r32;
+  const bool even = (r32 & 1) == 0;
+  const bool rot = (gn & ~1) < p.rope_cols;
+  static_assert(NT_BM * 64 * 2 <= NT_BN * NT_P, "the angle table fits one w staging buffer");
+  float2 *sc = reinterpret_cast<float2 *>(&ws[0][0]);  // [NT_BM][64] (sin, cos)
+  const bool table = n0 < p.rope_cols && p.head_dim <= 128;  // uniform
+  if (table) {
+    const int nq = min(p.head_dim / 2, 64);
+    for (int e = tid; e < NT_BM * 64; e += 256) {
+      const int r = e >> 6, q = e & 63;
+      float sn = 0.f, cs = 1.f;
+      if (q < nq) sincosf((float)(p.pos0 + m0 + r) * fr.f[q], &sn, &cs);
+      sc[e] = make_float2(sn, cs);
+    }
+    __syncthreads();
+  }
+  const int q = rot ? ((gn & ~1) % p.head_dim) >> 1 : 0;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int row = 8 * (i >> 2) + 4 * hf + (i & 3), gm = m0 + row;
+    float v = acc[i];
+    const float o = __shfl_xor(v, 1, 64);  // the pair's other column
+    if (rot) {  // op_rope.cuh:79-98: fp32 angle position * freq
+      float2 t;
+      if (table) {
+        t = sc[row * 64 + q];
+      } else {  // head_dim above 128: the angle of this element
+        sincosf((float)(p.pos0 + gm) * fr.f[q], &t.x, &t.y);
+      }
+      const float x0 = even ? v : o, x1 = even ? o : v;
+      v = even ? x0 * t.y - x1 * t.x : x0 * t.x + x1 * t.y;
+    }
+    if (gm < p.m && gn < p.n) ((float *)p.y)[(int64_t)gm * p.y_rs + gn] = v;
+  }
+}
+
 }  // namespace
 }  // namespace bn
 
@@ -721,6 +836,29 @@ extern "C" size_t bn_linear_rope_workspace_size(int dtype, int m, int n, int k) 
 namespace bn {
 
 namespace {
+// output-major w with more than four rows (linear_nt_kernel; fp32, plain
+// epilogue): x and w rows 16-byte aligned and k a multiple of 4 (checked by
+// the caller's layout test)
+int nt_run(const bn_view *x, const bn_view *w, const bn_view *y, int rope_cols, int position_offset,
+           int head_dim, const RopeFreqs &fr, const char *op, void *stream) {
+  int st;
+  if ((st = require_device(op, {x, w, y}))) return st;
+  if (y->h == 0 || y->w == 0) return BN_OK;
+  if ((st = ensure_device())) return st;
+  LinParams p = {};
+  p.x = (const float *)x->data + x->offset;
+  p.w = (const float *)w->data + w->offset;
+  p.y = (float *)y->data + y->offset;
+  p.x_rs = x->stride_h; p.w_rs = w->stride_w; p.y_rs = y->stride_h;
+  p.m = x->h; p.n = w->w; p.k = x->w;
+  p.rope_cols = rope_cols; p.head_dim = rope_cols ? head_dim : 2; p.pos0 = position_offset;
+  const int64_t tiles = (int64_t)((p.m + NT_BM - 1) / NT_BM) * ((p.n + NT_BN - 1) / NT_BN);
+  if (tiles > 0x7fffffff) return fail(BN_ERR_UNSUPPORTED, std::string(op) + ": too many output tiles");
+  hipLaunchKernelGGL(linear_nt_kernel, dim3((unsigned)tiles), dim3(256), 0, as_stream(stream), p, fr);
+  BN_LAUNCH_CHECK();
+  return BN_OK;
+}
+
 // output-major w (linear_gemv_t_kernel): shapes and the rotation table are
 // checked by linear_run; this checks the layout the kernel reads
 int gemv_t_run(const bn_view *x, const bn_view *w, const bn_view *y, int rope_cols,
@@ -745,6 +883,8 @@ int gemv_t_run(const bn_view *x, const bn_view *w, const bn_view *y, int rope_co
     return fail(BN_ERR_UNSUPPORTED,
                 std::string(op) + ": an output-major w needs 16-byte aligned rows of x and w, k a "
                                   "multiple of 16 bytes, contiguous rows of y and an even output width");
+  if (m > GV_M && !nrm && !mrg && !k_dst && epi == EPI_PLAIN && dt == BN_F32)
+    return nt_run(x, w, y, rope_cols, position_offset, head_dim, fr, op, stream);
   // the kernel stages mr rows (3 rows run the 4-row instance)
   const int mr = m <= 1 ? 1 : (m <= 2 ? 2 : 4);
   if (m > GV_M || (int64_t)mr * kp > GV_XMAX)

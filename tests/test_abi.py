@@ -294,7 +294,13 @@ def test_linear_rope_output_major_validation():
     # w viewed [k, n] with stride_h 1: the output-major few-rows kernel; its
     # limits are checked before the device
     wt = lambda k, n, sw=None: V(k, n, stride_h=1, stride_w=k if sw is None else sw)
+    # fp32 with more than 4 rows takes the many-rows matrix-core kernel (only
+    # the device is missing here); bf16 stays within the few-rows kernel
     s, m = st("bn_linear_rope", V(5, 256), wt(256, 128), V(5, 128), 0, 0, 64, 1e4, None, 0, None)
+    assert s == B.BN_ERR_NOT_DEVICE, m
+    bw = lambda k, n: V(k, n, dtype=B.BN_BF16, stride_h=1, stride_w=k)
+    s, m = st("bn_linear_rope", V(5, 256, dtype=B.BN_BF16), bw(256, 128), V(5, 128, dtype=B.BN_BF16), 0, 0,
+              64, 1e4, None, 0, None)
     assert s == B.BN_ERR_UNSUPPORTED and "at most 4 rows" in m
     s, m = st("bn_linear_rope", V(1, 256), wt(256, 127), V(1, 127), 0, 0, 64, 1e4, None, 0, None)
     assert s == B.BN_ERR_UNSUPPORTED and "even output width" in m

@@ -431,11 +431,36 @@ def test_linear_rope_output_major_strided_and_limits():
     ref = O.linear_rope(xb, np.ascontiguousarray(wb[:320, :256].T), 128, 9, 64, 1e4)
     assert_close(got[:, 40:360], ref, FP32_TOL, "out-major strided")
     assert np.all(got[:, :40] == 7.0) and np.all(got[:, 360:] == 7.0)
-    # more than 4 rows, or an odd output width, is refused for this layout
+    # more than 4 rows of bf16, or an odd output width, is refused for this layout
     with pytest.raises(B.BnError, match="at most 4 rows"):
-        B.linear_rope(torch.randn((5, 256), device="cuda"), w)
+        B.linear_rope(torch.randn((5, 256), device="cuda").bfloat16(), w.bfloat16())
     with pytest.raises(B.BnError, match="even output width"):
         B.linear_rope(dev(xb), dev(wb)[:319, :256].t())
+
+
+@pytest.mark.parametrize("case", [(512, 2048, 2560, 2304, 0),    # config 4's prompt QKV + RoPE
+                                  (512, 2048, 2048, 0, 0),       # its O projection
+                                  (37, 5632, 2048, 0, 0),        # down, ragged row tile
+                                  (5, 520, 330, 192, 40),        # ragged column tile, k not a multiple of 32
+                                  (96, 64, 4032, 4032, 16000),   # every column rotated, late positions
+                                  (40, 256, 512, 512, 5)])       # head_dim 256: angles per element
+def test_linear_rope_output_major_many_rows(case):
+    """fp32, w output-major (the transposed view of an [N, K] matrix), more
+    than 4 rows: the matrix-core kernel of 32 x 160 output tiles; against the
+    oracle's op_mm + op_rope, and the same bits for a row computed inside
+    different row tiles (each output is one fixed-order sum)."""
+    M, K, N, rc, off = case
+    r = rng(65)
+    x = r.standard_normal((M, K)).astype(np.float32)
+    wt = (r.standard_normal((N, K)) / np.sqrt(K)).astype(np.float32)
+    wd = dev(wt)
+    hd = 256 if K == 256 else 64
+    y = B.linear_rope(dev(x), wd.t(), rope_cols=rc, position_offset=off, head_dim=hd)
+    ref = O.linear_rope(x, np.ascontiguousarray(wt.T), rc, off, hd, 1e4)
+    assert_close(host(y), ref, FP32_TOL, f"out-major many rows {case}")
+    if M > 40:   # rows 33.. as rows 0.. of a second call (another row tile position)
+        y2 = B.linear_rope(dev(x[33:]), wd.t(), rope_cols=rc, position_offset=off + 33, head_dim=hd)
+        assert torch.equal(y2, y[33:])
 
 
 def test_linear_rope_empty_k_gives_zeros():
