@@ -155,7 +155,9 @@ int bn_matmul(const bn_view *a, const bn_view *b, const bn_view *c, void *stream
  * M*ceil(K / (64*elements per 16 bytes))*64*elements per 16 bytes <= 16384
  * this streams each output's contiguous weights once with no k split (no
  * workspace; N even; x rows 16-byte aligned, y rows contiguous at any
- * stride); other M are BN_ERR_UNSUPPORTED for that layout. */
+ * stride); fp32 with more rows runs a matrix-core kernel of 32 x 128 output
+ * tiles (no workspace, no k split); bf16 with more than 4 rows is
+ * BN_ERR_UNSUPPORTED for that layout. */
 size_t bn_linear_rope_workspace_size(int dtype, int m, int n, int k);
 int bn_linear_rope(const bn_view *x, const bn_view *w, const bn_view *y,
                    int rope_cols, int position_offset, int head_dim, float theta,
@@ -330,8 +332,11 @@ int bn_llama_decode(const bn_llama_config *config, const float *embed,
  * whole cache is attended).  workspace: device memory of
  * bn_gqa_decode_workspace_size() bytes (NULL: taken from the pool when the
  * call needs it); single-pass calls use none: bf16 caches with
- * batch*n_kv_heads >= the device's compute units, fp32 caches of at most 1024
- * keys with batch*n_heads <= 256. */
+ * batch*n_kv_heads >= the device's compute units.  fp32 caches of at most
+ * 1024 keys with batch*n_heads <= 256 keep 4 split records per (sequence,
+ * head) in it and merge them in the same launch, counting on a ring of 16
+ * counter slots inside the library: at most 16 such calls in flight at once
+ * on one GPU (more would share a slot and race). */
 size_t bn_gqa_decode_workspace_size(int batch, int max_len, int n_heads,
                                     int head_dim);
 int bn_gqa_decode(int dtype, const void *q, const void *k_cache,
@@ -373,7 +378,8 @@ int bn_gqa_decode_planned(int dtype, const void *q, const void *k_cache,
  * would exceed the array fails with BN_ERR_UNSUPPORTED before any device
  * work.  Every call on one GPU shares that GPU's array and leaves its last
  * contents there (nothing needs clearing: each call writes every record it
- * reads), so calls that overlap on one GPU -- on different streams, or from
+ * reads; the short-cache split's counters return to zero at the end of each
+ * launch), so calls that overlap on one GPU -- on different streams, or from
  * different threads -- race; serialise them. */
 #define BN_GQA_DECODE_SCRATCH_BYTES (32u << 20)
 int bn_gqa_decode_noalloc(int dtype, const void *q, const void *k_cache,
