@@ -98,9 +98,27 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dq_kernel(BwdParams p) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r32 = lane & 31, hf = lane >> 5;
   const int n_mt = (p.seq_q + 127) / 128;
-  const int mt = n_mt - 1 - (int)(blockIdx.x / (p.batch * p.n_heads));  // heaviest first
-  const int bh = (int)(blockIdx.x % (p.batch * p.n_heads));
-  const int b = bh / p.n_heads, h = bh % p.n_heads, g = h / p.group;
+  int mt, b, h;
+  {
+    // workgroups are dealt to the 8 XCDs in turn: when the (batch, KV head)
+    // groups are a multiple of 8, XCD x takes groups x, x + 8, ... (all their
+    // query heads and row tiles, heaviest first), so a group's K/V is read
+    // from HBM once per launch and then from that XCD's L2
+    const int L = blockIdx.x, NG = p.batch * p.n_kv;
+    if (NG % 8 == 0) {
+      const int x = L & 7, j = L >> 3, per_mt = (NG >> 3) * p.group;
+      mt = n_mt - 1 - j / per_mt;
+      const int r = j % per_mt, gi = (r / p.group) * 8 + x;
+      b = gi / p.n_kv;
+      h = (gi % p.n_kv) * p.group + r % p.group;
+    } else {
+      mt = n_mt - 1 - L / (p.batch * p.n_heads);  // heaviest first
+      const int bh = L % (p.batch * p.n_heads);
+      b = bh / p.n_heads;
+      h = bh % p.n_heads;
+    }
+  }
+  const int g = h / p.group;
   const int q0 = mt * 128 + wave * 32, qrow = q0 + r32;
   const bool row_ok = qrow < p.seq_q;
   const int qr = min(qrow, p.seq_q - 1);
