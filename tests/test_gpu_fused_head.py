@@ -108,27 +108,29 @@ def test_fused_head_attention_rejects_misaligned_rows():
                0, None)
 
 
-@pytest.mark.parametrize("Sq,Sk,H,Hkv,causal,off", [
-    (600, 1100, 32, 4, False, 0),   # non-causal, ragged row tile and key block
-    (700, 700, 16, 4, True, 0),     # n_rep 4
-    (530, 800, 32, 4, True, 270),   # rows at positions 270..799 of an 800-key context
-    (560, 560, 32, 4, True, -40),   # rows 0..39 see no key: zeros
+@pytest.mark.parametrize("Sq,Sk,H,Hkv,causal,off,D", [
+    (600, 1100, 32, 4, False, 0, 64),   # non-causal, ragged row tile and key block
+    (700, 700, 16, 4, True, 0, 64),     # n_rep 4
+    (530, 800, 32, 4, True, 270, 64),   # rows at positions 270..799 of an 800-key context
+    (560, 560, 32, 4, True, -40, 64),   # rows 0..39 see no key: zeros
+    (520, 520, 16, 2, True, 0, 128),    # head_dim 128, two KV heads (KV*D = 256)
+    (515, 515, 8, 8, True, 3, 32),      # head_dim 32, n_rep 1
 ])
-def test_fused_head_attention_matrix_core_rows(Sq, Sk, H, Hkv, causal, off):
+def test_fused_head_attention_matrix_core_rows(Sq, Sk, H, Hkv, causal, off, D):
     """The matrix-core path (seq_q >= 512, KV*D = 256): the whole output
     computed, 64-row blocks at both ends checked against the oracle chain on
     the same rows (a block starting at row i0 sits at position i0 + off)."""
-    D = 64
     r = np.random.default_rng(Sq * 7 + Sk)
     q = r.standard_normal((Sq, H * D)).astype(np.float32)
     k = r.standard_normal((Sk, Hkv * D)).astype(np.float32)
     v = r.standard_normal((Sk, Hkv * D)).astype(np.float32)
-    got = host(run(dev(q), dev(k), dev(v), H, Hkv, D, 0.125, causal, off))
+    sc = 1.0 / np.sqrt(D)
+    got = host(run(dev(q), dev(k), dev(v), H, Hkv, D, sc, causal, off))
     assert np.isfinite(got).all()
     if off < 0:
         assert not got[:-off].any()
     for i0 in (max(0, -off), Sq - 64):
-        ref = O.fused_head_attention(q[i0:i0 + 64], k, v, D, H // Hkv, 0.125, causal, i0 + off)
+        ref = O.fused_head_attention(q[i0:i0 + 64], k, v, D, H // Hkv, sc, causal, i0 + off)
         assert_close(got[i0:i0 + 64], ref, FP32_TOL, f"rows {i0}..{i0 + 63}")
 
 

@@ -149,8 +149,11 @@ def decode_case(target, i):
     return dtype, Bn, L, H, Hkv, lens.astype(np.int32)
 
 
-@pytest.mark.parametrize("i", range(4))
-@pytest.mark.parametrize("target", DECODE_TARGETS)
+DECODE_SWEEP = [(t, i) for t in DECODE_TARGETS for i in range(4)] + \
+    [("f32_short", i) for i in range(4, 12)]   # the in-launch merge of the short-cache split
+
+
+@pytest.mark.parametrize("target,i", DECODE_SWEEP)
 def test_decode_sweep(target, i):
     dtype, Bn, L, H, Hkv, lens = decode_case(target, i)
     assert decode_path(dtype, Bn, L, H, Hkv) == target
