@@ -111,6 +111,7 @@ def lib():
         "bn_gqa_decode_workspace_size": ([i, i, i, i], sz),
         "bn_gqa_decode": ([i, vp, vp, vp, vp, vp] + [i] * 5 + [f, vp, sz, vp], i),
         "bn_gqa_decode_noalloc": ([i, vp, vp, vp, vp, vp] + [i] * 5 + [f, vp], i),
+        "bn_gqa_decode_strided": ([i, vp, vp, vp, vp, vp] + [i] * 5 + [i64] * 3 + [f, vp, sz, vp], i),
         "bn_gqa_decode_planned_workspace_size": ([i, i, i, i, i], sz),
         "bn_gqa_decode_planned": ([i, vp, vp, vp, vp, vp, vp] + [i] * 5 + [f, vp, sz, vp], i),
     }
@@ -261,18 +262,34 @@ def linear_rope(x, w, y=None, rope_cols=0, position_offset=0, head_dim=64, theta
 
 
 def gqa_decode(q, k_cache, v_cache, seq_lens, o=None, scale=None, workspace=None, stream=None):
-    """q [B,H,D], caches [B,Lmax,Hkv,D], seq_lens int32 [B] (device)."""
+    """q [B,H,D] and o contiguous, caches [B,Lmax,Hkv,D], seq_lens int32 [B]
+    (device).  Contiguous caches take bn_gqa_decode; any other layout whose
+    key rows are contiguous (e.g. the head-major storage
+    ``torch.empty(B, Hkv, Lmax, D).transpose(1, 2)``) takes
+    bn_gqa_decode_strided with the caches' strides (K and V alike)."""
     import torch
     B, H, D = q.shape
     _, Lmax, Hkv, _ = k_cache.shape
     if o is None:
         o = torch.empty_like(q)
+    if not (q.is_contiguous() and o.is_contiguous()):
+        raise ValueError("gqa_decode: q and o must be contiguous [B, H, D]")
+    if tuple(v_cache.shape) != tuple(k_cache.shape) or v_cache.stride() != k_cache.stride():
+        raise ValueError("gqa_decode: k_cache and v_cache must have the same shape and strides")
     sc = 1.0 / math.sqrt(D) if scale is None else scale
     ws_ptr, ws_bytes = (None, 0) if workspace is None else (workspace.data_ptr(),
                                                             workspace.numel() * workspace.element_size())
-    call("bn_gqa_decode", _torch_dtype_code(q), q.data_ptr(), k_cache.data_ptr(),
-         v_cache.data_ptr(), seq_lens.data_ptr(), o.data_ptr(), B, Lmax, H, Hkv, D, sc,
-         ws_ptr, ws_bytes, stream_of(stream))
+    if k_cache.is_contiguous():
+        call("bn_gqa_decode", _torch_dtype_code(q), q.data_ptr(), k_cache.data_ptr(),
+             v_cache.data_ptr(), seq_lens.data_ptr(), o.data_ptr(), B, Lmax, H, Hkv, D, sc,
+             ws_ptr, ws_bytes, stream_of(stream))
+        return o
+    if k_cache.stride(3) != 1:
+        raise ValueError("gqa_decode: cache key rows must be contiguous (stride 1 along head_dim)")
+    call("bn_gqa_decode_strided", _torch_dtype_code(q), q.data_ptr(), k_cache.data_ptr(),
+         v_cache.data_ptr(), seq_lens.data_ptr(), o.data_ptr(), B, Lmax, H, Hkv, D,
+         k_cache.stride(0), k_cache.stride(2), k_cache.stride(1), sc, ws_ptr, ws_bytes,
+         stream_of(stream))
     return o
 
 
@@ -288,6 +305,8 @@ def gqa_decode_planned(q, k_cache, v_cache, seq_lens, h_seq_lens, o=None, scale=
     if o is None:
         o = torch.empty_like(q)
     sc = 1.0 / math.sqrt(D) if scale is None else scale
+    if not all(t.is_contiguous() for t in (q, o, k_cache, v_cache)):
+        raise ValueError("gqa_decode_planned: q, o and the caches must be contiguous")
     hl = np.ascontiguousarray(np.asarray(h_seq_lens, dtype=np.int32))
     assert hl.shape == (B,)
     ws_ptr, ws_bytes = (None, 0) if workspace is None else (workspace.data_ptr(),

@@ -94,6 +94,11 @@ struct DecodeParams {
   int batch, max_len, n_heads, n_kv_heads, n_split, chunk;
   float c;        // scale * log2(e)
   int hlen = -1;  // >= 0: every sequence's length, from the host (lens not read)
+  // cache strides in elements: sequence, KV head, key row (a contiguous
+  // [batch, max_len, n_kv_heads, 64] cache: max_len*n_kv_heads*64, 64,
+  // n_kv_heads*64; a head-major [batch, n_kv_heads, max_len, 64] one:
+  // n_kv_heads*max_len*64, max_len*64, 64)
+  int64_t kv_bs = 0, kv_hs = 0, kv_rs = 0;
   // DEC_SHORT: per-(sequence, query head) counters (zero at launch, cleared
   // again by each unit's last split): the last split to arrive merges the
   // unit's records and writes the output in the same launch; null: the
@@ -174,9 +179,9 @@ __global__ __launch_bounds__(64 * WV) void decode_split_kernel(DecodeParams p) {
   const int kw0 = CONTIG ? k_begin + wave * per : k_begin + wave * KPI * NT;
   const int kw1 = CONTIG ? min(kw0 + per, k_end) : k_end;
 
-  const int64_t kv_rs = (int64_t)p.n_kv_heads * HD;
-  const T *Kb = (const T *)p.k + ((int64_t)b * p.max_len) * kv_rs + (int64_t)g * HD + sub * VEC;
-  const T *Vb = (const T *)p.v + ((int64_t)b * p.max_len) * kv_rs + (int64_t)g * HD + sub * VEC;
+  const int64_t kv_rs = p.kv_rs;
+  const T *Kb = (const T *)p.k + b * p.kv_bs + g * p.kv_hs + sub * VEC;
+  const T *Vb = (const T *)p.v + b * p.kv_bs + g * p.kv_hs + sub * VEC;
 
 #pragma unroll
   for (int h = 0; h < G; ++h)
@@ -383,9 +388,9 @@ void decode_bf16_mfma_kernel(DecodeParams p) {
   const int k_end = min(k_begin + p.chunk, len);
   const int ntiles = (k_end - k_begin + TK - 1) / TK;
 
-  const int64_t kv_rs = (int64_t)p.n_kv_heads * HD;
-  const bf16_t *Kb = (const bf16_t *)p.k + (int64_t)b * p.max_len * kv_rs + (int64_t)g * HD + 8 * grp;
-  const bf16_t *Vb = (const bf16_t *)p.v + (int64_t)b * p.max_len * kv_rs + (int64_t)g * HD + 8 * grp;
+  const int64_t kv_rs = p.kv_rs;
+  const bf16_t *Kb = (const bf16_t *)p.k + b * p.kv_bs + g * p.kv_hs + 8 * grp;
+  const bf16_t *Vb = (const bf16_t *)p.v + b * p.kv_bs + g * p.kv_hs + 8 * grp;
 
   // B operand of S^T: column l16 = query head g*G + l16 (zero past G), d = 8grp + 32t + 0..7
   dbf16x8_t qb[2];
@@ -578,9 +583,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void d
   const int k_end = min(k_begin + p.chunk, len);
   const int ntiles = (k_end - k_begin + TK - 1) / TK;
 
-  const int64_t kv_rs = (int64_t)p.n_kv_heads * HD;
-  const bf16_t *Kr = (const bf16_t *)p.k + (int64_t)b * p.max_len * kv_rs + (int64_t)g0 * HD;
-  const bf16_t *Vr = (const bf16_t *)p.v + (int64_t)b * p.max_len * kv_rs + (int64_t)g0 * HD;
+  const int64_t kv_rs = p.kv_rs;
+  const bf16_t *Kr = (const bf16_t *)p.k + b * p.kv_bs + g0 * p.kv_hs;
+  const bf16_t *Vr = (const bf16_t *)p.v + b * p.kv_bs + g0 * p.kv_hs;
 
   dbf16x8_t qb[2];
 #pragma unroll
@@ -600,13 +605,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void d
   };
   static_assert(RCH == 4, "register tile holds 4 chunks per array");
   const int crow = tid >> 5, ccol = (tid & 31) * 8;  // chunk i adds 8 rows
+  const int64_t cofs = (ccol >> 6) * p.kv_hs + (ccol & 63);  // head ccol/64 of the four
   auto gload = [&](RegTile &r, int ti) __attribute__((always_inline)) {
     const int kb = k_begin + TK * min(ti, ntiles - 1);  // clamped: same load count on every path
     const int last = k_end - 1;  // past the end: a valid row, masked to P = 0
-    const int64_t o0 = (int64_t)min(kb + crow, last) * kv_rs + ccol;
-    const int64_t o1 = (int64_t)min(kb + crow + 8, last) * kv_rs + ccol;
-    const int64_t o2 = (int64_t)min(kb + crow + 16, last) * kv_rs + ccol;
-    const int64_t o3 = (int64_t)min(kb + crow + 24, last) * kv_rs + ccol;
+    const int64_t o0 = (int64_t)min(kb + crow, last) * kv_rs + cofs;
+    const int64_t o1 = (int64_t)min(kb + crow + 8, last) * kv_rs + cofs;
+    const int64_t o2 = (int64_t)min(kb + crow + 16, last) * kv_rs + cofs;
+    const int64_t o3 = (int64_t)min(kb + crow + 24, last) * kv_rs + cofs;
     // streamed once: non-temporal loads
     r.k0 = __builtin_nontemporal_load((const u32x4 *)(Kr + o0)); r.v0 = __builtin_nontemporal_load((const u32x4 *)(Vr + o0));
     r.k1 = __builtin_nontemporal_load((const u32x4 *)(Kr + o1)); r.v1 = __builtin_nontemporal_load((const u32x4 *)(Vr + o1));
@@ -759,9 +765,9 @@ __global__ __launch_bounds__(64 * WWV) void decode_bf16_whole_kernel(DecodeParam
   const int tstride = TK * WWV;  // keys between a wave's tiles
   const int ntiles = all_tiles > wave ? (all_tiles - wave + WWV - 1) / WWV : 0;
 
-  const int64_t kv_rs = (int64_t)p.n_kv_heads * HD;
-  const bf16_t *Kr = (const bf16_t *)p.k + (int64_t)b * p.max_len * kv_rs + (int64_t)g * HD;
-  const bf16_t *Vr = (const bf16_t *)p.v + (int64_t)b * p.max_len * kv_rs + (int64_t)g * HD;
+  const int64_t kv_rs = p.kv_rs;
+  const bf16_t *Kr = (const bf16_t *)p.k + b * p.kv_bs + g * p.kv_hs;
+  const bf16_t *Vr = (const bf16_t *)p.v + b * p.kv_bs + g * p.kv_hs;
 
   dbf16x8_t qb[2];
 #pragma unroll
@@ -940,6 +946,7 @@ struct PlanParams {
   uint32_t *cnt;  // this launch's per-unit counters: zero at launch, cleared by each unit's last part
   int batch, max_len, n_heads, n_kv_heads, n_units, share, total;  // share: sequence tiles per group
   float c;                         // scale * log2(e)
+  int64_t kv_bs, kv_hs, kv_rs;     // cache strides (elements): sequence, KV head, key row
   uint32_t wg_start[kPlanBins];    // group: first sequence (bits 0..15), its first tile (16..31)
   uint32_t unit[kPlanUnits];       // record base (0..11), first group (12..23), parts (24..31)
   int32_t len[kPlanUnits];         // per sequence: length, clamped to [0, max_len]
@@ -962,7 +969,7 @@ __global__ __launch_bounds__(64 * WWV) void decode_bf16_planned_kernel(PlanParam
   // the same time), so the KV heads' slices of a cache row are read close in
   // time, as in the whole-cache kernel
   const int grp_id = bin / Hkv, gh = bin - grp_id * Hkv;
-  const int64_t kv_rs = (int64_t)Hkv * HD;
+  const int64_t kv_rs = p.kv_rs;
   auto tiles_of = [&](int b) { return (p.len[b] + TK - 1) / TK; };
 
   // units with no key at all: zeros, each written by workgroup u % gridDim.x
@@ -988,8 +995,8 @@ __global__ __launch_bounds__(64 * WWV) void decode_bf16_planned_kernel(PlanParam
     x.len = p.len[b];
     x.end = min(ntile, lb + (x.len + TK - 1) / TK - t);
     x.kb0 = TK * (t - lb);
-    x.kr = (const bf16_t *)p.k + (int64_t)b * p.max_len * kv_rs + (int64_t)g * HD;
-    x.vr = (const bf16_t *)p.v + (int64_t)b * p.max_len * kv_rs + (int64_t)g * HD;
+    x.kr = (const bf16_t *)p.k + b * p.kv_bs + g * p.kv_hs;
+    x.vr = (const bf16_t *)p.v + b * p.kv_bs + g * p.kv_hs;
   };
   auto seg_first = [&](Seg &x) __attribute__((always_inline)) {
     x.s = 0;
@@ -1355,6 +1362,9 @@ int decode_short_partials(const float *q, const float *k_cache, const float *v_c
   p.q = q; p.k = k_cache; p.v = v_cache; p.lens = seq_lens; p.o = nullptr; p.ws = part;
   p.hlen = host_len;
   p.batch = batch; p.max_len = max_len; p.n_heads = n_heads; p.n_kv_heads = n_kv_heads;
+  p.kv_rs = (int64_t)n_kv_heads * HD;  // contiguous [batch, max_len, n_kv_heads, 64]
+  p.kv_hs = HD;
+  p.kv_bs = (int64_t)max_len * p.kv_rs;
   p.n_split = kShortSplits;
   p.chunk = 0;
   p.c = scale * 1.4426950408889634f;
@@ -1450,11 +1460,14 @@ namespace {
 // bn_gqa_decode and bn_gqa_decode_noalloc: the same validation, kernels and
 // launch shapes; they differ only in where the split-K partials live (the
 // caller's workspace or the pool, against the file-scope scratch array).
+// strides: the caches' element strides (sequence, KV head, key row), or null
+// for a contiguous [batch, max_len, n_kv_heads, head_dim] cache.
 int gqa_decode_impl(int dtype, const void *q, const void *k_cache, const void *v_cache,
                     const int32_t *seq_lens, void *o, int batch, int max_len, int n_heads,
                     int n_kv_heads, int head_dim, float scale, void *workspace,
-                    size_t workspace_bytes, bool noalloc, void *stream) {
-  const char *op = noalloc ? "GQA decode (no allocation)" : "GQA decode";
+                    size_t workspace_bytes, bool noalloc, void *stream,
+                    const int64_t *strides = nullptr) {
+  const char *op = noalloc ? "GQA decode (no allocation)" : strides ? "GQA decode (strided)" : "GQA decode";
   if (dtype != BN_F32 && dtype != BN_BF16)
     return fail(BN_ERR_UNSUPPORTED, std::string(op) + ": dtype must be F32 or BF16");
   if (batch < 0 || max_len < 0)
@@ -1469,6 +1482,14 @@ int gqa_decode_impl(int dtype, const void *q, const void *k_cache, const void *v
     return fail(BN_ERR_INVALID_ARG, std::string(op) + ": scale must be positive and finite");
   if (batch == 0) return BN_OK;
   if (max_len == 0) return fail(BN_ERR_SHAPE, std::string(op) + ": max_len must be positive");
+  if (strides) {
+    // every key row starts 16-byte aligned (the kernels load 16 bytes per lane)
+    const int64_t align = dtype == BN_BF16 ? 8 : 4;
+    for (int i = 0; i < 3; ++i)
+      if (strides[i] <= 0 || strides[i] % align != 0 || strides[i] > ((int64_t)1 << 40))
+        return fail(BN_ERR_INVALID_ARG, std::string(op) + ": cache strides must be positive multiples of " +
+                                            std::to_string(align) + " elements (16 bytes)");
+  }
   if (!q || !k_cache || !v_cache || !seq_lens || !o)
     return fail(BN_ERR_INVALID_ARG, std::string(op) + ": NULL pointer");
   if (((uintptr_t)q | (uintptr_t)k_cache | (uintptr_t)v_cache) & 15u)
@@ -1485,6 +1506,9 @@ int gqa_decode_impl(int dtype, const void *q, const void *k_cache, const void *v
   DecodeParams p;
   p.q = q; p.k = k_cache; p.v = v_cache; p.lens = seq_lens; p.o = o;
   p.batch = batch; p.max_len = max_len; p.n_heads = n_heads; p.n_kv_heads = n_kv_heads;
+  p.kv_bs = strides ? strides[0] : (int64_t)max_len * n_kv_heads * HD;
+  p.kv_hs = strides ? strides[1] : HD;
+  p.kv_rs = strides ? strides[2] : (int64_t)n_kv_heads * HD;
   const bool short_split = short_path_ok(dtype, batch, max_len, n_heads);
   if (!short_split && dtype == BN_BF16) {  // one workgroup per (sequence, KV head) when that fills the CUs
     int st = ensure_device();
@@ -1638,6 +1662,17 @@ int bn_gqa_decode_noalloc(int dtype, const void *q, const void *k_cache, const v
                          n_kv_heads, head_dim, scale, nullptr, 0, true, stream);
 }
 
+int bn_gqa_decode_strided(int dtype, const void *q, const void *k_cache, const void *v_cache,
+                          const int32_t *seq_lens, void *o, int batch, int max_len, int n_heads,
+                          int n_kv_heads, int head_dim, int64_t cache_seq_stride,
+                          int64_t cache_head_stride, int64_t cache_row_stride, float scale,
+                          void *workspace, size_t workspace_bytes, void *stream) {
+  const int64_t strides[3] = {cache_seq_stride, cache_head_stride, cache_row_stride};
+  return gqa_decode_impl(dtype, q, k_cache, v_cache, seq_lens, o, batch, max_len, n_heads,
+                         n_kv_heads, head_dim, scale, workspace, workspace_bytes, false, stream,
+                         strides);
+}
+
 size_t bn_gqa_decode_planned_workspace_size(int batch, int max_len, int n_heads, int n_kv_heads,
                                             int head_dim) {
   if (batch <= 0 || max_len <= 0 || n_heads <= 0 || n_kv_heads <= 0 || n_heads % n_kv_heads ||
@@ -1686,6 +1721,9 @@ int bn_gqa_decode_planned(int dtype, const void *q, const void *k_cache, const v
                            head_dim, scale, workspace, workspace_bytes, false, stream);
   pl.q = q; pl.k = k_cache; pl.v = v_cache; pl.o = o;
   pl.batch = batch; pl.max_len = max_len; pl.n_heads = n_heads; pl.n_kv_heads = n_kv_heads;
+  pl.kv_rs = (int64_t)n_kv_heads * HD;  // contiguous [batch, max_len, n_kv_heads, 64]
+  pl.kv_hs = HD;
+  pl.kv_bs = (int64_t)max_len * pl.kv_rs;
   pl.c = scale * 1.4426950408889634f;
   pl.cnt = plan_counter_slot(library_device());
   if (!pl.cnt)

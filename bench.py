@@ -9,8 +9,10 @@ One step = one prefill launch over the whole batch, inputs resident in HBM.
 Also measured in the same run and reported as sub-objects:
   decode        config 3: B=64 one-token decode over a bf16 cache of 4096
                 (uniform), in GB/s of K/V + q + o bytes; two cache sets are
-                rotated so the 268 MB cache cannot sit in the 256 MB MALL
-  decode_ragged config 3 with lengths uniform in [512, 4096]
+                rotated so the 268 MB cache cannot sit in the 256 MB MALL;
+                caches stored head-major [B, Hkv, L, 64] (bn_gqa_decode_strided),
+                the token-major [B, L, Hkv, 64] figure (bn_gqa_decode) beside it
+  decode_ragged config 3 with lengths uniform in [512, 4096], the same two layouts
   prefill_fp32  config 2 in fp32
   rmsnorm_rope  config 5's fused RMSNorm+RoPE on [16384, 2048] bf16, GB/s
   prefill_long  config 5's prefill, B=1, S=16384, bf16
@@ -291,20 +293,25 @@ def decode_lengths(kind, B_=64, L=4096, seed=2):
     return np.full(B_, L, np.int32)
 
 
-def bench_decode(kind, steps, warmup, seed=2, planned=False):
+def bench_decode(kind, steps, warmup, seed=2, planned=False, layout="token_major"):
     """Config 3 decode; planned=True times bn_gqa_decode_planned (the host
     lengths plan equal tile shares per compute unit) instead of
-    bn_gqa_decode."""
+    bn_gqa_decode.  layout: the caches' storage -- "token_major"
+    [B, L, Hkv, 64] contiguous (bn_gqa_decode) or "head_major" [B, Hkv, L, 64]
+    (each (sequence, KV head)'s rows contiguous; bn_gqa_decode_strided)."""
     import torch
     import bnhip
     B_, L, H, Hkv = 64, 4096, 32, 4
     lens = decode_lengths(kind, B_, L, seed)
     g = torch.Generator(device="cuda").manual_seed(seed)
+    cache = ((lambda: torch.randn((B_, L, Hkv, 64), generator=g, device="cuda").bfloat16())
+             if layout == "token_major" else
+             (lambda: torch.randn((B_, Hkv, L, 64), generator=g, device="cuda").bfloat16()
+              .transpose(1, 2)))
     sets = []
     for _ in range(2):  # 2 x 268 MB > 256 MB MALL: every launch streams from HBM
-        sets.append((torch.randn((B_, H, 64), generator=g, device="cuda").bfloat16(),
-                     torch.randn((B_, L, Hkv, 64), generator=g, device="cuda").bfloat16(),
-                     torch.randn((B_, L, Hkv, 64), generator=g, device="cuda").bfloat16()))
+        sets.append((torch.randn((B_, H, 64), generator=g, device="cuda").bfloat16(), cache(),
+                     cache()))
     ld = torch.from_numpy(lens).cuda()
     nws = bnhip.lib().bn_gqa_decode_planned_workspace_size(B_, L, H, Hkv, 64)
     ws = torch.empty(nws, dtype=torch.uint8, device="cuda")
@@ -323,9 +330,13 @@ def bench_decode(kind, steps, warmup, seed=2, planned=False):
     desc = {"uniform": "uniform 4096", "ragged": f"ragged U[512,4096] seed {seed}",
             "two_class": "512 and 4096 alternating", "skewed": "four 4096 among 600"}[kind]
     key = {"uniform": "decode", "ragged": "decode_ragged"}.get(kind, "")
+    if layout == "head_major":
+        key += "_head_major"
     return {"value": round(gbs, 2), "unit": "GB/s", "ms_per_launch": round(ms, 5),
             "bytes_per_launch": nb, "lengths": f"{desc}, sum {int(lens.sum())}",
-            "entry_point": "bn_gqa_decode_planned" if planned else "bn_gqa_decode",
+            "cache_layout": "[B, L, Hkv, 64]" if layout == "token_major" else "[B, Hkv, L, 64]",
+            "entry_point": ("bn_gqa_decode_planned" if planned else
+                            "bn_gqa_decode" if layout == "token_major" else "bn_gqa_decode_strided"),
             "roofline": roofline("hbm", gbs, PEAK_HBM_GBS, "GB/s",
                                  measured_traffic("decode_planned_" + kind) if planned
                                  else measured_traffic(key))}
@@ -863,6 +874,9 @@ def main():
     ap.add_argument("--tl-warmup", type=int, default=2,
                     help="config 4: warm-up decode tokens before the timed generate (0: none, "
                          "so a kernel trace holds exactly one prefill + 128 steps)")
+    ap.add_argument("--decode-token-major", choices=("beside", "skip"), default="beside",
+                    help="config 3's token-major cache figure beside the head-major one, or "
+                         "skipped (profiling runs whose counters must cover one layout)")
     ap.add_argument("--only", default="",
                     help="comma list of extra workloads (default: all but copy): "
                          "decode,ragged,planned,fp32,norm,long,addnorm,swiglu,linear,bwd,block,tinyllama,copy; "
@@ -893,12 +907,17 @@ def main():
            "roofline": head["roofline"]}
     print(f"prefill bf16: {head['value']} TFLOP/s ({head['ms_per_launch']} ms)", file=sys.stderr,
           flush=True)
-    if want("decode"):
-        out["decode"] = bench_decode("uniform", K, W)
-        print(f"decode: {out['decode']['value']} GB/s", file=sys.stderr, flush=True)
-    if want("ragged"):
-        out["decode_ragged"] = bench_decode("ragged", K, W)
-        print(f"decode ragged: {out['decode_ragged']['value']} GB/s", file=sys.stderr, flush=True)
+    # config 3 in the head-major cache layout (bn_gqa_decode_strided), the
+    # token-major one (bn_gqa_decode) beside it
+    beside =args.decode_token_major == "beside"
+    for sel, key, kind in (("decode", "decode", "uniform"), ("ragged", "decode_ragged", "ragged")):
+        if want(sel):
+            out[key] = bench_decode(kind, K, W, layout="head_major")
+            if beside:
+                out[key]["token_major"] = bench_decode(kind, K, W)
+            print(f"{key}: {out[key]['value']} GB/s (token-major "
+                  f"{out[key]['token_major']['value'] if beside else 'skipped'})", file=sys.stderr,
+                  flush=True)
     if want("planned"):
         out["decode_planned"] = bench_decode_planned(K, W)
         print(f"decode planned: { {k: v['planned']['value'] for k, v in out['decode_planned'].items() if k != 'roofline'} }",

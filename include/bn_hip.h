@@ -350,6 +350,28 @@ int bn_gqa_decode(int dtype, const void *q, const void *k_cache,
                   int head_dim, float scale, void *workspace,
                   size_t workspace_bytes, void *stream);
 
+/* bn_gqa_decode over caches of any layout whose key rows are head_dim
+ * contiguous elements: element k of key row j of KV head g of sequence b is
+ * cache[b*cache_seq_stride + g*cache_head_stride + j*cache_row_stride + k]
+ * (strides in elements, positive multiples of 16 bytes; K and V share them).
+ * The same row of the reference as bn_gqa_decode (the last row of the causal
+ * softmax, op_softmax.cuh:89-99, over the prefix llama_model.py:135-141
+ * recomputes); the reference keeps no cache, so its layout is this library's
+ * choice.  bn_gqa_decode is this call with the contiguous
+ * [batch, max_len, n_kv_heads, head_dim] strides (max_len*n_kv_heads*head_dim,
+ * head_dim, n_kv_heads*head_dim).  A head-major [batch, n_kv_heads, max_len,
+ * head_dim] cache (n_kv_heads*max_len*head_dim, max_len*head_dim, head_dim)
+ * keeps each (sequence, KV head)'s rows contiguous in HBM and streams faster
+ * on bf16 caches of at least one (sequence, KV head) per compute unit.  Same
+ * kernels, workspace and results as bn_gqa_decode on the same values. */
+int bn_gqa_decode_strided(int dtype, const void *q, const void *k_cache,
+                          const void *v_cache, const int32_t *seq_lens, void *o,
+                          int batch, int max_len, int n_heads, int n_kv_heads,
+                          int head_dim, int64_t cache_seq_stride,
+                          int64_t cache_head_stride, int64_t cache_row_stride,
+                          float scale, void *workspace, size_t workspace_bytes,
+                          void *stream);
+
 /* bn_gqa_decode with the lengths also on the host (h_seq_lens: host int32
  * [batch], the values seq_lens holds on the device), as a serving loop has
  * them.  Replaces the same row as bn_gqa_decode (the last row of the causal

@@ -145,6 +145,41 @@ def test_decode_noalloc_validation(kw, status):
     assert m.startswith("GQA decode (no allocation):")
 
 
+@pytest.mark.parametrize("kw,status", [
+    (dict(bs=0), B.BN_ERR_INVALID_ARG),
+    (dict(hs=-64), B.BN_ERR_INVALID_ARG),
+    (dict(rs=60), B.BN_ERR_INVALID_ARG),                    # rows not 16-byte aligned (bf16)
+    (dict(dt=B.BN_F32, rs=66), B.BN_ERR_INVALID_ARG),       # nor in fp32
+    (dict(hs=1 << 41), B.BN_ERR_INVALID_ARG),
+    (dict(H=24), B.BN_ERR_UNSUPPORTED),                     # the shape checks of bn_gqa_decode
+    (dict(lens=0), B.BN_ERR_INVALID_ARG),
+    (dict(ws=0x9000, wsb=16), B.BN_ERR_INVALID_ARG),
+])
+def test_decode_strided_validation(kw, status):
+    # head-major [64, 4, 4096, 64] strides unless changed; fake pointers, no GPU
+    a = dict(dt=B.BN_BF16, q=0x1000, k=0x2000, v=0x3000, lens=0x5000, o=0x4000, B=64,
+             L=4096, H=32, Hkv=4, D=64, bs=4 * 4096 * 64, hs=4096 * 64, rs=64, sc=0.125,
+             ws=None, wsb=0)
+    a.update(kw)
+    s, m = st("bn_gqa_decode_strided", a["dt"], a["q"], a["k"], a["v"], a["lens"], a["o"],
+              a["B"], a["L"], a["H"], a["Hkv"], a["D"], a["bs"], a["hs"], a["rs"], a["sc"],
+              a["ws"], a["wsb"], None)
+    assert s == status, m
+    assert m.startswith("GQA decode (strided):"), m
+
+
+def test_decode_strided_fp32_alignment():
+    """fp32 rows need 4-element strides, bf16 rows 8: a stride of 4 passes the
+    fp32 check and fails the bf16 one (the fp32 call then stops at the NULL
+    lengths, before any device work)."""
+    args = lambda dt: (dt, 0x1000, 0x2000, 0x3000, 0, 0x4000, 1, 256, 8, 1, 64, 4 * 256, 4, 64,
+                       0.125, None, 0, None)
+    s, m = st("bn_gqa_decode_strided", *args(B.BN_BF16))
+    assert s == B.BN_ERR_INVALID_ARG and "multiples of 8 elements" in m, m
+    s, m = st("bn_gqa_decode_strided", *args(B.BN_F32))
+    assert s == B.BN_ERR_INVALID_ARG and "NULL pointer" in m, m
+
+
 @pytest.mark.parametrize("kw,status,stem", [
     (dict(hl=0), B.BN_ERR_INVALID_ARG, "GQA decode (planned): NULL host lengths"),
     (dict(ws=0x9000, wsb=16), B.BN_ERR_INVALID_ARG, "GQA decode (planned): workspace of 16 bytes"),
@@ -416,3 +451,23 @@ def test_fused_head_attention_validation(kw, status, msg):
     s, m = st("bn_fused_head_attention", q, k, v, o, a["H"], a["Hkv"], a["D"], 0.125, 1, 0, None)
     assert s == status, m
     assert m.startswith("Fused-head attention:") and msg in m, m
+
+
+def test_decode_wrappers_refuse_layouts_they_cannot_pass():
+    """bnhip.gqa_decode passes any cache whose key rows are contiguous (through
+    bn_gqa_decode_strided) and refuses the rest on the host; the planned call
+    takes contiguous caches only (CPU tensors: nothing reaches a device)."""
+    import torch
+    q = torch.zeros((2, 8, 64))
+    kc = torch.zeros((2, 16, 2, 64))
+    hm = torch.zeros((2, 2, 16, 64)).transpose(1, 2)
+    lens = torch.zeros(2, dtype=torch.int32)
+    with pytest.raises(ValueError, match="same shape and strides"):
+        B.gqa_decode(q, kc, hm, lens)
+    with pytest.raises(ValueError, match="stride 1 along head_dim"):
+        cols = torch.zeros((2, 16, 2, 128))[..., ::2]
+        B.gqa_decode(q, cols, cols, lens)
+    with pytest.raises(ValueError, match="q and o must be contiguous"):
+        B.gqa_decode(torch.zeros((8, 2, 64)).transpose(0, 1), kc, kc, lens)
+    with pytest.raises(ValueError, match="must be contiguous"):
+        B.gqa_decode_planned(q, hm, hm, lens, [16, 16])
