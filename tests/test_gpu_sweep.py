@@ -162,8 +162,10 @@ def test_decode_sweep(target, i):
     q = draw(rng, (Bn, H, 64), dtype)
     kc = draw(rng, (Bn, L, Hkv, 64), dtype)
     vc = draw(rng, (Bn, L, Hkv, 64), dtype)
-    got = host(B.gqa_decode(dev(q, TD[dtype]), dev(kc, TD[dtype]), dev(vc, TD[dtype]),
-                            torch.from_numpy(lens).cuda(), scale=SCALE))
+    qd, kd, vd = dev(q, TD[dtype]), dev(kc, TD[dtype]), dev(vc, TD[dtype])
+    ld = torch.from_numpy(lens).cuda()
+    out = B.gqa_decode(qd, kd, vd, ld, scale=SCALE)
+    got = host(out)
     for b in range(Bn):
         Lb = int(min(max(lens[b], 0), L))
         if Lb == 0:
@@ -172,6 +174,26 @@ def test_decode_sweep(target, i):
         ref = O.gqa_decode(q[b:b + 1], kc[b:b + 1, :Lb], vc[b:b + 1, :Lb],
                            np.array([Lb], np.int32), SCALE)
         assert_close(got[b:b + 1], ref, TOL[dtype], f"{what} b={b} len={Lb}")
+    # the same caches in a random other layout (bn_gqa_decode_strided): the same bits
+    head_major, gap, pad = bool(rng.integers(2)), int(rng.choice([0, 1, 5])), int(rng.choice([0, 8, 32]))
+    ks, vs = (strided_cache(c, head_major, gap, pad) for c in (kd, vd))
+    assert torch.equal(B.gqa_decode(qd, ks, vs, ld, scale=SCALE), out), \
+        f"{what}: strided (head_major={head_major}, gap={gap}, pad={pad}) differs"
+
+
+def strided_cache(c, head_major, gap, pad):
+    """c [B, L, Hkv, 64] copied into a wider storage -- head-major [B, Hkv, L + gap, 64 + pad]
+    or token-major [B, L + gap, Hkv, 64 + pad], the unused elements NaN -- returned as a
+    [B, L, Hkv, 64] view of it."""
+    Bn, L, Hkv, D = c.shape
+    if head_major:
+        s = torch.full((Bn, Hkv, L + gap, D + pad), float("nan"), dtype=c.dtype, device=c.device)
+        v = s[:, :, :L, :D].transpose(1, 2)
+    else:
+        s = torch.full((Bn, L + gap, Hkv, D + pad), float("nan"), dtype=c.dtype, device=c.device)
+        v = s[:, :L, :, :D]
+    v.copy_(c)
+    return v
 
 
 # ------------------------------------------------------------------- backward
