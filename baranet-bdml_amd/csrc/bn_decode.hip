@@ -544,10 +544,11 @@ void decode_bf16_mfma_kernel(DecodeParams p) {
 
 // bf16 cache, n_kv_heads a multiple of 4: whole-row streaming version.
 // A workgroup = (sequence, 4 consecutive KV heads, chunk).  Its 256 threads
-// load each 32-key tile as contiguous 16-byte chunks of the cache rows (one
-// load instruction covers 1 KB: two token rows of the 4 heads), which
-// streams HBM far better than per-head 64-byte pieces, into registers two
-// tiles ahead, then write it row-major to LDS.  Wave w is KV head g0 + w:
+// load each 32-key tile as 16-byte chunks of the 4 heads' 128-byte key rows
+// (in a token-major cache one load instruction covers 1 KB: two token rows
+// of the 4 heads, which streams HBM far better than per-head 64-byte
+// pieces; other layouts reach each head's row through the head stride),
+// into registers two tiles ahead, then write it row-major to LDS.  Wave w is KV head g0 + w:
 // K fragments come from LDS with ds_read_b128, V^T fragments with the gfx950
 // transpose read ds_read_b64_tr_b16, and the wave writes its own partials.
 typedef short ds4_t __attribute__((ext_vector_type(4)));
