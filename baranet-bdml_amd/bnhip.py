@@ -114,6 +114,8 @@ def lib():
         "bn_gqa_decode_strided": ([i, vp, vp, vp, vp, vp] + [i] * 5 + [i64] * 3 + [f, vp, sz, vp], i),
         "bn_gqa_decode_planned_workspace_size": ([i, i, i, i, i], sz),
         "bn_gqa_decode_planned": ([i, vp, vp, vp, vp, vp, vp] + [i] * 5 + [f, vp, sz, vp], i),
+        "bn_gqa_decode_planned_strided": ([i, vp, vp, vp, vp, vp, vp] + [i] * 5 + [i64] * 3 +
+                                          [f, vp, sz, vp], i),
     }
     for name, (args, res) in sig.items():
         fn = getattr(L, name)
@@ -297,7 +299,9 @@ def gqa_decode_planned(q, k_cache, v_cache, seq_lens, h_seq_lens, o=None, scale=
                        workspace=None, stream=None):
     """gqa_decode with the lengths also on the host (h_seq_lens: a sequence of
     ints, the values of the device tensor seq_lens): equal shares of the
-    batch's tiles per compute unit when the lengths are ragged."""
+    batch's tiles per compute unit when the lengths are ragged.  Caches as
+    for gqa_decode: contiguous, or any layout with contiguous key rows
+    (bn_gqa_decode_planned_strided)."""
     import numpy as np
     import torch
     B, H, D = q.shape
@@ -305,15 +309,25 @@ def gqa_decode_planned(q, k_cache, v_cache, seq_lens, h_seq_lens, o=None, scale=
     if o is None:
         o = torch.empty_like(q)
     sc = 1.0 / math.sqrt(D) if scale is None else scale
-    if not all(t.is_contiguous() for t in (q, o, k_cache, v_cache)):
-        raise ValueError("gqa_decode_planned: q, o and the caches must be contiguous")
+    if not (q.is_contiguous() and o.is_contiguous()):
+        raise ValueError("gqa_decode_planned: q and o must be contiguous [B, H, D]")
+    if tuple(v_cache.shape) != tuple(k_cache.shape) or v_cache.stride() != k_cache.stride():
+        raise ValueError("gqa_decode_planned: k_cache and v_cache must have the same shape and strides")
     hl = np.ascontiguousarray(np.asarray(h_seq_lens, dtype=np.int32))
     assert hl.shape == (B,)
     ws_ptr, ws_bytes = (None, 0) if workspace is None else (workspace.data_ptr(),
                                                             workspace.numel() * workspace.element_size())
-    call("bn_gqa_decode_planned", _torch_dtype_code(q), q.data_ptr(), k_cache.data_ptr(),
+    if k_cache.is_contiguous():
+        call("bn_gqa_decode_planned", _torch_dtype_code(q), q.data_ptr(), k_cache.data_ptr(),
+             v_cache.data_ptr(), seq_lens.data_ptr(), hl.ctypes.data, o.data_ptr(), B, Lmax, H, Hkv,
+             D, sc, ws_ptr, ws_bytes, stream_of(stream))
+        return o
+    if k_cache.stride(3) != 1:
+        raise ValueError("gqa_decode_planned: cache key rows must be contiguous (stride 1 along head_dim)")
+    call("bn_gqa_decode_planned_strided", _torch_dtype_code(q), q.data_ptr(), k_cache.data_ptr(),
          v_cache.data_ptr(), seq_lens.data_ptr(), hl.ctypes.data, o.data_ptr(), B, Lmax, H, Hkv, D,
-         sc, ws_ptr, ws_bytes, stream_of(stream))
+         k_cache.stride(0), k_cache.stride(2), k_cache.stride(1), sc, ws_ptr, ws_bytes,
+         stream_of(stream))
     return o
 
 

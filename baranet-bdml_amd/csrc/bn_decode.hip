@@ -24,6 +24,7 @@
 
 #include <algorithm>
 #include <atomic>
+#include <cstdlib>
 #include <mutex>
 #include <vector>
 
@@ -34,12 +35,6 @@
 // to a kernel (on the host the name is only a stand-in); it uses the device
 // address hipGetSymbolAddress returns for the current device.
 static __device__ __align__(256) float scratch[BN_GQA_DECODE_SCRATCH_BYTES / sizeof(float)];
-
-// Per-unit part counters of bn_gqa_decode_planned: slots of 256 counters,
-// zero at load time; each launch takes the next slot of a host-side ring and
-// every cut unit's last part clears its counter, so a slot is zero again when
-// its turn comes round (launches share a slot only when 16 are in flight).
-static __device__ __align__(256) uint32_t plan_counters[16 * 256];
 
 // Per-(sequence, query head) split counters of the short-cache decode's
 // in-launch merge: slots of kShortMaxUnits counters, zero at load time, a
@@ -929,40 +924,58 @@ __global__ __launch_bounds__(64 * WWV) void decode_bf16_whole_kernel(DecodeParam
 // share touches a few units (segments); its waves take the share's tiles in
 // turn (tile i -> wave i % 4, the loads running on across segment
 // boundaries), keep one (m, l, acc) per segment, and merge them through LDS
-// at the end.  A unit lying wholly in the share is written directly; a cut
-// unit's part writes an (m, l, acc) record through to memory, and the last
-// of its parts to arrive (a per-unit counter) reads the records back past
-// the caches, merges them and writes the output -- in the same launch.
+// at the end.  A unit lying wholly in the share is written directly.  A cut
+// unit's head (its first tiles: the LAST segment of the share where it
+// starts) merges it; every later part is the FIRST segment of its share, so
+// its waves finish it early and hand their states to a fifth wave of the
+// workgroup (through LDS and a workgroup counter), which merges them and
+// writes the part's (m, l, acc) record to memory while the four stream on
+// (written through to memory, a store holds up the wave that issued it, so
+// none of the streaming waves issues one) -- every 64-bit word holding a
+// value and this launch's epoch, so a reader knows a word is this launch's
+// without any ordering between words, counters or waits.  At the end the
+// head loads the records (one round trip: they were written while the rest
+// of the shares streamed), merges and writes the output.  A record not yet this launch's
+// is polled again a bounded number of times; past that the head streams the
+// unit's remaining keys itself (never needed when the launch's workgroups
+// run side by side, which 256 of them on 256 compute units do), so no
+// workgroup waits on another without limit.
 constexpr int kPlanBins = 256;   // workgroups of a planned launch, at most
 constexpr int kPlanUnits = 256;  // (sequence, KV head) units, at most
 constexpr int kPlanSeg = 8;      // units one share may touch, at most
-constexpr int kPlanSlots = 16;   // counter slots (plan_counters): planned launches in flight
-
-static_assert(kPlanSlots * kPlanUnits == 16 * 256, "plan_counters holds kPlanSlots slots of kPlanUnits");
+constexpr int kPlanPolls = 1 << 14;  // re-polls of a record before the head streams the keys itself
+// a part's record, G query heads: acc[G][HD], then m[G] (log2 units), l[G]
+// (64-bit words; the writer wave's store instructions cover 512 contiguous bytes)
+template <int G> constexpr int rec_words() { return G * HD + 2 * G; }
 
 struct PlanParams {
   const void *q, *k, *v;
   void *o;
-  float *rec;     // part records [record][G][HD + 2]: m (log2 units), l, acc
-  uint32_t *cnt;  // this launch's per-unit counters: zero at launch, cleared by each unit's last part
+  uint64_t *rec;  // part records [record][rec_words<G>()], epoch in bits 32..63 of each word
   int batch, max_len, n_heads, n_kv_heads, n_units, share, total;  // share: sequence tiles per group
   float c;                         // scale * log2(e)
+  uint32_t epoch;                  // this launch's tag (never 0; a fresh workspace may hold anything)
+  int max_polls;                   // kPlanPolls; -1: ignore records, the heads stream every key
   int64_t kv_bs, kv_hs, kv_rs;     // cache strides (elements): sequence, KV head, key row
   uint32_t wg_start[kPlanBins];    // group: first sequence (bits 0..15), its first tile (16..31)
   uint32_t unit[kPlanUnits];       // record base (0..11), first group (12..23), parts (24..31)
   int32_t len[kPlanUnits];         // per sequence: length, clamped to [0, max_len]
 };
 
+// WWV streaming waves and one record-writer wave per workgroup
+constexpr int kPlanThreads = 64 * (WWV + 1);
+
 template <int G>
-__global__ __launch_bounds__(64 * WWV) void decode_bf16_planned_kernel(PlanParams p) {
+__global__ __launch_bounds__(kPlanThreads) void decode_bf16_planned_kernel(PlanParams p) {
   __shared__ __attribute__((aligned(16))) bf16_t KT[WWV][TK * WKP];
   __shared__ __attribute__((aligned(16))) bf16_t VT[WWV][TK * WKP];
   __shared__ float red_m[kPlanSeg][WWV][G], red_l[kPlanSeg][WWV][G];
   __shared__ float red_o[kPlanSeg][WWV][G][HD];
-  __shared__ int s_last;
+  __shared__ uint32_t seg0_done;  // streaming waves that have handed over segment 0
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const bool streamer = wave < WWV;  // wave WWV writes segment 0's record
   const int l16 = lane & 15, grp = lane >> 4;
   const int bin = blockIdx.x, Hkv = p.n_kv_heads;
   // workgroups come in groups of Hkv, one per KV head, that walk the same
@@ -977,9 +990,11 @@ __global__ __launch_bounds__(64 * WWV) void decode_bf16_planned_kernel(PlanParam
   for (int u = bin; u < p.n_units; u += gridDim.x) {
     if (p.len[u / Hkv] == 0) {
       bf16_t *out = (bf16_t *)p.o + ((int64_t)(u / Hkv) * p.n_heads + (int64_t)(u % Hkv) * G) * HD;
-      for (int idx = tid; idx < G * HD; idx += 64 * WWV) out[idx] = f32_to_bf16(0.f);
+      for (int idx = tid; idx < G * HD; idx += kPlanThreads) out[idx] = f32_to_bf16(0.f);
     }
   }
+  if (tid == 0) seg0_done = 0;
+  __syncthreads();
   // This group's share [grp_id * share, +ntile) of the batch's sequence
   // tiles, as segments (one sequence each, sequences with keys in order) of
   // this workgroup's KV head.  Every wave walks them itself in scalar
@@ -1112,21 +1127,41 @@ __global__ __launch_bounds__(64 * WWV) void decode_bf16_planned_kernel(PlanParam
       o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb, o[dt], 0, 0, 0);
     }
   };
-  // this wave's state of segment s into LDS (o[dt][i] = O^T[16dt + 4grp + i][head l16])
-  auto flush = [&](int s) __attribute__((always_inline)) {
+  // segment 0 of the share is a later part of a cut unit (not its head):
+  // every wave writes its state of it to the part's record as it moves on
+  uint64_t *rec0 = nullptr;
+  if (ntile > 0) {
+    const int b0 = (int)(p.wg_start[grp_id] & 0xffffu);
+    const uint32_t info0 = p.unit[b0 * Hkv + gh];
+    const int parts0 = (int)(info0 >> 24), part0 = grp_id - (int)((info0 >> 12) & 0xfffu);
+    if (parts0 > 1 && part0 > 0 && part0 < parts0)
+      rec0 = p.rec + (int64_t)((info0 & 0xfffu) + part0) * rec_words<G>();
+  }
+  const uint64_t tag = (uint64_t)p.epoch << 32;
+  auto put = [&](uint64_t *a, float v) __attribute__((always_inline)) {
+    __hip_atomic_store(a, tag | __builtin_bit_cast(uint32_t, v), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_SYSTEM);
+  };
+  // this wave's state of segment s into LDS slot ls (o[dt][i] = O^T[16dt + 4grp + i][head l16])
+  auto flush_to = [&](int s, int ls) __attribute__((always_inline)) {
     float lt = l + __shfl_xor(l, 16, 64);
     lt += __shfl_xor(lt, 32, 64);
     if (l16 < G) {
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) red_o[s][wave][l16][16 * dt + 4 * grp + i] = o[dt][i];
+        for (int i = 0; i < 4; ++i) red_o[ls][wave][l16][16 * dt + 4 * grp + i] = o[dt][i];
       if (grp == 0) {
-        red_m[s][wave][l16] = m * c;  // -inf: no key of s in this wave
-        red_l[s][wave][l16] = lt;
+        red_m[ls][wave][l16] = m * c;  // -inf: no key of s in this wave
+        red_l[ls][wave][l16] = lt;
       }
     }
+    if (s == 0 && rec0) {  // segment 0 handed to the writer wave (LDS writes first)
+      __builtin_amdgcn_wave_barrier();
+      if (lane == 0) __hip_atomic_fetch_add(&seg0_done, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
   };
+  auto flush = [&](int s) __attribute__((always_inline)) { flush_to(s, s); };
   auto reset = [&]() __attribute__((always_inline)) {
     m = -INFINITY;
     l = 0.f;
@@ -1139,7 +1174,7 @@ __global__ __launch_bounds__(64 * WWV) void decode_bf16_planned_kernel(PlanParam
   // when pre enters a new segment its query rows are loaded into qn, taken
   // over by qb when the wave's tiles reach that segment.
   int sc = -1;  // segment of the wave's running state
-  if (wave < ntile) {  // wave-uniform
+  if (streamer && wave < ntile) {  // wave-uniform
     Seg cur, pre;
     seg_first(cur);
     seg_adv(cur, wave);
@@ -1183,19 +1218,48 @@ __global__ __launch_bounds__(64 * WWV) void decode_bf16_planned_kernel(PlanParam
       }
     }
   }
-  if (sc >= 0) flush(sc);
-  reset();
-  for (int x = sc + 1; x < nseg; ++x) flush(x);
+  if (streamer) {
+    if (sc >= 0) flush(sc);
+    reset();
+    for (int x = sc + 1; x < nseg; ++x) flush(x);
+  } else if (rec0) {
+    // the writer wave: once the streaming waves have handed over segment 0
+    // (bounded wait inside this workgroup; without the record the head
+    // streams the keys itself), merge their states and write the record
+    int polls = 0;
+    while (__hip_atomic_load(&seg0_done, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < (uint32_t)WWV &&
+           polls < kPlanPolls) {
+      __builtin_amdgcn_s_sleep(2);
+      ++polls;
+    }
+    if (polls < kPlanPolls) {
+      for (int idx = lane; idx < G * HD; idx += 64) {
+        const int h = idx / HD, d = idx - h * HD;
+        float M = red_m[0][0][h];
+#pragma unroll
+        for (int w = 1; w < WWV; ++w) M = fmaxf(M, red_m[0][w][h]);
+        float L = 0.f, A = 0.f;
+#pragma unroll
+        for (int w = 0; w < WWV; ++w) {
+          const float wt = __builtin_amdgcn_exp2f(red_m[0][w][h] - M);
+          L += red_l[0][w][h] * wt;
+          A += red_o[0][w][h][d] * wt;
+        }
+        put(rec0 + idx, A);
+        if (d == 0) {
+          put(rec0 + G * HD + h, M);
+          put(rec0 + G * HD + G + h, L);
+        }
+      }
+    }
+  }
   __syncthreads();
 
-  // Merge the waves of each segment.  A unit wholly in this share is
-  // written; a cut unit's part writes its record through to memory
-  // (system-scope stores, waited for), then counts itself on the unit's
-  // counter; the part that counts last reads every record past the caches
-  // (system-scope loads) and writes the output.  No cache write-back or
-  // invalidation (an agent-scope release/acquire pair per part measured
-  // twice the kernel's time on config 3; atomic exchanges and atomic adds
-  // of zero for the records, five times).
+  // Merge the waves of each segment.  A unit wholly in this share is written.
+  // A cut unit's later parts wrote their records from the waves (above); its
+  // head -- the share's last segment -- loads them past the caches
+  // (system-scope loads), each word tagged with this launch's epoch, merges
+  // and writes the output.
   Seg x;
   if (nseg > 0) seg_first(x);
   for (int s = 0; s < nseg; ++s) {
@@ -1203,61 +1267,130 @@ __global__ __launch_bounds__(64 * WWV) void decode_bf16_planned_kernel(PlanParam
     const int b = x.b, g = gh, u = b * Hkv + g;
     const uint32_t info = p.unit[u];
     const int parts = (int)(info >> 24), part = grp_id - (int)((info >> 12) & 0xfffu);
-    if (parts > 1 && (part < 0 || part >= parts)) continue;  // a plan inconsistent with the walk: no write
+    if (parts > 1 && part != 0) continue;  // a later part: its record is written
     bf16_t *out = (bf16_t *)p.o + ((int64_t)b * p.n_heads + (int64_t)g * G) * HD;
-    float *rec = p.rec + (int64_t)((info & 0xfffu) + part) * G * (HD + 2);
-    for (int idx = tid; idx < G * HD; idx += 64 * WWV) {
+    // this share's waves: (M, L, A) of output idx from LDS slot ls
+    auto own = [&](int ls, int idx, float &M, float &L, float &A) __attribute__((always_inline)) {
       const int h = idx / HD, d = idx - h * HD;
-      float M = red_m[s][0][h];
+      M = red_m[ls][0][h];
 #pragma unroll
-      for (int w = 1; w < WWV; ++w) M = fmaxf(M, red_m[s][w][h]);  // finite: some wave has keys
-      float L = 0.f, A = 0.f;
+      for (int w = 1; w < WWV; ++w) M = fmaxf(M, red_m[ls][w][h]);
+      L = 0.f;
+      A = 0.f;
+      if (M == -INFINITY) return;  // no key in any wave (a fallback slot can be empty)
 #pragma unroll
       for (int w = 0; w < WWV; ++w) {
-        const float wt = __builtin_amdgcn_exp2f(red_m[s][w][h] - M);
-        L += red_l[s][w][h] * wt;
-        A += red_o[s][w][h][d] * wt;
+        const float wt = __builtin_amdgcn_exp2f(red_m[ls][w][h] - M);
+        L += red_l[ls][w][h] * wt;
+        A += red_o[ls][w][h][d] * wt;
       }
-      if (parts <= 1) {
-        out[idx] = f32_to_bf16(A / L);
-      } else {
-        float *r = rec + h * (HD + 2);
-        __hip_atomic_store(r + 2 + d, A, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-        if (d == 0) {
-          __hip_atomic_store(r, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-          __hip_atomic_store(r + 1, L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-        }
-      }
-    }
-    if (parts <= 1) continue;  // uniform
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's record stores done
-    __syncthreads();
-    if (tid == 0) {
-      const uint32_t seen = __hip_atomic_fetch_add(p.cnt + u, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      const bool last = seen == (uint32_t)parts - 1;
-      if (last) __hip_atomic_store(p.cnt + u, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      s_last = last;
-    }
-    __syncthreads();
-    if (s_last) {
-      float *rec0 = p.rec + (int64_t)(info & 0xfffu) * G * (HD + 2);
-      for (int idx = tid; idx < G * HD; idx += 64 * WWV) {
-        const int h = idx / HD, d = idx - h * HD;
-        // system-scope loads: past the caches, from where the stores went
-        auto rd = [&](const float *a) { return __hip_atomic_load(a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM); };
-        float M = -INFINITY;
-        for (int q = 0; q < parts; ++q) M = fmaxf(M, rd(rec0 + (q * G + h) * (HD + 2)));
-        float L = 0.f, A = 0.f;
-        for (int q = 0; q < parts; ++q) {
-          float *r = rec0 + (q * G + h) * (HD + 2);
-          const float wt = __builtin_amdgcn_exp2f(rd(r) - M);
-          L += rd(r + 1) * wt;
-          A += rd(r + 2 + d) * wt;
-        }
+    };
+    if (parts <= 1) {
+      for (int idx = tid; idx < G * HD; idx += kPlanThreads) {
+        float M, L, A;
+        own(s, idx, M, L, A);
         out[idx] = f32_to_bf16(A / L);
       }
+      continue;
     }
-    __syncthreads();  // s_last is rewritten by the next segment
+    // the head of a cut unit: this share holds its first tiles, the later
+    // parts the rest; each thread merges its outputs from its own loads
+    constexpr int NO = (G * HD + kPlanThreads - 1) / kPlanThreads;  // outputs per thread
+    const uint64_t *recb = p.rec + (int64_t)(info & 0xfffu) * rec_words<G>();
+    float Mv[NO], Lv[NO], Av[NO];
+    bool ok = true;
+    auto gather = [&]() __attribute__((always_inline)) {
+      ok = true;
+#pragma unroll
+      for (int j = 0; j < NO; ++j) {
+        const int idx = min(tid + kPlanThreads * j, G * HD - 1);  // past G*HD: a repeat, not stored
+        own(s, idx, Mv[j], Lv[j], Av[j]);
+      }
+      // one part at a time, every word of the part requested before any is
+      // used: one round trip per later part
+      for (int q = 1; q < parts; ++q) {
+        const uint64_t *r = recb + (int64_t)q * rec_words<G>();
+        uint64_t wm[NO], wl[NO], wa[NO];
+#pragma unroll
+        for (int j = 0; j < NO; ++j) {
+          const int idx = min(tid + kPlanThreads * j, G * HD - 1);
+          const int h = idx / HD;
+          wm[j] = __hip_atomic_load(r + G * HD + h, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+          wl[j] = __hip_atomic_load(r + G * HD + G + h, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+          wa[j] = __hip_atomic_load(r + idx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        }
+#pragma unroll
+        for (int j = 0; j < NO; ++j) {
+          ok = ok && (wm[j] >> 32) == p.epoch && (wl[j] >> 32) == p.epoch && (wa[j] >> 32) == p.epoch;
+          const float mq = __builtin_bit_cast(float, (uint32_t)wm[j]);
+          const float m2 = fmaxf(Mv[j], mq);  // finite: this share's part has keys
+          const float a1 = __builtin_amdgcn_exp2f(Mv[j] - m2), a2 = __builtin_amdgcn_exp2f(mq - m2);
+          Lv[j] = Lv[j] * a1 + __builtin_bit_cast(float, (uint32_t)wl[j]) * a2;
+          Av[j] = Av[j] * a1 + __builtin_bit_cast(float, (uint32_t)wa[j]) * a2;
+          Mv[j] = m2;
+        }
+      }
+    };
+    bool all_ok = false;
+    if (p.max_polls >= 0) {
+      gather();
+      all_ok = __syncthreads_and(ok);
+      for (int poll = 0; !all_ok && poll < p.max_polls; ++poll) {
+        __builtin_amdgcn_s_sleep(4);
+        gather();
+        all_ok = __syncthreads_and(ok);
+      }
+    }
+    if (!all_ok) {
+      // Fallback: stream the unit's keys past this share's tiles here, into a
+      // free LDS slot (slot 0 is finished when s > 0; slot 1 is unused when
+      // the share holds this segment only), and merge with this share's part.
+      const int ls = s == 0 ? 1 : 0;
+      // local tile i of x holds keys x.kb0 + 32 i, so the later parts start
+      // at the unit's tile x.kb0 / 32 + x.end
+      const int first_rest = x.kb0 / TK + x.end;
+      const int rest = tiles_of(b) - first_rest;
+      Seg y = x;
+      y.kb0 = TK * first_rest;  // local tile i of y: keys kb0 + 32 i
+      if (streamer) {
+        reset();
+        if (wave < rest) {
+          dbf16x8_t qf[2];
+          gload_q(qf, y);
+          qb[0] = qf[0];
+          qb[1] = qf[1];
+          for (int i = wave; i < rest; i += WWV) {
+            RegTile r;
+            gload(r, i, y);
+            __builtin_amdgcn_wave_barrier();
+            lstore(r);
+            __builtin_amdgcn_wave_barrier();
+            compute(y.kb0 + TK * i, y.len);
+            __builtin_amdgcn_wave_barrier();
+          }
+        }
+        flush_to(-1, ls);
+      }
+      __syncthreads();
+#pragma unroll
+      for (int j = 0; j < NO; ++j) {
+        const int idx = min(tid + kPlanThreads * j, G * HD - 1);
+        float M, L, A, M2, L2, A2;
+        own(s, idx, M, L, A);
+        own(ls, idx, M2, L2, A2);
+        const float mm = fmaxf(M, M2);
+        const float a1 = __builtin_amdgcn_exp2f(M - mm), a2 = __builtin_amdgcn_exp2f(M2 - mm);
+        Mv[j] = mm;
+        Lv[j] = L * a1 + L2 * a2;
+        Av[j] = A * a1 + A2 * a2;
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < NO; ++j) {
+      const int idx = tid + kPlanThreads * j;
+      if (idx < G * HD) out[idx] = f32_to_bf16(Av[j] / Lv[j]);
+    }
+    __syncthreads();  // the fallback's LDS slot and state are reused by the next segment
   }
 }
 
@@ -1381,8 +1514,9 @@ constexpr int kMaxScratchDevices = 64;
 static std::mutex g_scratch_mu;
 static void *g_scratch_ptr[kMaxScratchDevices];
 
-static void *g_plan_cnt_ptr[kMaxScratchDevices];
-static std::atomic<uint32_t> g_plan_next{0};
+// the planned decode's launch epochs (the tag of every record word a launch
+// writes; never 0)
+static std::atomic<uint32_t> g_plan_epoch{0};
 static void *g_short_cnt_ptr[kMaxScratchDevices];
 static std::atomic<uint32_t> g_short_next{0};
 
@@ -1393,17 +1527,13 @@ int decode_scratch_setup(int device) {
                                         std::to_string(kMaxScratchDevices) + " devices)");
   std::lock_guard<std::mutex> lk(g_scratch_mu);
   if (g_scratch_ptr[device]) return BN_OK;
-  void *ptr = nullptr, *cnt = nullptr;
+  void *ptr = nullptr;
   BN_HIP_TRY(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
   if (!ptr) return fail(BN_ERR_HIP, "bn_init: decode scratch has no device address");
-  // the planned decode's part counters, looked up with the scratch
-  BN_HIP_TRY(hipGetSymbolAddress(&cnt, HIP_SYMBOL(plan_counters)));
-  if (!cnt) return fail(BN_ERR_HIP, "bn_init: decode plan counters have no device address");
   void *scnt = nullptr;  // the short-cache decode's split counters
   BN_HIP_TRY(hipGetSymbolAddress(&scnt, HIP_SYMBOL(short_counters)));
   if (!scnt) return fail(BN_ERR_HIP, "bn_init: short decode counters have no device address");
   g_scratch_ptr[device] = ptr;
-  g_plan_cnt_ptr[device] = cnt;
   g_short_cnt_ptr[device] = scnt;
   return BN_OK;
 }
@@ -1414,16 +1544,11 @@ void *decode_scratch(int device) {
   std::lock_guard<std::mutex> lk(g_scratch_mu);
   return g_scratch_ptr[device];
 }
-// the next counter slot of the planned decode on `device` (null: not set up)
-uint32_t *plan_counter_slot(int device) {
-  if (device < 0 || device >= kMaxScratchDevices) return nullptr;
-  void *base;
-  {
-    std::lock_guard<std::mutex> lk(g_scratch_mu);
-    base = g_plan_cnt_ptr[device];
-  }
-  if (!base) return nullptr;
-  return (uint32_t *)base + (g_plan_next.fetch_add(1) % kPlanSlots) * kPlanUnits;
+// the next planned-decode launch epoch (never 0)
+uint32_t next_plan_epoch() {
+  uint32_t e = g_plan_epoch.fetch_add(1) + 1;
+  if (e == 0) e = g_plan_epoch.fetch_add(1) + 1;
+  return e;
 }
 // the next counter slot of the short-cache decode on `device` (null: not set up)
 constexpr int kShortSlots = 16;
@@ -1680,16 +1805,24 @@ size_t bn_gqa_decode_planned_workspace_size(int batch, int max_len, int n_heads,
       head_dim != HD)
     return 0;
   // the unplanned fallback's partials, or the plan's part records (at most
-  // one per unit plus one per workgroup boundary)
-  const size_t recs = ((size_t)batch * n_kv_heads + kPlanBins) * (n_heads / n_kv_heads) * (HD + 2) *
-                      sizeof(float);
+  // one per unit plus one per workgroup boundary; each holds every wave's
+  // state as epoch-tagged 64-bit words)
+  const size_t recs = ((size_t)batch * n_kv_heads + kPlanBins) *
+                      ((size_t)(n_heads / n_kv_heads) * HD + 2 * (n_heads / n_kv_heads)) * sizeof(uint64_t);
   return std::max(bn_gqa_decode_workspace_size(batch, max_len, n_heads, head_dim), recs);
 }
 
-int bn_gqa_decode_planned(int dtype, const void *q, const void *k_cache, const void *v_cache,
-                          const int32_t *seq_lens, const int32_t *h_seq_lens, void *o, int batch,
-                          int max_len, int n_heads, int n_kv_heads, int head_dim, float scale,
-                          void *workspace, size_t workspace_bytes, void *stream) {
+}  // extern "C"
+
+namespace bn {
+namespace {
+// bn_gqa_decode_planned and bn_gqa_decode_planned_strided (strides: null for
+// a contiguous [batch, max_len, n_kv_heads, 64] cache)
+int gqa_decode_planned_impl(int dtype, const void *q, const void *k_cache, const void *v_cache,
+                            const int32_t *seq_lens, const int32_t *h_seq_lens, void *o, int batch,
+                            int max_len, int n_heads, int n_kv_heads, int head_dim, float scale,
+                            void *workspace, size_t workspace_bytes, void *stream,
+                            const int64_t *strides) {
   const char *op = "GQA decode (planned)";
   if (batch > 0 && !h_seq_lens)
     return fail(BN_ERR_INVALID_ARG, std::string(op) + ": NULL host lengths");
@@ -1708,6 +1841,9 @@ int bn_gqa_decode_planned(int dtype, const void *q, const void *k_cache, const v
                  n_heads % n_kv_heads == 0 && (G == 1 || G == 2 || G == 4 || G == 8) &&
                  (scale > 0.f) && std::isfinite(scale) && q && k_cache && v_cache && seq_lens && o &&
                  !(((uintptr_t)q | (uintptr_t)k_cache | (uintptr_t)v_cache) & 15u);
+  if (strides)
+    for (int i = 0; i < 3; ++i)
+      planned = planned && strides[i] > 0 && strides[i] % 8 == 0 && strides[i] <= ((int64_t)1 << 40);
   int st;
   PlanParams pl;
   int bins = 0, records = 0;
@@ -1719,27 +1855,29 @@ int bn_gqa_decode_planned(int dtype, const void *q, const void *k_cache, const v
   }
   if (!planned)
     return gqa_decode_impl(dtype, q, k_cache, v_cache, seq_lens, o, batch, max_len, n_heads, n_kv_heads,
-                           head_dim, scale, workspace, workspace_bytes, false, stream);
+                           head_dim, scale, workspace, workspace_bytes, false, stream, strides);
   pl.q = q; pl.k = k_cache; pl.v = v_cache; pl.o = o;
   pl.batch = batch; pl.max_len = max_len; pl.n_heads = n_heads; pl.n_kv_heads = n_kv_heads;
-  pl.kv_rs = (int64_t)n_kv_heads * HD;  // contiguous [batch, max_len, n_kv_heads, 64]
-  pl.kv_hs = HD;
-  pl.kv_bs = (int64_t)max_len * pl.kv_rs;
+  pl.kv_bs = strides ? strides[0] : (int64_t)max_len * n_kv_heads * HD;
+  pl.kv_hs = strides ? strides[1] : HD;
+  pl.kv_rs = strides ? strides[2] : (int64_t)n_kv_heads * HD;
   pl.c = scale * 1.4426950408889634f;
-  pl.cnt = plan_counter_slot(library_device());
-  if (!pl.cnt)
-    return fail(BN_ERR_HIP, std::string(op) + ": plan counters not set up for device " +
-                                std::to_string(library_device()));
+  pl.epoch = next_plan_epoch();
+  // BN_PLAN_FALLBACK=1 (tests): the heads ignore the records and stream the
+  // later parts' keys themselves -- the path a head takes if a record never
+  // arrives
+  const char *fb = std::getenv("BN_PLAN_FALLBACK");
+  pl.max_polls = (fb && fb[0] == '1') ? -1 : kPlanPolls;
   hipStream_t s = as_stream(stream);
   void *ws = workspace;
   bool own = false;
-  const size_t need = (size_t)std::max(records, 1) * G * (HD + 2) * sizeof(float);
+  const size_t need = (size_t)std::max(records, 1) * ((size_t)G * HD + 2 * G) * sizeof(uint64_t);
   if (!ws && records > 0) {
     if ((st = bn_alloc(&ws, need, stream))) return st;
     own = true;
   }
-  pl.rec = (float *)ws;
-  const dim3 grid((unsigned)bins), block(64 * WWV);
+  pl.rec = (uint64_t *)ws;
+  const dim3 grid((unsigned)bins), block(kPlanThreads);
   switch (G) {
     case 1: hipLaunchKernelGGL(decode_bf16_planned_kernel<1>, grid, block, 0, s, pl); break;
     case 2: hipLaunchKernelGGL(decode_bf16_planned_kernel<2>, grid, block, 0, s, pl); break;
@@ -1756,6 +1894,32 @@ int bn_gqa_decode_planned(int dtype, const void *q, const void *k_cache, const v
     if (st == BN_OK) st = st2;
   }
   return st;
+}
+}  // namespace
+}  // namespace bn
+
+extern "C" {
+
+int bn_gqa_decode_planned(int dtype, const void *q, const void *k_cache, const void *v_cache,
+                          const int32_t *seq_lens, const int32_t *h_seq_lens, void *o, int batch,
+                          int max_len, int n_heads, int n_kv_heads, int head_dim, float scale,
+                          void *workspace, size_t workspace_bytes, void *stream) {
+  return gqa_decode_planned_impl(dtype, q, k_cache, v_cache, seq_lens, h_seq_lens, o, batch, max_len,
+                                 n_heads, n_kv_heads, head_dim, scale, workspace, workspace_bytes,
+                                 stream, nullptr);
+}
+
+int bn_gqa_decode_planned_strided(int dtype, const void *q, const void *k_cache,
+                                  const void *v_cache, const int32_t *seq_lens,
+                                  const int32_t *h_seq_lens, void *o, int batch, int max_len,
+                                  int n_heads, int n_kv_heads, int head_dim,
+                                  int64_t cache_seq_stride, int64_t cache_head_stride,
+                                  int64_t cache_row_stride, float scale, void *workspace,
+                                  size_t workspace_bytes, void *stream) {
+  const int64_t strides[3] = {cache_seq_stride, cache_head_stride, cache_row_stride};
+  return gqa_decode_planned_impl(dtype, q, k_cache, v_cache, seq_lens, h_seq_lens, o, batch, max_len,
+                                 n_heads, n_kv_heads, head_dim, scale, workspace, workspace_bytes,
+                                 stream, strides);
 }
 
 }  // extern "C"

@@ -335,19 +335,22 @@ def bench_decode(kind, steps, warmup, seed=2, planned=False, layout="token_major
     return {"value": round(gbs, 2), "unit": "GB/s", "ms_per_launch": round(ms, 5),
             "bytes_per_launch": nb, "lengths": f"{desc}, sum {int(lens.sum())}",
             "cache_layout": "[B, L, Hkv, 64]" if layout == "token_major" else "[B, Hkv, L, 64]",
-            "entry_point": ("bn_gqa_decode_planned" if planned else
+            "entry_point": (("bn_gqa_decode_planned" if layout == "token_major"
+                             else "bn_gqa_decode_planned_strided") if planned else
                             "bn_gqa_decode" if layout == "token_major" else "bn_gqa_decode_strided"),
             "roofline": roofline("hbm", gbs, PEAK_HBM_GBS, "GB/s",
-                                 measured_traffic("decode_planned_" + kind) if planned
-                                 else measured_traffic(key))}
+                                 measured_traffic("decode_planned_" + kind +
+                                                  ("_head_major" if layout == "head_major" else ""))
+                                 if planned else measured_traffic(key))}
 
 
 def bench_decode_planned(steps, warmup):
-    """The planned decode beside bn_gqa_decode on three ragged patterns."""
+    """The planned decode beside the whole-cache kernel on three ragged
+    patterns, both on head-major caches (the config-3 lines' layout)."""
     out = {}
     for kind in ("ragged", "two_class", "skewed"):
-        pl = bench_decode(kind, steps, warmup, planned=True)
-        plain = bench_decode(kind, steps, warmup) if kind != "ragged" else None
+        pl = bench_decode(kind, steps, warmup, planned=True, layout="head_major")
+        plain = bench_decode(kind, steps, warmup, layout="head_major") if kind != "ragged" else None
         out[kind] = {"planned": pl}
         if plain is not None:
             out[kind]["bn_gqa_decode"] = plain

@@ -383,9 +383,9 @@ int bn_gqa_decode_strided(int dtype, const void *q, const void *k_cache,
  * at least as many (sequence, KV head) units as compute units (at most 256)
  * and a longest cache above 1.25x the mean.  Every other call (a balanced
  * batch included) runs bn_gqa_decode on seq_lens.  workspace: device memory of
- * bn_gqa_decode_planned_workspace_size() bytes, or NULL (the pool).  Two
- * planned calls in flight at once on one GPU share part counters only when
- * 16 planned launches are in flight together. */
+ * bn_gqa_decode_planned_workspace_size() bytes, or NULL (the pool); calls in
+ * flight at once need workspaces of their own (each launch tags the records
+ * it writes there with its own epoch; nothing else is shared). */
 size_t bn_gqa_decode_planned_workspace_size(int batch, int max_len, int n_heads,
                                             int n_kv_heads, int head_dim);
 int bn_gqa_decode_planned(int dtype, const void *q, const void *k_cache,
@@ -394,6 +394,20 @@ int bn_gqa_decode_planned(int dtype, const void *q, const void *k_cache,
                           int max_len, int n_heads, int n_kv_heads, int head_dim,
                           float scale, void *workspace, size_t workspace_bytes,
                           void *stream);
+
+/* bn_gqa_decode_planned over caches of any layout whose key rows are contiguous
+ * (strides as for bn_gqa_decode_strided; the unplanned fallback is
+ * bn_gqa_decode_strided).  Same reference row; the plan and kernel are the
+ * planned call's. */
+int bn_gqa_decode_planned_strided(int dtype, const void *q, const void *k_cache,
+                                  const void *v_cache, const int32_t *seq_lens,
+                                  const int32_t *h_seq_lens, void *o, int batch,
+                                  int max_len, int n_heads, int n_kv_heads,
+                                  int head_dim, int64_t cache_seq_stride,
+                                  int64_t cache_head_stride,
+                                  int64_t cache_row_stride, float scale,
+                                  void *workspace, size_t workspace_bytes,
+                                  void *stream);
 
 /* No counterpart in the reference.  For callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, harnesses that

@@ -197,13 +197,24 @@ def test_decode_planned_validation(kw, status, stem):
     assert m.startswith(stem), m
 
 
+def test_decode_planned_strided_validation():
+    # bad strides leave the plan and fail in bn_gqa_decode_strided's checks (fake pointers)
+    args = (B.BN_BF16, 0x1000, 0x2000, 0x3000, 0x5000, 0x6000, 0x4000, 64, 4096, 32, 4, 64,
+            4 * 4096 * 64, 4096 * 64, 60, 0.125, None, 0, None)
+    s, m = st("bn_gqa_decode_planned_strided", *args)
+    assert s == B.BN_ERR_INVALID_ARG and m.startswith("GQA decode (strided): cache strides"), m
+    s, m = st("bn_gqa_decode_planned_strided", *args[:5], 0, *args[6:])
+    assert s == B.BN_ERR_INVALID_ARG and m == "GQA decode (planned): NULL host lengths", m
+
+
 def test_decode_planned_workspace_size():
     L = B.lib()
-    # the fallback's partials (config 3) exceed the plan's records
+    # config 3: the unplanned fallback's partials exceed the plan's records
     assert L.bn_gqa_decode_planned_workspace_size(64, 4096, 32, 4, 64) == \
         L.bn_gqa_decode_workspace_size(64, 4096, 32, 64)
-    # short caches: the records ((64*4 + 256) parts of 8 heads x 66 floats) are larger
-    assert L.bn_gqa_decode_planned_workspace_size(64, 128, 32, 4, 64) == (64 * 4 + 256) * 8 * 66 * 4
+    # short caches: the records are larger -- (64*4 + 256) parts, each 8 heads x 64
+    # acc words plus 8 m and 8 l words, 8-byte epoch-tagged
+    assert L.bn_gqa_decode_planned_workspace_size(64, 128, 32, 4, 64) == (64 * 4 + 256) * (8 * 64 + 16) * 8
     assert L.bn_gqa_decode_planned_workspace_size(64, 128, 32, 4, 32) == 0
     assert L.bn_gqa_decode_planned_workspace_size(64, 128, 30, 4, 64) == 0
 
@@ -454,9 +465,9 @@ def test_fused_head_attention_validation(kw, status, msg):
 
 
 def test_decode_wrappers_refuse_layouts_they_cannot_pass():
-    """bnhip.gqa_decode passes any cache whose key rows are contiguous (through
-    bn_gqa_decode_strided) and refuses the rest on the host; the planned call
-    takes contiguous caches only (CPU tensors: nothing reaches a device)."""
+    """bnhip.gqa_decode and gqa_decode_planned pass any cache whose key rows
+    are contiguous (through the strided entry points) and refuse the rest on
+    the host (CPU tensors: nothing reaches a device)."""
     import torch
     q = torch.zeros((2, 8, 64))
     kc = torch.zeros((2, 16, 2, 64))
@@ -469,5 +480,8 @@ def test_decode_wrappers_refuse_layouts_they_cannot_pass():
         B.gqa_decode(q, cols, cols, lens)
     with pytest.raises(ValueError, match="q and o must be contiguous"):
         B.gqa_decode(torch.zeros((8, 2, 64)).transpose(0, 1), kc, kc, lens)
-    with pytest.raises(ValueError, match="must be contiguous"):
-        B.gqa_decode_planned(q, hm, hm, lens, [16, 16])
+    with pytest.raises(ValueError, match="same shape and strides"):
+        B.gqa_decode_planned(q, kc, hm, lens, [16, 16])
+    with pytest.raises(ValueError, match="stride 1 along head_dim"):
+        cols = torch.zeros((2, 16, 2, 128))[..., ::2]
+        B.gqa_decode_planned(q, cols, cols, lens, [16, 16])

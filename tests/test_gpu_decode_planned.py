@@ -1,7 +1,8 @@
 """GPU parity of the planned ragged decode (bn_gqa_decode_planned).
 
 The host lengths choose equal shares of the batch's tiles per compute unit;
-cut caches are merged in the same launch by their last part.  Every sequence
+a cut cache is merged in the same launch by its head part (its first tiles),
+from the records its later parts' waves wrote with this launch's epoch.  Every sequence
 of every case is compared with the CPU oracle at the bf16 bound (2e-2), and
 the planned call with bn_gqa_decode (which it must agree with to the same
 bound: both are the same softmax row).  Length sets: config 3's ragged draw
@@ -9,6 +10,8 @@ bound: both are the same softmax row).  Length sets: config 3's ragged draw
 sequences of length 0 and 1, other query-group sizes, and batches the plan
 does not take (balanced, or more than 256 units) which run bn_gqa_decode.
 """
+import os
+
 import numpy as np
 import pytest
 import torch
@@ -46,6 +49,12 @@ def lengths(kind, Bn, L, seed=2):
     raise ValueError(kind)
 
 
+def head_major(c):
+    """The same values as the contiguous cache c [B, L, Hkv, 64], stored
+    [B, Hkv, L, 64], as a [B, L, Hkv, 64] view."""
+    return c.transpose(1, 2).contiguous().transpose(1, 2)
+
+
 def run_case(Bn, L, H, Hkv, lens, seed=9, workspace=True):
     r = np.random.default_rng(seed)
     q = bf16_round(r.standard_normal((Bn, H, 64)).astype(np.float32))
@@ -61,7 +70,7 @@ def run_case(Bn, L, H, Hkv, lens, seed=9, workspace=True):
     B.gqa_decode_planned(qd, kd, vd, ld, lens, o1, scale=0.125, workspace=ws)
     o2 = B.gqa_decode_planned(qd, kd, vd, ld, lens, scale=0.125, workspace=ws)
     torch.cuda.synchronize()
-    assert torch.equal(o1, o2), "a second call gives other bits (counters not back at zero?)"
+    assert torch.equal(o1, o2), "a second call on the same workspace gives other bits"
     got = host(o1)
     for b in range(Bn):
         Lb = int(lens[b])
@@ -99,3 +108,39 @@ def test_planned_decode_unplanned_batches(kind, Bn):
     # balanced lengths, or 384 units: bn_gqa_decode runs, same results
     L = 1024
     run_case(Bn, L, 32, 4, lengths(kind, Bn, L), seed=13)
+
+
+def test_planned_decode_head_major_caches():
+    """bn_gqa_decode_planned_strided on head-major caches: the same kernel and
+    plan, only the row addresses change -- bit for bit the contiguous call."""
+    Bn, L, H, Hkv = 64, 4096, 32, 4
+    lens = lengths("ragged", Bn, L)
+    g = torch.Generator(device="cuda").manual_seed(21)
+    q = torch.randn((Bn, H, 64), generator=g, device="cuda").bfloat16()
+    kc = torch.randn((Bn, L, Hkv, 64), generator=g, device="cuda").bfloat16()
+    vc = torch.randn((Bn, L, Hkv, 64), generator=g, device="cuda").bfloat16()
+    ld = torch.from_numpy(lens).cuda()
+    ws = torch.empty(B.lib().bn_gqa_decode_planned_workspace_size(Bn, L, H, Hkv, 64),
+                     dtype=torch.uint8, device="cuda")
+    want = B.gqa_decode_planned(q, kc, vc, ld, lens, scale=0.125, workspace=ws)
+    ks, vs = head_major(kc), head_major(vc)
+    assert not ks.is_contiguous()
+    for _ in range(2):
+        got = B.gqa_decode_planned(q, ks, vs, ld, lens, scale=0.125, workspace=ws)
+        assert torch.equal(got, want)
+    ref = host(B.gqa_decode(q, ks, vs, ld, scale=0.125))  # the whole-cache kernel, same layout
+    assert_close(host(want), ref, BF16_TOL, "planned vs bn_gqa_decode_strided")
+
+
+@pytest.mark.parametrize("kind", ["ragged", "skewed", "zeros"])
+def test_planned_decode_fallback_path(kind):
+    """BN_PLAN_FALLBACK=1 makes every head ignore the records and stream its
+    cut cache's later keys itself -- what a head does if a record never
+    arrives.  Forced from the host, so no kernel waits on anything; the results
+    must hold the same bounds, and repeat bit for bit."""
+    Bn, L, H, Hkv = 64, 4096, 32, 4
+    os.environ["BN_PLAN_FALLBACK"] = "1"
+    try:
+        run_case(Bn, L, H, Hkv, lengths(kind, Bn, L), seed=17)
+    finally:
+        del os.environ["BN_PLAN_FALLBACK"]
