@@ -729,37 +729,59 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void d
 // the next tile register-staged; the scores and P V on
 // v_mfma_f32_16x16x32_bf16 as in the whole-row kernel.  The waves'
 // (m, l, acc) are merged through LDS at the end and the workgroup writes the
-// G output rows.
-constexpr int WWV = 4;  // waves per workgroup (8 measured 8% slower on config 3, 2 3% slower)
+// G output rows.  Four waves stream a cache (8 measured 8% slower on config
+// 3, 2 3% slower).  When a KV head's rows are contiguous (row stride
+// head_dim: a head-major cache) the workgroup has WWX waves and a cache more
+// than 1.25x the batch's mean length uses all of them (once the other caches
+// are done, one CU streams a long cache faster with more waves: config 3's
+// ragged draw -4%, a few long caches among short ones -12%; uniform lengths
+// keep four); token-major caches stream slower with more waves and keep four.
+constexpr int WWV = 4;  // streaming waves per workgroup
+constexpr int WWX = 6;  // waves of an adaptive whole-cache workgroup, active for a long cache
+constexpr int kMeanBatchMax = 512;  // longer batches: four waves for every cache
 constexpr int WKP = HD + 8;  // tile row pitch, 144 B: b128 K reads of 16 rows and tr16 V
                              // reads of 4 rows x 32 B hit distinct banks
 
-template <int G>
-__global__ __launch_bounds__(64 * WWV) void decode_bf16_whole_kernel(DecodeParams p) {
-  __shared__ __attribute__((aligned(16))) bf16_t KT[WWV][TK * WKP];
-  __shared__ __attribute__((aligned(16))) bf16_t VT[WWV][TK * WKP];
-  __shared__ float red_m[WWV][G], red_l[WWV][G];
-  __shared__ float red_o[WWV][G][HD];
+// NW waves per workgroup: WWV, or WWX with the long-cache adaptation
+template <int G, int NW>
+__global__ __launch_bounds__(64 * NW) void decode_bf16_whole_kernel(DecodeParams p) {
+  __shared__ __attribute__((aligned(16))) bf16_t KT[NW][TK * WKP];
+  __shared__ __attribute__((aligned(16))) bf16_t VT[NW][TK * WKP];
+  __shared__ float red_m[NW][G], red_l[NW][G];
+  __shared__ float red_o[NW][G][HD];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l16 = lane & 15, grp = lane >> 4;
   const int b = blockIdx.x / p.n_kv_heads, g = blockIdx.x % p.n_kv_heads;
+  auto clamp_len = [&](int x) { return x < 0 ? 0 : (x > p.max_len ? p.max_len : x); };
 
-  int len = p.lens[b];
-  len = len < 0 ? 0 : (len > p.max_len ? p.max_len : len);
+  // the batch's total length (batches up to kMeanBatchMax sequences), summed
+  // by every wave itself (no barrier), read with this sequence's length
+  const bool adapt = NW > WWV && p.batch <= kMeanBatchMax;
+  int part = 0;
+  if (adapt)
+    for (int i = lane; i < p.batch; i += 64) part += clamp_len(p.lens[i]);
+  const int len = clamp_len(p.lens[b]);
   bf16_t *out = (bf16_t *)p.o + ((int64_t)b * p.n_heads + (int64_t)g * G) * HD;
   if (len == 0) {  // no key: zeros
-    for (int idx = tid; idx < G * HD; idx += 64 * WWV) out[idx] = f32_to_bf16(0.f);
+    for (int idx = tid; idx < G * HD; idx += 64 * NW) out[idx] = f32_to_bf16(0.f);
     return;
   }
-  // wave w takes the 32-key tiles w, w + WWV, w + 2*WWV, ...: the waves of a
-  // workgroup stream adjacent tiles (a contiguous key range per wave, or the
+  int nw = WWV;  // streaming waves of this workgroup (uniform)
+  if (adapt) {
+#pragma unroll
+    for (int o2 = 32; o2 > 0; o2 >>= 1) part += __shfl_xor(part, o2, 64);
+    const int total = __builtin_amdgcn_readfirstlane(part);  // <= 512 * max_len
+    if ((int64_t)len * p.batch * 4 > (int64_t)total * 5) nw = NW;
+  }
+  // wave w < nw takes the 32-key tiles w, w + nw, w + 2*nw, ...: the waves of
+  // a workgroup stream adjacent tiles (a contiguous key range per wave, or the
   // KV heads of one sequence placed on one XCD, measured 3-4% slower)
   const int all_tiles = (len + TK - 1) / TK;
   const int kw0 = TK * wave, kw1 = len;
-  const int tstride = TK * WWV;  // keys between a wave's tiles
-  const int ntiles = all_tiles > wave ? (all_tiles - wave + WWV - 1) / WWV : 0;
+  const int tstride = TK * nw;  // keys between a wave's tiles
+  const int ntiles = wave < nw && all_tiles > wave ? (all_tiles - wave + nw - 1) / nw : 0;
 
   const int64_t kv_rs = p.kv_rs;
   const bf16_t *Kr = (const bf16_t *)p.k + b * p.kv_bs + g * p.kv_hs;
@@ -899,14 +921,14 @@ __global__ __launch_bounds__(64 * WWV) void decode_bf16_whole_kernel(DecodeParam
     }
   }
   __syncthreads();
-  for (int idx = tid; idx < G * HD; idx += 64 * WWV) {
+  for (int idx = tid; idx < G * HD; idx += 64 * NW) {
     const int h = idx / HD, d = idx - h * HD;
     float M = red_m[0][h];
 #pragma unroll
-    for (int w = 1; w < WWV; ++w) M = fmaxf(M, red_m[w][h]);  // finite: wave 0 has keys
+    for (int w = 1; w < NW; ++w) M = fmaxf(M, red_m[w][h]);  // finite: wave 0 has keys
     float L = 0.f, A = 0.f;
 #pragma unroll
-    for (int w = 0; w < WWV; ++w) {
+    for (int w = 0; w < NW; ++w) {
       const float wt = __builtin_amdgcn_exp2f(red_m[w][h] - M);
       L += red_l[w][h] * wt;
       A += red_o[w][h][d] * wt;
@@ -1646,13 +1668,23 @@ int gqa_decode_impl(int dtype, const void *q, const void *k_cache, const void *v
       p.chunk = max_len;
       p.c = scale * 1.4426950408889634f;
       hipStream_t s = as_stream(stream);
-      const dim3 grid((unsigned)((int64_t)batch * n_kv_heads)), block(64 * WWV);
+      // a KV head's rows contiguous: long caches may take more waves
+      const bool wide = p.kv_rs == HD && batch <= kMeanBatchMax;
+      const dim3 grid((unsigned)((int64_t)batch * n_kv_heads)), block(64 * (wide ? WWX : WWV));
+#define BN_WHOLE(GG)                                                                        \
+  do {                                                                                      \
+    if (wide)                                                                               \
+      hipLaunchKernelGGL((decode_bf16_whole_kernel<GG, WWX>), grid, block, 0, s, p);        \
+    else                                                                                    \
+      hipLaunchKernelGGL((decode_bf16_whole_kernel<GG, WWV>), grid, block, 0, s, p);        \
+  } while (0)
       switch (G) {
-        case 1: hipLaunchKernelGGL(decode_bf16_whole_kernel<1>, grid, block, 0, s, p); break;
-        case 2: hipLaunchKernelGGL(decode_bf16_whole_kernel<2>, grid, block, 0, s, p); break;
-        case 4: hipLaunchKernelGGL(decode_bf16_whole_kernel<4>, grid, block, 0, s, p); break;
-        default: hipLaunchKernelGGL(decode_bf16_whole_kernel<8>, grid, block, 0, s, p); break;
+        case 1: BN_WHOLE(1); break;
+        case 2: BN_WHOLE(2); break;
+        case 4: BN_WHOLE(4); break;
+        default: BN_WHOLE(8); break;
       }
+#undef BN_WHOLE
       BN_LAUNCH_CHECK();
       return BN_OK;
     }

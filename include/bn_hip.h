@@ -363,7 +363,12 @@ int bn_gqa_decode(int dtype, const void *q, const void *k_cache,
  * head_dim] cache (n_kv_heads*max_len*head_dim, max_len*head_dim, head_dim)
  * keeps each (sequence, KV head)'s rows contiguous in HBM and streams faster
  * on bf16 caches of at least one (sequence, KV head) per compute unit.  Same
- * kernels, workspace and results as bn_gqa_decode on the same values. */
+ * kernels, workspace and results as bn_gqa_decode on the same values, except
+ * that when a KV head's rows are contiguous (cache_row_stride == head_dim),
+ * bf16 caches of at least one (sequence, KV head) per compute unit in batches
+ * of at most 512 stream a cache longer than 1.25x the batch's mean length
+ * with six waves instead of four: the same row to the bf16 tolerance, summed
+ * in another order. */
 int bn_gqa_decode_strided(int dtype, const void *q, const void *k_cache,
                           const void *v_cache, const int32_t *seq_lens, void *o,
                           int batch, int max_len, int n_heads, int n_kv_heads,

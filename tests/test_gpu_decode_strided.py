@@ -3,7 +3,11 @@ contiguous [batch, max_len, n_kv_heads, 64].
 
 The kernels run the same arithmetic in the same order whatever the strides,
 so each strided call must equal the contiguous call on the same values bit
-for bit; a few sequences per case are also checked against the CPU oracle
+for bit -- except on the one-workgroup-per-(sequence, KV head) bf16 path when
+a KV head's rows are contiguous (head-major): there a cache longer than 1.25x
+the batch's mean streams with six waves instead of four, the same row in
+another summation order, held to the bf16 bound against the contiguous call.
+A few sequences per case are also checked against the CPU oracle
 Cases cover every decode path: the one-workgroup-
 per-(sequence, KV head) bf16 kernel (config 3's shape, uniform and ragged),
 the split-K bf16 kernels (whole-row and per-head), the fp32 split kernel and
@@ -85,7 +89,12 @@ def test_strided_equals_contiguous_and_oracle(case, layout):
     want = B.gqa_decode(q, kc, vc, ld, scale=0.125, workspace=ws)
     got = B.gqa_decode(q, ks, vs, ld, scale=0.125, workspace=ws)
     torch.cuda.synchronize()
-    assert torch.equal(got, want), f"{layout}: differs from the contiguous call"
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    wide = dtype == "bf16" and Bn * Hkv >= cus and ks.stride(1) == 64  # rows of a head contiguous
+    if wide and kind == "ragged":
+        assert_close(host(got), host(want), TOL[dtype], f"{layout}: against the contiguous call")
+    else:
+        assert torch.equal(got, want), f"{layout}: differs from the contiguous call"
     gh = host(got)
     assert np.all(np.isfinite(gh))
     for b in sorted({0, 1, 2, 3, Bn - 1} & set(range(Bn))):

@@ -177,8 +177,13 @@ def test_decode_sweep(target, i):
     # the same caches in a random other layout (bn_gqa_decode_strided): the same bits
     head_major, gap, pad = bool(rng.integers(2)), int(rng.choice([0, 1, 5])), int(rng.choice([0, 8, 32]))
     ks, vs = (strided_cache(c, head_major, gap, pad) for c in (kd, vd))
-    assert torch.equal(B.gqa_decode(qd, ks, vs, ld, scale=SCALE), out), \
-        f"{what}: strided (head_major={head_major}, gap={gap}, pad={pad}) differs"
+    got_s = B.gqa_decode(qd, ks, vs, ld, scale=SCALE)
+    what_s = f"{what}: strided (head_major={head_major}, gap={gap}, pad={pad})"
+    if target == "bf16_whole" and head_major and pad == 0:
+        # a head's rows contiguous: long caches may stream with six waves
+        assert_close(host(got_s), got, TOL[dtype], what_s)
+    else:
+        assert torch.equal(got_s, out), f"{what_s} differs"
 
 
 def strided_cache(c, head_major, gap, pad):
