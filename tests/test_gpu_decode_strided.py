@@ -4,7 +4,8 @@ contiguous [batch, max_len, n_kv_heads, 64].
 The kernels run the same arithmetic in the same order whatever the strides,
 so each strided call must equal the contiguous call on the same values bit
 for bit -- except on the one-workgroup-per-(sequence, KV head) bf16 path when
-a KV head's rows are contiguous (head-major): there a cache longer than 1.25x
+a KV head's rows are contiguous (head-major) and the batch holds at most 512
+sequences: there a cache longer than 1.25x
 the batch's mean streams with six waves instead of four, the same row in
 another summation order, held to the bf16 bound against the contiguous call.
 A few sequences per case are also checked against the CPU oracle
@@ -64,6 +65,8 @@ CASES = [
     ("bf16", 64, 4096, 32, 4, "uniform"),  # config 3: one workgroup per (sequence, KV head)
     ("bf16", 64, 4096, 32, 4, "ragged"),
     ("bf16", 80, 300, 16, 4, "ragged"),    # the same kernel, G = 4, short caches
+    ("bf16", 512, 96, 16, 2, "ragged"),    # the same kernel, the largest batch that sums its lengths
+    ("bf16", 520, 96, 16, 2, "ragged"),    # past it: four waves for every cache, any layout
     ("bf16", 2, 4096, 32, 4, "ragged"),    # split-K, whole-row kernel (4 KV heads per workgroup)
     ("bf16", 3, 1000, 16, 2, "ragged"),    # split-K, per-head kernel (n_kv_heads not a multiple of 4)
     ("f32", 2, 2048, 32, 4, "ragged"),     # fp32 split-K
@@ -90,7 +93,8 @@ def test_strided_equals_contiguous_and_oracle(case, layout):
     got = B.gqa_decode(q, ks, vs, ld, scale=0.125, workspace=ws)
     torch.cuda.synchronize()
     cus = torch.cuda.get_device_properties(0).multi_processor_count
-    wide = dtype == "bf16" and Bn * Hkv >= cus and ks.stride(1) == 64  # rows of a head contiguous
+    # rows of a head contiguous, batch of at most 512 sequences: the adaptive kernel
+    wide = dtype == "bf16" and Bn * Hkv >= cus and ks.stride(1) == 64 and Bn <= 512
     if wide and kind == "ragged":
         assert_close(host(got), host(want), TOL[dtype], f"{layout}: against the contiguous call")
     else:
