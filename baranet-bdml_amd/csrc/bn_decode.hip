@@ -1085,7 +1085,8 @@ __global__ __launch_bounds__(kPlanThreads) void decode_bf16_planned_kernel(PlanP
                                             ((int64_t)b * p.n_heads + g * G + l16) * HD + 8 * grp + 32 * t)
                       : dbf16x8_t{};
   };
-  bf16_t *const kt = KT[wave], *const vt = VT[wave];
+  // the writer wave (wave WWV) has no tile of its own and never uses these
+  bf16_t *const kt = KT[streamer ? wave : 0], *const vt = VT[streamer ? wave : 0];
   auto lstore = [&](const RegTile &r) __attribute__((always_inline)) {
     *(u32x4 *)(kt + crow * WKP + ccol) = r.k0;
     *(u32x4 *)(kt + (crow + 8) * WKP + ccol) = r.k1;
